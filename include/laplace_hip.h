@@ -1,0 +1,126 @@
+/*
+ * laplace_hip.h - C ABI of the MI355X (gfx950) GGUF quantized-matmul back-end.
+ *
+ * The functions below are what the Laplace C++ engine binds to replace its
+ * CPU matmul back-end. Plain pointers and sizes only; no HIP or torch types.
+ * `type` is a GGMLType value (reference src/tensor.h:11-34): Q4_0 = 2,
+ * Q8_0 = 8, Q4_K = 12, Q6_K = 14 are handled; every other type makes the
+ * call return "not handled" so the caller falls back to its CPU path.
+ *
+ * Two families:
+ *   1. Host-pointer, synchronous entry points with the exact signatures of
+ *      the reference's back-end function-pointer types (src/kernels.h:94-119):
+ *      x, w, y live in host memory; y is complete when the call returns;
+ *      false means "type or shape not handled here, fall back". Weights are
+ *      served from device copies made by lp_register_weights (or a copy
+ *      cached by host pointer on first use, as the reference's Metal back-end
+ *      does, src/metal.mm:601-621).
+ *   2. Device-pointer, stream-ordered entry points (suffix _dev) for callers
+ *      that keep x, w, y in HBM. They never allocate: scratch for quantized
+ *      activations is a caller-provided workspace sized by
+ *      lp_act_workspace_bytes. They return an lp_status code.
+ *
+ * Numerics follow the reference's int8-activation path
+ * (src/matmul_simd.cpp): activations are quantized to 32-element int8
+ * blocks exactly as quantize_act_q8_neon does (:348-410, bit-exact), the
+ * per-block int32 dot sums equal the NEON kernels' (:143-342, bit-exact),
+ * and fp32 outputs agree with the reference within 1e-4 normwise relative
+ * error (fp32 accumulation order differs).
+ */
+#ifndef LAPLACE_HIP_H
+#define LAPLACE_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    LP_OK = 0,
+    LP_UNSUPPORTED = 1,  /* type/shape/alignment not handled: caller falls back */
+    LP_EINVAL = 2,       /* bad argument (null pointer, short workspace, ...) */
+    LP_EHIP = 3,         /* a HIP runtime call failed; see lp_last_error() */
+    LP_ENODEV = 4        /* no usable gfx950 device */
+} lp_status;
+
+/* ---- 1. drop-in back-end ABI (host pointers, synchronous) ---------------- */
+
+/* y[M,N] = X[M,K] @ W^T, W = N contiguous rows of K elements of `type`.
+ * Replaces gemm_fn (src/kernels.h:97-98) / gemm_simd (src/matmul_simd.cpp:480-496). */
+bool lp_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N);
+
+/* y[k*N + j] = dot(x, W_{expert_idx[k]} row j), one shared activation row.
+ * Replaces moe_gemv_fn (src/kernels.h:100-105) / moe_gemv_simd (src/matmul_simd.cpp:580-596). */
+bool lp_moe_gemv(const float* x, const uint8_t* w, uint32_t type, const int* expert_idx,
+                 int n_experts, float* y, int K, int N);
+
+/* y[k*N + j] = dot(x + k*K, W_{expert_idx[k]} row j).
+ * Replaces moe_gemv_multi_fn (src/kernels.h:107-112) / moe_gemv_multi_simd (:598-614). */
+bool lp_moe_gemv_multi(const float* x, const uint8_t* w, uint32_t type, const int* expert_idx,
+                       int n_experts, float* y, int K, int N);
+
+typedef bool (*lp_gemm_fn)(const float*, const uint8_t*, uint32_t, float*, int, int, int);
+typedef bool (*lp_moe_gemv_fn)(const float*, const uint8_t*, uint32_t, const int*, int,
+                               float*, int, int);
+
+/* Getters in the style of get_simd_gemm (src/kernels.h:114-119): NULL when
+ * no gfx950 device is usable, so the caller keeps its scalar path. */
+lp_gemm_fn     lp_get_gemm(void);
+lp_moe_gemv_fn lp_get_moe_gemv(void);
+lp_moe_gemv_fn lp_get_moe_gemv_multi(void);
+
+/* Copies [base, base+size) of host memory (e.g. the mmap'd GGUF file) to the
+ * current device once; host weight pointers inside it then resolve to the
+ * device copy. Mirrors matmul_register_weights (src/matmul.h:47-48) and the
+ * Metal registration it forwards to (src/metal.mm:581-599). */
+int lp_register_weights(const void* base, size_t size);
+/* Drops every registered region and cached weight copy of the current device. */
+void lp_release_weights(void);
+
+/* Host-pointer quantizer, the ActQ8 fields as separate arrays (test hook):
+ * d, sum, sum_lo, sum_hi hold M*K/32 values, qs M*K codes. K % 32 == 0. */
+int lp_quantize_act(const float* x, int M, int K, float* d, float* sum, int16_t* sum_lo,
+                    int16_t* sum_hi, int8_t* qs);
+
+/* ---- 2. device-pointer, stream-ordered API ------------------------------- */
+
+/* Bytes of workspace holding M rows of quantized activations of length K. */
+size_t lp_act_workspace_bytes(int M, int K);
+
+/* Quantize x[M,K] (device) into the workspace (codes, scales, sums). */
+int lp_quantize_act_dev(const float* x, int M, int K, void* ws, size_t ws_bytes, void* stream);
+
+/* Read back the quantized activations held in a workspace into device
+ * arrays in the host-API layout (test hook). */
+int lp_act_unpack_dev(const void* ws, int M, int K, float* d, float* sum, int32_t* sums16,
+                      int8_t* qs, void* stream);
+
+/* y[M,N] = X[M,K] @ W^T on device pointers: quantize, then GEMV (M <= 8)
+ * or GEMM. x, w, y and ws are device pointers; `stream` is a hipStream_t
+ * (NULL = default stream). Asynchronous with respect to the host. */
+int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                void* ws, size_t ws_bytes, void* stream);
+
+/* Same product from activations already quantized into ws. */
+int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                  void* stream);
+
+/* Per-sub-block int32 dots through the GEMV decoders (test hook):
+ * out[(m*N + j)*S + s], S = K/32 (K/16 for Q6_K). */
+int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M,
+                      int K, int N, void* stream);
+
+/* ---- diagnostics ----------------------------------------------------------- */
+
+/* Text of the last error on this thread ("" if none). */
+const char* lp_last_error(void);
+/* 1 if the current device is usable (gfx950), 0 otherwise. */
+int lp_device_ok(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

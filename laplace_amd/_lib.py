@@ -1,0 +1,67 @@
+"""ctypes binding of ``liblaplace_hip.so`` (the C ABI of include/laplace_hip.h).
+
+Loading fails loudly: if the library has not been built there is no CPU
+fallback in this package, by design. Build it with
+``python -m laplace_amd.build``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblaplace_hip.so")
+
+LP_OK, LP_UNSUPPORTED, LP_EINVAL, LP_EHIP, LP_ENODEV = 0, 1, 2, 3, 4
+STATUS_NAMES = {0: "LP_OK", 1: "LP_UNSUPPORTED", 2: "LP_EINVAL", 3: "LP_EHIP", 4: "LP_ENODEV"}
+
+# Every symbol the header declares, with (restype, argtypes).
+_vp, _i, _u32, _sz, _b = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_bool
+SIGNATURES = {
+    "lp_gemm": (_b, [_vp, _vp, _u32, _vp, _i, _i, _i]),
+    "lp_moe_gemv": (_b, [_vp, _vp, _u32, _vp, _i, _vp, _i, _i]),
+    "lp_moe_gemv_multi": (_b, [_vp, _vp, _u32, _vp, _i, _vp, _i, _i]),
+    "lp_get_gemm": (_vp, []),
+    "lp_get_moe_gemv": (_vp, []),
+    "lp_get_moe_gemv_multi": (_vp, []),
+    "lp_register_weights": (_i, [_vp, _sz]),
+    "lp_release_weights": (None, []),
+    "lp_quantize_act": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "lp_act_workspace_bytes": (_sz, [_i, _i]),
+    "lp_quantize_act_dev": (_i, [_vp, _i, _i, _vp, _sz, _vp]),
+    "lp_act_unpack_dev": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "lp_gemm_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "lp_gemm_q_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
+    "lp_block_sums_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
+    "lp_moe_grouped_dev": (_i, [_vp, _i, _vp, _vp, _u32, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "lp_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "lp_last_error": (C.c_char_p, []),
+    "lp_device_ok": (_i, []),
+}
+
+_lib = None
+
+
+class LaplaceHipError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built: run `python -m laplace_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != LP_OK:
+        msg = lib().lp_last_error().decode(errors="replace")
+        raise LaplaceHipError(f"{what}: {STATUS_NAMES.get(rc, rc)}: {msg}")

@@ -1,0 +1,432 @@
+// lp_api.cpp - C ABI over the gfx950 kernels (declarations in
+// include/laplace_hip.h).
+//
+// Host-pointer entry points keep the reference back-end's contract
+// (src/kernels.h:94-119): synchronous, internally parallel, false when the
+// type is not handled. They stage x and y through pinned host buffers on a
+// library-owned stream and take weights from device copies: a registered
+// region (lp_register_weights, after src/metal.mm:581-599) or a copy cached
+// by host pointer on first use (after get_weight_buf, src/metal.mm:601-621).
+// Calls are serialised by one mutex, as the Metal back-end does
+// (src/metal.mm:646).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/laplace_hip.h"
+#include "lp_internal.h"
+
+namespace lp {
+
+static thread_local char g_err[512];
+
+static void set_err(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+#define LP_HIP(call)                                                              \
+    do {                                                                          \
+        hipError_t e_ = (call);                                                   \
+        if (e_ != hipSuccess) {                                                   \
+            set_err("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_),        \
+                    __FILE__, __LINE__);                                          \
+            return LP_EHIP;                                                       \
+        }                                                                         \
+    } while (0)
+
+struct DevInfo {
+    bool probed = false;
+    bool ok = false;
+    int cus = 0;
+};
+
+static std::mutex g_info_mtx;
+static std::unordered_map<int, DevInfo> g_info;
+
+static DevInfo& dev_info() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lk(g_info_mtx);
+    DevInfo& di = g_info[dev];
+    if (!di.probed) {
+        di.probed = true;
+        hipDeviceProp_t p;
+        if (dev >= 0 && hipGetDeviceProperties(&p, dev) == hipSuccess) {
+            di.cus = p.multiProcessorCount;
+            di.ok = std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+        }
+    }
+    return di;
+}
+
+int device_cu_count() {
+    int n = dev_info().cus;
+    return n > 0 ? n : 256;
+}
+
+// ---------------------------------------------------------------------------
+// Workspace layout for quantized activations:
+//   [qs: M*K int8][d: M*nb f32][sum: M*nb f32][s16: M*nb i32], each 256-B aligned.
+
+static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static size_t ws_bytes(int M, int K) {
+    const size_t nbk = (size_t)M * (K / 32);
+    return up256((size_t)M * K) + 3 * up256(nbk * 4);
+}
+
+static ActView ws_view(void* ws, int M, int K) {
+    uint8_t* p = static_cast<uint8_t*>(ws);
+    const size_t nbk = (size_t)M * (K / 32);
+    ActView a;
+    a.qs = reinterpret_cast<int8_t*>(p);
+    p += up256((size_t)M * K);
+    a.d = reinterpret_cast<float*>(p);
+    p += up256(nbk * 4);
+    a.sum = reinterpret_cast<float*>(p);
+    p += up256(nbk * 4);
+    a.s16 = reinterpret_cast<int32_t*>(p);
+    return a;
+}
+
+static bool type_handled(uint32_t t) {
+    return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K;
+}
+
+// Shape/alignment preconditions of the kernels. Returns LP_OK or the status
+// to report.
+static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
+    if (!type_handled(type)) {
+        set_err("type %u not handled on the GPU", type);
+        return LP_UNSUPPORTED;
+    }
+    if (M < 0 || K <= 0 || N < 0) {
+        set_err("bad shape M=%d K=%d N=%d", M, K, N);
+        return LP_EINVAL;
+    }
+    const int need = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;
+    if (K % need != 0 || K > 32768) {
+        set_err("K=%d must be a multiple of %d and at most 32768", K, need);
+        return LP_UNSUPPORTED;
+    }
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+    const uintptr_t align = (type == T_Q4_K) ? 16 : 4;
+    if (a % align != 0) {
+        set_err("weights must be %zu-byte aligned for type %u", (size_t)align, type);
+        return LP_UNSUPPORTED;
+    }
+    return LP_OK;
+}
+
+static int gemm_q(const ActView& A, const uint8_t* w, uint32_t type, float* y, int M, int K,
+                  int N, hipStream_t st) {
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mt = M - m0 < 8 ? M - m0 : 8;
+        ActView sub;
+        sub.qs = A.qs + (size_t)m0 * K;
+        sub.d = A.d + (size_t)m0 * (K / 32);
+        sub.sum = A.sum + (size_t)m0 * (K / 32);
+        sub.s16 = A.s16 + (size_t)m0 * (K / 32);
+        LP_HIP(launch_gemv(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
+    }
+    return LP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Host-pointer machinery.
+
+struct Region {
+    const uint8_t* host;
+    size_t size;
+    uint8_t* dev;
+};
+
+struct HostCtx {
+    hipStream_t stream = nullptr;
+    std::vector<Region> regions;                       // registered ranges
+    std::unordered_map<const void*, Region> copies;    // per-pointer cache
+    void* ws = nullptr;
+    size_t ws_cap = 0;
+    float* xd = nullptr;
+    size_t xd_cap = 0;
+    float* yd = nullptr;
+    size_t yd_cap = 0;
+    int* idx_d = nullptr;
+    size_t idx_cap = 0;
+    float* x_pin = nullptr;
+    size_t x_pin_cap = 0;
+    float* y_pin = nullptr;
+    size_t y_pin_cap = 0;
+};
+
+static std::mutex g_host_mtx;
+static std::unordered_map<int, HostCtx> g_host;
+
+static HostCtx* host_ctx() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    HostCtx& c = g_host[dev];
+    if (!c.stream && hipStreamCreate(&c.stream) != hipSuccess) return nullptr;
+    return &c;
+}
+
+template <typename T>
+static int grow_dev(T*& p, size_t& cap, size_t bytes) {
+    if (bytes <= cap) return LP_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    LP_HIP(hipMalloc(reinterpret_cast<void**>(&p), bytes));
+    cap = bytes;
+    return LP_OK;
+}
+
+template <typename T>
+static int grow_pinned(T*& p, size_t& cap, size_t bytes) {
+    if (bytes <= cap) return LP_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+    LP_HIP(hipHostMalloc(reinterpret_cast<void**>(&p), bytes, hipHostMallocDefault));
+    cap = bytes;
+    return LP_OK;
+}
+
+// Device address of `len` bytes of host weights at w.
+static int resolve_weights(HostCtx& c, const uint8_t* w, size_t len, const uint8_t** out) {
+    for (const Region& r : c.regions) {
+        if (w >= r.host && w + len <= r.host + r.size) {
+            *out = r.dev + (w - r.host);
+            return LP_OK;
+        }
+    }
+    auto it = c.copies.find(w);
+    if (it != c.copies.end() && it->second.size >= len) {
+        *out = it->second.dev;
+        return LP_OK;
+    }
+    if (it != c.copies.end()) {
+        (void)hipFree(it->second.dev);
+        c.copies.erase(it);
+    }
+    uint8_t* d = nullptr;
+    LP_HIP(hipMalloc(reinterpret_cast<void**>(&d), len));
+    if (hipMemcpy(d, w, len, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        set_err("weight upload failed");
+        return LP_EHIP;
+    }
+    c.copies[w] = Region{w, len, d};
+    *out = d;
+    return LP_OK;
+}
+
+// Shared body of the host-pointer GEMM / MoE calls. rows = activation rows
+// staged (M for the GEMM, 1 or n_experts for MoE).
+static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K,
+                     int N) {
+    int st = check_shape(type, w, M, K, N);
+    if (st != LP_OK) return st;
+    if (!dev_info().ok) {
+        set_err("no gfx950 device");
+        return LP_ENODEV;
+    }
+    if (M == 0 || N == 0) return LP_OK;
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) {
+        set_err("no HIP device/stream");
+        return LP_ENODEV;
+    }
+    const size_t xb = sizeof(float) * (size_t)M * K, yb = sizeof(float) * (size_t)M * N;
+    const uint8_t* wd = nullptr;
+    int rc;
+    if ((rc = resolve_weights(*c, w, row_bytes(type, K) * (size_t)N, &wd)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->xd, c->xd_cap, xb)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->yd, c->yd_cap, yb)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->ws, c->ws_cap, ws_bytes(M, K))) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->x_pin, c->x_pin_cap, xb)) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, yb)) != LP_OK) return rc;
+    std::memcpy(c->x_pin, x, xb);
+    LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
+    const ActView A = ws_view(c->ws, M, K);
+    LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
+    if ((rc = gemm_q(A, wd, type, c->yd, M, K, N, c->stream)) != LP_OK) return rc;
+    LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipStreamSynchronize(c->stream));
+    std::memcpy(y, c->y_pin, yb);
+    return LP_OK;
+}
+
+static int host_moe(const float* x, const uint8_t* w, uint32_t type, const int* idx, int n_exp,
+                    float* y, int K, int N, bool multi) {
+    int st = check_shape(type, w, 1, K, N);
+    if (st != LP_OK) return st;
+    if (n_exp <= 0 || N == 0) return LP_OK;
+    const size_t rb = row_bytes(type, K), per_expert = rb * (size_t)N;
+    // Each selected expert is a GEMM over its slice of the stacked tensor
+    // (the sequential fallback of src/matmul.cpp:469-476, :493-499).
+    for (int k = 0; k < n_exp; k++) {
+        const uint8_t* we = w + (size_t)idx[k] * per_expert;
+        const float* xk = multi ? x + (size_t)k * K : x;
+        int rc = host_gemm(xk, we, type, y + (size_t)k * N, 1, K, N);
+        if (rc != LP_OK) return rc;
+    }
+    return LP_OK;
+}
+
+}  // namespace lp
+
+using namespace lp;
+
+extern "C" {
+
+bool lp_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N) {
+    int rc = host_gemm(x, w, type, y, M, K, N);
+    if (rc != LP_OK && rc != LP_UNSUPPORTED) fprintf(stderr, "[laplace_hip] %s\n", g_err);
+    return rc == LP_OK;
+}
+
+bool lp_moe_gemv(const float* x, const uint8_t* w, uint32_t type, const int* expert_idx,
+                 int n_experts, float* y, int K, int N) {
+    int rc = host_moe(x, w, type, expert_idx, n_experts, y, K, N, false);
+    if (rc != LP_OK && rc != LP_UNSUPPORTED) fprintf(stderr, "[laplace_hip] %s\n", g_err);
+    return rc == LP_OK;
+}
+
+bool lp_moe_gemv_multi(const float* x, const uint8_t* w, uint32_t type, const int* expert_idx,
+                       int n_experts, float* y, int K, int N) {
+    int rc = host_moe(x, w, type, expert_idx, n_experts, y, K, N, true);
+    if (rc != LP_OK && rc != LP_UNSUPPORTED) fprintf(stderr, "[laplace_hip] %s\n", g_err);
+    return rc == LP_OK;
+}
+
+lp_gemm_fn lp_get_gemm(void) { return dev_info().ok ? lp_gemm : nullptr; }
+lp_moe_gemv_fn lp_get_moe_gemv(void) { return dev_info().ok ? lp_moe_gemv : nullptr; }
+lp_moe_gemv_fn lp_get_moe_gemv_multi(void) { return dev_info().ok ? lp_moe_gemv_multi : nullptr; }
+
+int lp_register_weights(const void* base, size_t size) {
+    if (!base || size == 0) {
+        set_err("empty region");
+        return LP_EINVAL;
+    }
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) return LP_ENODEV;
+    uint8_t* d = nullptr;
+    LP_HIP(hipMalloc(reinterpret_cast<void**>(&d), size));
+    if (hipMemcpy(d, base, size, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        set_err("weight upload failed");
+        return LP_EHIP;
+    }
+    c->regions.push_back(Region{static_cast<const uint8_t*>(base), size, d});
+    return LP_OK;
+}
+
+void lp_release_weights(void) {
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) return;
+    (void)hipStreamSynchronize(c->stream);
+    for (Region& r : c->regions) (void)hipFree(r.dev);
+    for (auto& kv : c->copies) (void)hipFree(kv.second.dev);
+    c->regions.clear();
+    c->copies.clear();
+}
+
+int lp_quantize_act(const float* x, int M, int K, float* d, float* sum, int16_t* sum_lo,
+                    int16_t* sum_hi, int8_t* qs) {
+    if (K % 32 != 0 || M < 0) return LP_EINVAL;
+    if (!dev_info().ok) return LP_ENODEV;
+    if (M == 0) return LP_OK;
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) return LP_ENODEV;
+    const size_t xb = sizeof(float) * (size_t)M * K;
+    const size_t nbk = (size_t)M * (K / 32);
+    int rc;
+    if ((rc = grow_dev(c->xd, c->xd_cap, xb)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->ws, c->ws_cap, ws_bytes(M, K))) != LP_OK) return rc;
+    LP_HIP(hipMemcpyAsync(c->xd, x, xb, hipMemcpyHostToDevice, c->stream));
+    const ActView A = ws_view(c->ws, M, K);
+    LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
+    std::vector<int32_t> s16(nbk);
+    LP_HIP(hipMemcpyAsync(qs, A.qs, (size_t)M * K, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipMemcpyAsync(d, A.d, nbk * 4, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipMemcpyAsync(sum, A.sum, nbk * 4, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipMemcpyAsync(s16.data(), A.s16, nbk * 4, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipStreamSynchronize(c->stream));
+    for (size_t i = 0; i < nbk; i++) {
+        sum_lo[i] = (int16_t)(uint16_t)((uint32_t)s16[i] & 0xffffu);
+        sum_hi[i] = (int16_t)(uint16_t)((uint32_t)s16[i] >> 16);
+    }
+    return LP_OK;
+}
+
+size_t lp_act_workspace_bytes(int M, int K) { return ws_bytes(M, K); }
+
+int lp_quantize_act_dev(const float* x, int M, int K, void* ws, size_t wsb, void* stream) {
+    if (K % 32 != 0 || M < 0 || (M > 0 && (!x || !ws))) return LP_EINVAL;
+    if (wsb < ws_bytes(M, K)) {
+        set_err("workspace %zu < %zu bytes", wsb, ws_bytes(M, K));
+        return LP_EINVAL;
+    }
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+        set_err("x must be 16-byte aligned");
+        return LP_EINVAL;
+    }
+    LP_HIP(launch_quantize(x, M, K, ws_view(ws, M, K), static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
+int lp_act_unpack_dev(const void* ws, int M, int K, float* d, float* sum, int32_t* sums16,
+                      int8_t* qs, void* stream) {
+    const ActView A = ws_view(const_cast<void*>(ws), M, K);
+    const size_t nbk = (size_t)M * (K / 32);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (qs) LP_HIP(hipMemcpyAsync(qs, A.qs, (size_t)M * K, hipMemcpyDeviceToDevice, st));
+    if (d) LP_HIP(hipMemcpyAsync(d, A.d, nbk * 4, hipMemcpyDeviceToDevice, st));
+    if (sum) LP_HIP(hipMemcpyAsync(sum, A.sum, nbk * 4, hipMemcpyDeviceToDevice, st));
+    if (sums16) LP_HIP(hipMemcpyAsync(sums16, A.s16, nbk * 4, hipMemcpyDeviceToDevice, st));
+    return LP_OK;
+}
+
+int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                  void* stream) {
+    int rc = check_shape(type, w, M, K, N);
+    if (rc != LP_OK) return rc;
+    return gemm_q(ws_view(const_cast<void*>(ws), M, K), w, type, y, M, K, N,
+                  static_cast<hipStream_t>(stream));
+}
+
+int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                void* ws, size_t wsb, void* stream) {
+    int rc = check_shape(type, w, M, K, N);
+    if (rc != LP_OK) return rc;
+    if ((rc = lp_quantize_act_dev(x, M, K, ws, wsb, stream)) != LP_OK) return rc;
+    return lp_gemm_q_dev(ws, w, type, y, M, K, N, stream);
+}
+
+int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M, int K,
+                      int N, void* stream) {
+    int rc = check_shape(type, w, M, K, N);
+    if (rc != LP_OK) return rc;
+    LP_HIP(launch_block_sums(type, w, ws_view(const_cast<void*>(ws), M, K), out, M, K, N,
+                             static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
+const char* lp_last_error(void) { return g_err; }
+
+int lp_device_ok(void) { return dev_info().ok ? 1 : 0; }
+
+}  // extern "C"

@@ -1,0 +1,246 @@
+// lp_chunks.h - per-type decode of one 64-element "chunk" of a weight row
+// against the matching 64 quantized activations.
+//
+// A chunk is the unit one lane owns in the GEMV: 64 consecutive elements of
+// K, i.e. 2 activation blocks. For every type the same two steps run:
+//   isums()   the exact int32 sub-block dots the reference's NEON kernels
+//             form (src/matmul_simd.cpp:143-342): per 32-element block for
+//             Q8_0/Q4_0/Q4_K, per 16 elements for Q6_K;
+//   partial() the fp32 block-scale epilogue over those integers.
+// Weights are read straight from HBM as dwords (nontemporal: each weight
+// byte is used once per launch); activations come from registers the lane
+// filled once (Act) and reuses for every row it visits.
+#pragma once
+
+#include "lp_device.h"
+
+namespace lp {
+
+template <uint32_t T> struct Chunk;
+
+// ---------------------------------------------------------------------------
+// Q8_0: chunk c = blocks 2c, 2c+1 = 68 bytes at row + 68c (4-byte aligned
+// when the row is). Reference: dot_row_q8_0_int_neon, matmul_simd.cpp:143-160.
+template <> struct Chunk<T_Q8_0> {
+    static constexpr int NSUB = 2;
+    __device__ static int sub_index(int c, int s) { return 2 * c + s; }
+    struct Wt { uint32_t w[17]; };
+    struct Act { uint32_t q[2][8]; float d[2]; float s[2]; int qsum[4]; };
+
+    __device__ static void load_w(const uint8_t* row, int c, Wt& w) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * c);
+#pragma unroll
+        for (int i = 0; i < 17; i++) w.w[i] = __builtin_nontemporal_load(p + i);
+    }
+    __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) s0 = dot4(alignb(w.w[i + 1], w.w[i], 2), a.q[0][i], s0);
+#pragma unroll
+        for (int i = 0; i < 8; i++) s1 = dot4(w.w[9 + i], a.q[1][i], s1);
+        is[0] = s0;
+        is[1] = s1;
+    }
+    __device__ static float partial(const Wt& w, const Act& a, const int (&is)[NSUB], int) {
+        float d0 = fp16_bits_to_f32(w.w[0]);
+        float d1 = fp16_bits_to_f32(w.w[8] >> 16);
+        float acc = (d0 * a.d[0]) * (float)is[0];
+        return fmaf(d1 * a.d[1], (float)is[1], acc);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q4_0: chunk c = blocks 2c, 2c+1 = 36 bytes at row + 36c.
+// Reference: dot_row_q4_0_int_neon, matmul_simd.cpp:162-182: the integer is
+// sum(nibble * q) with the unsigned nibble; the -8 offset is applied in fp32
+// through the activation block sum.
+template <> struct Chunk<T_Q4_0> {
+    static constexpr int NSUB = 2;
+    __device__ static int sub_index(int c, int s) { return 2 * c + s; }
+    struct Wt { uint32_t w[9]; };
+    struct Act { uint32_t q[2][8]; float d[2]; float s[2]; int qsum[4]; };
+
+    __device__ static void load_w(const uint8_t* row, int c, Wt& w) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 36 * c);
+#pragma unroll
+        for (int i = 0; i < 9; i++) w.w[i] = __builtin_nontemporal_load(p + i);
+    }
+    __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t q = alignb(w.w[i + 1], w.w[i], 2);
+            s0 = dot4(q & 0x0f0f0f0fu, a.q[0][i], s0);
+            s0 = dot4((q >> 4) & 0x0f0f0f0fu, a.q[0][4 + i], s0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t q = w.w[5 + i];
+            s1 = dot4(q & 0x0f0f0f0fu, a.q[1][i], s1);
+            s1 = dot4((q >> 4) & 0x0f0f0f0fu, a.q[1][4 + i], s1);
+        }
+        is[0] = s0;
+        is[1] = s1;
+    }
+    __device__ static float partial(const Wt& w, const Act& a, const int (&is)[NSUB], int) {
+        float d0 = fp16_bits_to_f32(w.w[0]);
+        float d1 = fp16_bits_to_f32(w.w[4] >> 16);
+        float acc = (d0 * a.d[0]) * (float)is[0];
+        acc = fmaf(d1 * a.d[1], (float)is[1], acc);
+        // - d * 8 * xa.sum per block
+        acc = fmaf(-(d0 * 8.0f), a.s[0], acc);
+        return fmaf(-(d1 * 8.0f), a.s[1], acc);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q4_K: chunk c = super-block c>>2, quarter jb = c&3: the 32 qs bytes
+// 32jb..32jb+31 whose low nibbles are sub-block 2jb and high nibbles
+// sub-block 2jb+1. Reference: dot_row_q4_k_int_neon, matmul_simd.cpp:226-283.
+// Super-blocks are 144 = 9*16 bytes, so every chunk is 16-byte aligned when
+// the tensor base is.
+template <> struct Chunk<T_Q4_K> {
+    static constexpr int NSUB = 2;
+    __device__ static int sub_index(int c, int s) { return 2 * c + s; }
+    struct Wt { u32x4 h; u32x4 q0, q1; };
+    struct Act { uint32_t q[2][8]; float d[2]; float s[2]; int qsum[4]; };
+
+    __device__ static void load_w(const uint8_t* row, int c, Wt& w) {
+        const uint8_t* blk = row + 144 * (c >> 2);
+        const int jb = c & 3;
+        w.h = ld_nt16(blk);
+        w.q0 = ld_nt16(blk + 16 + 32 * jb);
+        w.q1 = ld_nt16(blk + 32 + 32 * jb);
+    }
+    __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s0 = dot4(q[i] & 0x0f0f0f0fu, a.q[0][i], s0);
+            s1 = dot4((q[i] >> 4) & 0x0f0f0f0fu, a.q[1][i], s1);
+        }
+        is[0] = s0;
+        is[1] = s1;
+    }
+    __device__ static float partial(const Wt& w, const Act& a, const int (&is)[NSUB], int c) {
+        const float d = fp16_bits_to_f32(w.h.x);
+        const float dmin = fp16_bits_to_f32(w.h.x >> 16);
+        const int jb = c & 3;
+        uint32_t sc1, m1, sc2, m2;
+        scale_min_k4(2 * jb, w.h.y, w.h.z, w.h.w, sc1, m1);
+        scale_min_k4(2 * jb + 1, w.h.y, w.h.z, w.h.w, sc2, m2);
+        float acc = ((d * (float)sc1) * a.d[0]) * (float)is[0];
+        acc = fmaf((d * (float)sc2) * a.d[1], (float)is[1], acc);
+        acc = fmaf(-(dmin * (float)m1), a.s[0], acc);
+        return fmaf(-(dmin * (float)m2), a.s[1], acc);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q6_K: chunk c = super-block c>>2, half h = (c>>1)&1, lane-half lr = c&1.
+// It covers elements 128h + 32g + 16lr + l (g < 4, l < 16): four 16-element
+// groups, each with its own int8 scale sc[8h + 2g + lr]. Reference:
+// dot_row_q6_k_int_neon, matmul_simd.cpp:285-342. Super-blocks are 210
+// bytes, so chunks are only 2-byte aligned: loads go through load_window.
+// The 6-bit code v in [0, 63] is used unsigned and the -32 offset is applied
+// exactly as -32 * sum(q) over the same 16 saturated activations.
+template <> struct Chunk<T_Q6_K> {
+    static constexpr int NSUB = 4;
+    // group g of chunk c is 16-element sub-block 16sb + 8h + 2g + lr
+    __device__ static int sub_index(int c, int g) {
+        return 16 * (c >> 2) + 8 * ((c >> 1) & 1) + 2 * g + (c & 1);
+    }
+    struct Wt { uint32_t la[4], lb[4], qh[4], sc[2]; uint32_t d; };
+    struct Act { uint32_t q[4][4]; float d[4]; float s[2]; int qsum[4]; };
+
+    __device__ static void load_w(const uint8_t* row, int c, Wt& w) {
+        const uint8_t* blk = row + 210 * (c >> 2);
+        const int h = (c >> 1) & 1, lr = c & 1;
+        load_window<4>(blk + 64 * h + 16 * lr, w.la);
+        load_window<4>(blk + 64 * h + 32 + 16 * lr, w.lb);
+        load_window<4>(blk + 128 + 32 * h + 16 * lr, w.qh);
+        load_window<2>(blk + 192 + 8 * h, w.sc);
+        w.d = load_u16(blk + 208);
+    }
+    __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
+        int s[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t hb = w.qh[i];
+            const uint32_t v0 = (w.la[i] & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4);
+            const uint32_t v1 = (w.lb[i] & 0x0f0f0f0fu) | (((hb >> 2) & 0x03030303u) << 4);
+            const uint32_t v2 = ((w.la[i] >> 4) & 0x0f0f0f0fu) | (((hb >> 4) & 0x03030303u) << 4);
+            const uint32_t v3 = ((w.lb[i] >> 4) & 0x0f0f0f0fu) | (((hb >> 6) & 0x03030303u) << 4);
+            s[0] = dot4(v0, a.q[0][i], s[0]);
+            s[1] = dot4(v1, a.q[1][i], s[1]);
+            s[2] = dot4(v2, a.q[2][i], s[2]);
+            s[3] = dot4(v3, a.q[3][i], s[3]);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; g++) is[g] = s[g] - 32 * a.qsum[g];
+    }
+    __device__ static float partial(const Wt& w, const Act& a, const int (&is)[NSUB], int c) {
+        const float d = fp16_bits_to_f32(w.d);
+        const int lr = c & 1;
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int bidx = lr + 2 * g;   // byte of the 8 scale bytes of this half
+            const int sc = (int)(int8_t)((w.sc[bidx >> 2] >> (8 * (bidx & 3))) & 0xffu);
+            acc = fmaf((d * a.d[g]) * (float)sc, (float)is[g], acc);
+        }
+        return acc;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Activation registers for chunk c of one row of quantized activations.
+
+__device__ __forceinline__ void load_q16(const int8_t* p, uint32_t (&q)[4]) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+}
+
+__device__ __forceinline__ int qsum16(const uint32_t (&q)[4]) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s = dot4(q[i], 0x01010101u, s);
+    return s;
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void load_act(const ActView& A, int K, int m, int c,
+                                         typename Chunk<T>::Act& a) {
+    const int nb = K >> 5;
+    const int8_t* qrow = A.qs + (size_t)m * K;
+    const float* drow = A.d + (size_t)m * nb;
+    const float* srow = A.sum + (size_t)m * nb;
+    if constexpr (T == T_Q6_K) {
+        const int sb = c >> 2, h = (c >> 1) & 1, lr = c & 1;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int blk = 8 * sb + 4 * h + g;
+            load_q16(qrow + 32 * blk + 16 * lr, a.q[g]);
+            a.d[g] = drow[blk];
+            a.qsum[g] = qsum16(a.q[g]);
+        }
+        a.s[0] = a.s[1] = 0.0f;
+    } else {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int blk = 2 * c + b;
+            uint32_t lo[4], hi[4];
+            load_q16(qrow + 32 * blk, lo);
+            load_q16(qrow + 32 * blk + 16, hi);
+#pragma unroll
+            for (int i = 0; i < 4; i++) { a.q[b][i] = lo[i]; a.q[b][4 + i] = hi[i]; }
+            a.d[b] = drow[blk];
+            a.s[b] = srow[blk];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) a.qsum[i] = 0;
+    }
+}
+
+}  // namespace lp

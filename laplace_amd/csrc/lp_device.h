@@ -1,0 +1,108 @@
+// lp_device.h - device-side building blocks shared by the gfx950 kernels:
+// GGUF block geometry, fp16 decode, byte-window loads for blocks that are
+// only 2-byte aligned, int8 dot helpers and wavefront reductions.
+//
+// Block layouts are those of the reference's src/kernels.h:21-79 (GGUF):
+//   Q4_0  18 B : fp16 d, 16 B nibbles (low nibble = element l, high = l+16)
+//   Q8_0  34 B : fp16 d, 32 x int8
+//   Q4_K 144 B : fp16 d, fp16 dmin, 12 B packed 6-bit (scale, min) x 8, 128 B nibbles
+//   Q6_K 210 B : 128 B ql, 64 B qh, 16 x int8 scales, fp16 d (last)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lp {
+
+// GGMLType values (reference src/tensor.h:11-34).
+enum : uint32_t {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8,
+    T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30,
+};
+
+// Quantized activations in HBM, structure-of-arrays (one ActQ8 of the
+// reference, src/matmul_simd.cpp:26-32, is spread over the four arrays):
+//   qs   int8 [M, K]            codes, row-major (MFMA/dot friendly)
+//   d    f32  [M, K/32]         block scale amax/127
+//   sum  f32  [M, K/32]         d * (sum_lo + sum_hi)
+//   s16  i32  [M, K/32]         sum_lo | sum_hi << 16 (int16 each)
+struct ActView {
+    int8_t*  qs;
+    float*   d;
+    float*   sum;
+    int32_t* s16;
+};
+
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
+    // v_cvt_f32_f16 is exact for every finite fp16 value, subnormals
+    // included (fp16 denormals are not flushed on gfx950).
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+    return (float)v;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte nontemporal load (global_load_dwordx4 nt); p must be 16-byte aligned.
+__device__ __forceinline__ u32x4 ld_nt16(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// int8x4 . int8x4 + acc (v_dot4_i32_i8).
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int acc) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, acc, false);
+}
+
+// ((hi:lo) >> 8*sh)[31:0]  (v_alignbyte_b32)
+__device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+// NDW dwords of the byte window starting at p, for p only 2-byte aligned.
+// Loads NDW aligned dwords, plus one more only when p is not 4-byte aligned
+// (so a window ending exactly at an allocation end never reads past it by a
+// whole dword), then funnel-shifts them.
+template <int NDW>
+__device__ __forceinline__ void load_window(const uint8_t* p, uint32_t (&out)[NDW]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = (uint32_t)(a & 3);
+    uint32_t w[NDW + 1];
+#pragma unroll
+    for (int i = 0; i < NDW; i++) w[i] = __builtin_nontemporal_load(base + i);
+    w[NDW] = sh ? __builtin_nontemporal_load(base + NDW) : 0u;
+#pragma unroll
+    for (int i = 0; i < NDW; i++) out[i] = alignb(w[i + 1], w[i], sh);
+}
+
+// Two bytes at p (2-byte aligned) as a zero-extended u32.
+__device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Byte j (0..11) of the K-quant scale array held in three dwords.
+__device__ __forceinline__ uint32_t byte_of3(uint32_t s0, uint32_t s1, uint32_t s2, int j) {
+    uint32_t w = j < 4 ? s0 : (j < 8 ? s1 : s2);
+    return (w >> (8 * (j & 3))) & 0xffu;
+}
+
+// get_scale_min_k4 (reference src/kernels.h:82-90) on the 12 scale bytes.
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t& sc, uint32_t& mn) {
+    if (j < 4) {
+        sc = byte_of3(s0, s1, s2, j) & 63u;
+        mn = byte_of3(s0, s1, s2, j + 4) & 63u;
+    } else {
+        uint32_t hi = byte_of3(s0, s1, s2, j + 4);
+        sc = (hi & 0xfu) | ((byte_of3(s0, s1, s2, j - 4) >> 6) << 4);
+        mn = (hi >> 4) | ((byte_of3(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace lp

@@ -1,0 +1,35 @@
+// lp_internal.h - launchers shared between the kernel translation units and
+// the C-ABI layer (lp_api.cpp). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lp_device.h"
+
+namespace lp {
+
+// Bytes of one weight row of K elements: K / epb * bpb, as the reference
+// computes rb (src/matmul_simd.cpp:482). 0 for types this library does not
+// decode.
+inline size_t row_bytes(uint32_t type, int K) {
+    switch (type) {
+        case T_Q8_0: return (size_t)(K / 32) * 34;
+        case T_Q4_0: return (size_t)(K / 32) * 18;
+        case T_Q4_K: return (size_t)(K / 256) * 144;
+        case T_Q6_K: return (size_t)(K / 256) * 210;
+        default: return 0;
+    }
+}
+
+// Multiprocessor count of the current device (cached per device).
+int device_cu_count();
+
+hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st);
+hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
+                       int N, hipStream_t st);
+hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, int32_t* out,
+                             int M, int K, int N, hipStream_t st);
+
+}  // namespace lp

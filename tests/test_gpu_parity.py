@@ -1,0 +1,217 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on the
+same seeded inputs.
+
+Bars (from the reference's int8 path, src/matmul_simd.cpp):
+  * quantized activation blocks (d, sum, sum_lo, sum_hi, codes): bit-exact;
+  * per-sub-block int32 dot sums: bit-exact;
+  * fp32 outputs: normwise max|dy| / max|y| <= 1e-4 (TOL below), plus the
+    reference's own per-element acceptance (tests/test_matmul.cpp:88-97).
+"""
+import numpy as np
+import pytest
+
+from hip_util import (Q4_0, Q4_K, Q6_K, Q8_0, TYPES, NAMES, block_sums_dev, gemm_dev, normwise,
+                      quantize_dev, synth_weights, synth_x)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# quantizer
+
+
+def _edge_rows(K):
+    rows = []
+    x = np.zeros(K, np.float32)
+    rows.append(x.copy())                                   # all zero
+    x = np.ones(K, np.float32)
+    x[3] = np.nan
+    x[40] = np.inf
+    x[70] = -np.inf
+    rows.append(x)
+    x = np.zeros(K, np.float32)                             # ties at d = id = 1
+    x[0] = 127.0
+    x[1:11] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 100.5, -100.5, 126.5]
+    rows.append(x)
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(K) * 1e-39).astype(np.float32)   # subnormal inputs
+    x[32:64] *= 1e-5
+    rows.append(x)
+    x = (rng.standard_normal(K) * 1e30).astype(np.float32)
+    rows.append(x)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (8, 3584), (5, 2048), (64, 768)])
+def test_quantizer_bit_exact(orc, M, K):
+    _flush(f"quantizer M={M} K={K}")
+    x = synth_x(M, K, seed=M * 7 + K, outliers=0.01)
+    d, s, s16, qs = quantize_dev(x)
+    rd, rs, rlo, rhi, rqs = orc.quantize_act(x)
+    assert np.array_equal(qs, rqs)
+    assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+    lo = (s16 & 0xffff).astype(np.uint16).view(np.int16)
+    hi = ((s16.view(np.uint32) >> 16) & 0xffff).astype(np.uint16).view(np.int16)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+
+
+def test_quantizer_edge_cases_bit_exact(orc):
+    _flush("quantizer edge cases")
+    x = _edge_rows(256)
+    d, s, s16, qs = quantize_dev(x)
+    rd, rs, rlo, rhi, rqs = orc.quantize_act(x)
+    assert np.array_equal(qs, rqs)
+    # NaN blocks: compare NaN-ness, other values by bits
+    for a, b in ((d, rd), (s, rs)):
+        na, nb = np.isnan(a), np.isnan(b)
+        assert np.array_equal(na, nb)
+        assert np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+    lo = (s16 & 0xffff).astype(np.uint16).view(np.int16)
+    assert np.array_equal(lo, rlo)
+
+
+def test_quantizer_host_api(orc):
+    _flush("quantizer host api")
+    from laplace_amd import quantize_act
+    x = synth_x(3, 1024, seed=5, outliers=0.01)
+    got = quantize_act(x)
+    want = orc.quantize_act(x)
+    for g, w_ in zip(got, want):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(w_).view(np.uint8))
+
+
+# ---------------------------------------------------------------------------
+# integer block sums
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("K", [512, 2816, 4096])
+def test_block_sums_bit_exact(orc, t, K):
+    if t in (Q4_0, Q8_0) and K % 64:
+        pytest.skip("legacy chunk is 64 elements")
+    _flush(f"block sums {NAMES[t]} K={K}")
+    M, N = 3, 33
+    rng = np.random.default_rng(K + t)
+    w = rng.integers(0, 256, (K // (256 if t in (Q4_K, Q6_K) else 32)) * N *
+                     {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[t], dtype=np.uint8)
+    x = synth_x(M, K, seed=K, outliers=0.01)
+    got = block_sums_dev(t, x, w, N)
+    _, _, _, _, qs = orc.quantize_act(x)
+    want = orc.block_sums(t, w, qs, K, N)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# GEMV against the oracle's gemm_int
+
+
+def _check_against_oracle(orc, t, x, w, N, y):
+    ref = orc.gemm_int(t, x, w, N)
+    err = normwise(y, ref)
+    assert err <= TOL, f"normwise {err:.3g}"
+    diff = np.abs(y - ref)
+    ok = (diff <= 1e-3) | (diff <= 1e-3 * np.maximum(np.abs(y), np.abs(ref)))
+    assert ok.all(), f"{(~ok).sum()} outputs outside rel/abs 1e-3"
+
+
+REF_SHAPES = [(t, 512, n) for n in (1, 8, 33, 256) for t in TYPES] + \
+             [(t, 2816, n) for n in (1, 8, 256, 4096) for t in (Q4_K, Q6_K)]
+
+
+@pytest.mark.parametrize("t,K,N", REF_SHAPES, ids=lambda v: str(v))
+def test_gemv_reference_test_shapes(orc, t, K, N):
+    """The reference's matmul test inputs (tests/test_matmul.cpp:272-291)."""
+    _flush(f"gemv ref-shape {NAMES[t]} K={K} N={N}")
+    w = orc.ref_test_weights(t, K, N)
+    x = orc.ref_test_x(t, K)[None, :]
+    y = gemm_dev(t, x, w, N)
+    _check_against_oracle(orc, t, x, w, N, y)
+
+
+CONFIG_SHAPES = [
+    (Q8_0, 4096, 4096, 1),
+    (Q4_0, 4096, 14336, 1), (Q4_0, 14336, 4096, 1),
+    (Q4_K, 4096, 14336, 1),
+    (Q4_K, 3584, 18944, 1), (Q4_K, 3584, 18944, 4), (Q4_K, 3584, 18944, 8),
+    (Q6_K, 18944, 3584, 1), (Q6_K, 18944, 3584, 4), (Q6_K, 18944, 3584, 8),
+]
+
+
+@pytest.mark.parametrize("t,K,N,M", CONFIG_SHAPES, ids=lambda v: str(v))
+def test_gemv_baseline_configs(orc, t, K, N, M):
+    """BASELINE.json configs 1-3 at full size; the oracle checks a seeded
+    sample of 256 rows (rows are independent), the GPU computes all N."""
+    _flush(f"gemv config {NAMES[t]} K={K} N={N} M={M}")
+    w = synth_weights(t, K, N, seed=K * 3 + N)
+    x = synth_x(M, K, seed=K + M)
+    y = gemm_dev(t, x, w, N)
+    assert np.isfinite(y).all()
+    rb = len(w) // N
+    rows = np.sort(np.random.default_rng(N).choice(N, 256, replace=False))
+    ws = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    _check_against_oracle(orc, t, x, ws, len(rows), y[:, rows])
+
+
+@pytest.mark.parametrize("t", TYPES, ids=lambda t: NAMES[t])
+def test_batched_rows_equal_single(t):
+    """tests/test_matmul.cpp:217-250: matmul_rows(M=7) equals M matmul_row
+    calls within 1e-4 (random bytes as weights; NaN skipped)."""
+    _flush(f"batched vs single {NAMES[t]}")
+    M, K, N = 7, 512, 64
+    rng = np.random.default_rng(41 + t)
+    w = rng.integers(0, 256, (K // (256 if t in (Q4_K, Q6_K) else 32)) * N *
+                     {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[t], dtype=np.uint8)
+    x = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    yb = gemm_dev(t, x, w, N)
+    for m in range(M):
+        ys = gemm_dev(t, x[m:m + 1], w, N)[0]
+        a, b = yb[m], ys
+        both_nan = np.isnan(a) & np.isnan(b)
+        diff = np.abs(a - b)
+        ok = both_nan | (diff <= 1e-4) | (diff <= 1e-4 * np.maximum(np.abs(a), np.abs(b)))
+        assert ok.all()
+
+
+def test_subnormal_weight_scales(orc):
+    """fp16 scales that are all subnormal must not be flushed to zero."""
+    _flush("subnormal scales")
+    t, K, N = Q8_0, 512, 16
+    w = synth_weights(t, K, N, seed=3).reshape(-1, 34)
+    rng = np.random.default_rng(4)
+    w[:, 0:2] = rng.integers(1, 0x3ff, (w.shape[0], 1), dtype=np.uint16).view(np.uint8).reshape(-1, 2)
+    w = w.reshape(-1)
+    x = synth_x(1, K, seed=9)
+    y = gemm_dev(t, x, w, N)
+    ref = orc.gemm_int(t, x, w, N)
+    assert np.abs(ref).max() > 0
+    assert normwise(y, ref) <= TOL
+
+
+def test_host_api_matches_device_api(orc):
+    _flush("host api vs device api")
+    from laplace_amd import GGMLType, Tensor, matmul_rows
+    t, K, N, M = Q4_K, 2048, 384, 3
+    w = synth_weights(t, K, N, seed=77)
+    x = synth_x(M, K, seed=78)
+    y = np.zeros((M, N), np.float32)
+    matmul_rows(x, Tensor(GGMLType.Q4_K, (K, N), w), y, M, K, N)
+    yd = gemm_dev(t, x, w, N)
+    assert np.array_equal(y.view(np.uint32), yd.view(np.uint32))
+    _check_against_oracle(orc, t, x, w, N, y)
+
+
+def test_unsupported_type_is_reported():
+    from laplace_amd import _lib
+    import ctypes as C
+    x = np.zeros(256, np.float32)
+    w = np.zeros(256 * 2, np.uint8)
+    y = np.zeros(1, np.float32)
+    ok = _lib.lib().lp_gemm(x.ctypes.data, w.ctypes.data, 1, y.ctypes.data, 1, 256, 1)  # F16
+    assert ok is False
