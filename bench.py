@@ -1,0 +1,306 @@
+"""Benchmark of the MI355X GGUF quantized-matmul path (one GPU).
+
+Headline: Q4_K decode GEMV, W = 14336 x 4096
+(N x K), M = 1, fp32 activations quantized on the fly to 32-element int8
+blocks. One step = quantize x + GEMV against one weight copy; steps rotate
+over >= 16 distinct device copies of the weights (> 512 MB, twice the
+256 MB Infinity Cache) so every step streams its weights from HBM. Steps
+are captured in a HIP graph (torch.cuda.graph around the C-ABI calls, which
+launch on torch's current stream) and replayed; the timed region is
+bracketed by torch.cuda.synchronize().
+
+value = algorithmic bytes per step / time per step, in GB/s, where
+algorithmic bytes = weight bytes + 4*M*K (x) + 4*M*N (y).
+
+roofline: the GEMV kernel alone, timed with HIP events over graph replays
+of back-to-back GEMV launches on pre-quantized activations; achieved =
+algorithmic bytes per launch / average launch duration; peak = 8000 GB/s.
+traffic: HBM bytes per launch from rocprofv3 PMC runs, read from
+profiles/<workload>_traffic.json when that file exists (else null).
+
+cpu_baseline: the reference's portable scalar path (gemm_scalar<dot_row_q4_k>,
+src/matmul.cpp:137-167, :320-334) as restated in oracle/liboracle.so, on the
+host cores, same weights, whole matrix, median of repeated runs.
+
+Extra lines (also in the JSON, key "extra"): the other BASELINE.json GEMV
+configs, and the prefill GEMM when it is built.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_MIN_BYTES = 512 << 20
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+TNAME = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+
+def row_bytes(t, K):
+    return {Q4_0: K // 32 * 18, Q8_0: K // 32 * 34, Q4_K: K // 256 * 144, Q6_K: K // 256 * 210}[t]
+
+
+def synth_weights(t, K, N, seed):
+    """Seeded blocks with BASELINE.json's distributions (uniform codes and
+    6-bit fields, fp16 scales |N(0,1)| * 0.01, Q4_0 * 0.02, Q6_K int8
+    scales uniform in [-32, 31])."""
+    rng = np.random.default_rng(seed)
+    bpb = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[t]
+    w = rng.integers(0, 256, row_bytes(t, K) * N, dtype=np.uint8)
+    b = w.reshape(-1, bpb)
+    nb = b.shape[0]
+
+    def f16(scale):
+        return (np.abs(rng.standard_normal(nb)) * scale).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    if t == Q8_0:
+        b[:, 2:] = rng.integers(-127, 128, (nb, 32), dtype=np.int8).view(np.uint8)
+        b[:, 0:2] = f16(0.01)
+    elif t == Q4_0:
+        b[:, 0:2] = f16(0.02)
+    elif t == Q4_K:
+        b[:, 0:2] = f16(0.01)
+        b[:, 2:4] = f16(0.01)
+    elif t == Q6_K:
+        b[:, 192:208] = rng.integers(-32, 32, (nb, 16), dtype=np.int8).view(np.uint8)
+        b[:, 208:210] = f16(0.01)
+    return w
+
+
+def synth_x(M, K, seed, outliers=0.0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if outliers:
+        x[rng.random((M, K)) < outliers] *= 20.0
+    return x
+
+
+class Gpu:
+    def __init__(self):
+        import torch
+        from laplace_amd import _lib
+        self.torch = torch
+        self.L = _lib.lib()
+        self.check = _lib.check
+        if not torch.cuda.is_available():
+            raise SystemExit("bench.py needs a GPU (cuda:0)")
+        if self.L.lp_device_ok() != 1:
+            raise SystemExit("device is not gfx950")
+        self.dev = torch.device("cuda:0")
+
+    def stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def copies(self, w_host, min_bytes=ROTATE_MIN_BYTES, min_copies=16):
+        torch = self.torch
+        n = max(min_copies, -(-min_bytes // w_host.nbytes))
+        base = torch.from_numpy(w_host).to(self.dev)
+        out = [base]
+        for _ in range(n - 1):
+            out.append(base.clone())
+        return out
+
+
+def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
+    """Time quantize+GEMV steps over rotating weight copies; time the GEMV
+    kernel alone with HIP events. Returns a dict of figures."""
+    torch = g.torch
+    w = synth_weights(t, K, N, seed=seed + N + K)
+    x = synth_x(M, K, seed=seed + 1)
+    ws_list = g.copies(w)
+    ncp = len(ws_list)
+    xd = torch.from_numpy(x).to(g.dev)
+    y = torch.empty(M * N, dtype=torch.float32, device=g.dev)
+    nbws = int(g.L.lp_act_workspace_bytes(M, K))
+    ws = torch.empty(nbws, dtype=torch.uint8, device=g.dev)
+    alg_bytes = w.nbytes + 4 * M * K + 4 * M * N
+
+    def step(i):
+        g.check(g.L.lp_gemm_dev(xd.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),
+                                M, K, N, ws.data_ptr(), nbws, g.stream()), "lp_gemm_dev")
+
+    def gemv_only(i):
+        g.check(g.L.lp_gemm_q_dev(ws.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),
+                                  M, K, N, g.stream()), "lp_gemm_q_dev")
+
+    # eager reference result for the graph check
+    step(ncp - 1)
+    torch.cuda.synchronize()
+    y_eager = y.clone()
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(ncp):
+            step(i)
+    gk = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gk):
+        for i in range(ncp):
+            gemv_only(i)
+
+    reps = max(1, -(-steps // ncp))
+    wreps = max(1, -(-warmup // ncp))
+    for _ in range(wreps):
+        graph.replay()
+    torch.cuda.synchronize()
+    # every replay of the graph reproduces the eager result
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_eager), "graph replay differs from eager result"
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    nsteps = reps * ncp
+    ms_step = wall * 1e3 / nsteps
+
+    # GEMV kernel alone: HIP events on the launch stream around graph replays
+    for _ in range(wreps):
+        gk.replay()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        gk.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us_kernel = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+
+    return {
+        "type": TNAME[t], "N": N, "K": K, "M": M,
+        "alg_bytes": alg_bytes, "weight_bytes": int(w.nbytes),
+        "copies": ncp, "rotation_bytes": int(w.nbytes) * ncp,
+        "steps": nsteps, "ms_per_step": ms_step,
+        "gbs_step": alg_bytes / (ms_step * 1e-3) / 1e9,
+        "us_gemv": us_kernel,
+        "gbs_gemv": alg_bytes / (us_kernel * 1e-6) / 1e9,
+        "w_host": w, "x_host": x,
+    }
+
+
+def cpu_baseline(t, w, x, N, K, budget_s=12.0):
+    """Scalar fp32 path of the reference on the host, whole matrix."""
+    from oracle import oracle as orc
+    orc.build()
+    threads = min(16, os.cpu_count() or 1)
+    M = x.shape[0]
+    alg = w.nbytes + 4 * M * K + 4 * M * N
+    res = {}
+    for nth in (threads, 1):
+        times = []
+        t_end = time.perf_counter() + budget_s / 2
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+            t0 = time.perf_counter()
+            orc.gemm_scalar(t, x, w, N, nthreads=nth)
+            times.append(time.perf_counter() - t0)
+        res[nth] = (statistics.median(times), len(times))
+    med, runs = res[threads]
+    med1, runs1 = res[1]
+    return {
+        "value": alg / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{TNAME[t]} {N}x{K} M={M} whole matrix, gemm_scalar (src/matmul.cpp:320-334) "
+                  f"restated in oracle/lp_oracle.c, median of {runs} runs",
+        "value_1thread": alg / med1 / 1e9, "runs_1thread": runs1,
+    }
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run N torch device copies of 256 MiB (a copy kernel of known "
+                         "size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md for how the GEMV/GEMM/MoE would shard).", file=sys.stderr)
+        raise SystemExit(2)
+
+    g = Gpu()
+    if args.calib_copy_mib:
+        a = g.torch.empty(256 << 20, dtype=g.torch.uint8, device=g.dev)
+        b = g.torch.empty_like(a)
+        for _ in range(args.calib_copy_mib):
+            b.copy_(a)
+        g.torch.cuda.synchronize()
+        del a, b
+    t, N, K, M = Q4_K, 14336, 4096, 1
+    r = measure_gemv(g, t, N, K, M, args.steps, args.warmup)
+    name = "q4k_gemv_14336x4096_m1"
+    achieved = r["gbs_gemv"]
+    out = {
+        "metric": "Q4_K GEMV GB/s (% HBM peak) + prefill GEMM int8 TOPS (% MFMA peak)",
+        "value": round(r["gbs_step"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": r["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "Q4_K decode GEMV, W 14336x4096 (N x K), M=1, fp32 x quantized "
+                               "to 32-element int8 blocks in-step",
+                   "N": N, "K": K, "M": M, "weight_copies": r["copies"],
+                   "rotation_bytes": r["rotation_bytes"], "alg_bytes_per_step": r["alg_bytes"],
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(name),
+                     "kernel": "gemv_kernel<Q4_K,M=1>", "us_per_launch": round(r["us_gemv"], 3)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(t, r["w_host"], r["x_host"], N, K)
+    extra = []
+    if not args.no_extra:
+        cfgs = [(Q8_0, 4096, 4096, 1), (Q4_0, 14336, 4096, 1), (Q4_0, 4096, 14336, 1),
+                (Q4_K, 18944, 3584, 1), (Q4_K, 18944, 3584, 4), (Q4_K, 18944, 3584, 8),
+                (Q6_K, 3584, 18944, 1), (Q6_K, 3584, 18944, 4), (Q6_K, 3584, 18944, 8)]
+        for (tt, n, k, m) in cfgs:
+            e = measure_gemv(g, tt, n, k, m, max(64, args.steps // 4), 16)
+            extra.append({"workload": f"{TNAME[tt]} GEMV {n}x{k} M={m}",
+                          "gbs_step": round(e["gbs_step"], 1),
+                          "gbs_gemv": round(e["gbs_gemv"], 1),
+                          "hbm_frac_gemv": round(e["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                          "us_gemv": round(e["us_gemv"], 3)})
+            g.torch.cuda.empty_cache()
+    out["extra"] = extra
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -32,6 +32,12 @@ template <> struct Chunk<T_Q8_0> {
 #pragma unroll
         for (int i = 0; i < 17; i++) w.w[i] = __builtin_nontemporal_load(p + i);
     }
+    // row: LDS copy of the row, 4-byte aligned
+    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * c);
+#pragma unroll
+        for (int i = 0; i < 17; i++) w.w[i] = p[i];
+    }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s0 = 0, s1 = 0;
 #pragma unroll
@@ -64,6 +70,11 @@ template <> struct Chunk<T_Q4_0> {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 36 * c);
 #pragma unroll
         for (int i = 0; i < 9; i++) w.w[i] = __builtin_nontemporal_load(p + i);
+    }
+    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 36 * c);
+#pragma unroll
+        for (int i = 0; i < 9; i++) w.w[i] = p[i];
     }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s0 = 0, s1 = 0;
@@ -111,6 +122,14 @@ template <> struct Chunk<T_Q4_K> {
         w.h = ld_nt16(blk);
         w.q0 = ld_nt16(blk + 16 + 32 * jb);
         w.q1 = ld_nt16(blk + 32 + 32 * jb);
+    }
+    // row: LDS copy of the row, 16-byte aligned
+    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
+        const uint8_t* blk = row + 144 * (c >> 2);
+        const int jb = c & 3;
+        w.h = *reinterpret_cast<const u32x4*>(blk);
+        w.q0 = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * jb);
+        w.q1 = *reinterpret_cast<const u32x4*>(blk + 32 + 32 * jb);
     }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
@@ -162,6 +181,16 @@ template <> struct Chunk<T_Q6_K> {
         load_window<4>(blk + 128 + 32 * h + 16 * lr, w.qh);
         load_window<2>(blk + 192 + 8 * h, w.sc);
         w.d = load_u16(blk + 208);
+    }
+    // row: LDS copy of the row, 2-byte aligned
+    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
+        const uint8_t* blk = row + 210 * (c >> 2);
+        const int h = (c >> 1) & 1, lr = c & 1;
+        lds_window<4>(blk + 64 * h + 16 * lr, w.la);
+        lds_window<4>(blk + 64 * h + 32 + 16 * lr, w.lb);
+        lds_window<4>(blk + 128 + 32 * h + 16 * lr, w.qh);
+        lds_window<2>(blk + 192 + 8 * h, w.sc);
+        w.d = *reinterpret_cast<const uint16_t*>(blk + 208);
     }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s[4] = {0, 0, 0, 0};

@@ -74,6 +74,37 @@ __device__ __forceinline__ void load_window(const uint8_t* p, uint32_t (&out)[ND
     for (int i = 0; i < NDW; i++) out[i] = alignb(w[i + 1], w[i], sh);
 }
 
+// Same byte window read from LDS (p 2-byte aligned; NDW + 1 aligned dwords,
+// all inside the staged tile).
+template <int NDW>
+__device__ __forceinline__ void lds_window(const uint8_t* p, uint32_t (&out)[NDW]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = (uint32_t)(a & 3);
+    uint32_t w[NDW + 1];
+#pragma unroll
+    for (int i = 0; i <= NDW; i++) w[i] = base[i];
+#pragma unroll
+    for (int i = 0; i < NDW; i++) out[i] = alignb(w[i + 1], w[i], sh);
+}
+
+// Sum over groups of `lpr` consecutive lanes (lpr a power of two, 2..64)
+// with DPP lane moves; the group's sum lands in its last lane (lpr - 1).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_step(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                   0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+    v = dpp_step<0xb1, 0xf>(v);                 // quad_perm [1,0,3,2]
+    if (lpr > 2) v = dpp_step<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
+    if (lpr > 4) v = dpp_step<0x114, 0xf>(v);   // row_shr:4
+    if (lpr > 8) v = dpp_step<0x118, 0xf>(v);   // row_shr:8
+    if (lpr > 16) v = dpp_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    if (lpr > 32) v = dpp_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 // Two bytes at p (2-byte aligned) as a zero-extended u32.
 __device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);

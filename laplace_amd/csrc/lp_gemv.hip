@@ -91,109 +91,140 @@ hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipSt
 // ---------------------------------------------------------------------------
 // GEMV.
 //
-// Grid: each workgroup of WG = max(256, LPR) lanes holds SPW = WG / LPR row
-// slots. Slot s of workgroup b owns rows (b*SPW + s)*R + i*(gridDim*SPW*R)
-// + r for r < R, i = 0, 1, ...; every lane of the workgroup runs the same
-// number of iterations so the LDS barriers (LPR > 64) stay uniform.
+// One-shot tiles: workgroup b owns `tile_rows` consecutive weight rows (one
+// contiguous byte range) and requests all of it at once, so the whole
+// weight matrix is in flight at kernel start (33 MB fits the 256 CUs' LDS).
+// The tile is copied into LDS with global_load_lds_dwordx4: each wave moves
+// 1 KiB per instruction, lane i the 16 bytes at i*16, so every weight load
+// is a fully coalesced 1 KiB request (per-lane loads of the 144/210-byte
+// blocks at their natural offsets are scattered and were bound by the
+// texture-address unit). Each lane owns one 64-element chunk of K and keeps
+// its activation codes and scales in registers. The tile is decoded in
+// stages of one row per row slot while later pieces are still arriving;
+// partial sums are reduced with DPP, across waves through LDS, and y is
+// written at the end with coalesced stores.
 
-template <uint32_t T, int M, int R>
+constexpr int kPiece = 1024;   // bytes one wave moves per global_load_lds_dwordx4
+
+// s_waitcnt immediate for "at most n vector-memory ops outstanding" (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14); }
+
+// s_waitcnt with a run-time count (the instruction takes an immediate).
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+#define LP_W(i) case i: __builtin_amdgcn_s_waitcnt(waitcnt_vm(i)); break;
+        LP_W(1) LP_W(2) LP_W(3) LP_W(4) LP_W(5) LP_W(6) LP_W(7) LP_W(8)
+        LP_W(9) LP_W(10) LP_W(11) LP_W(12) LP_W(13) LP_W(14) LP_W(15) LP_W(16)
+        LP_W(17) LP_W(18) LP_W(19) LP_W(20) LP_W(21) LP_W(22) LP_W(23) LP_W(24)
+        LP_W(25) LP_W(26) LP_W(27) LP_W(28) LP_W(29) LP_W(30) LP_W(31) LP_W(32)
+#undef LP_W
+        default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+    }
+}
+
+// Stage s of a tile = rows [s*spw, (s+1)*spw): one row per row slot. The
+// tile's 1 KiB pieces are issued in byte order, piece p by wave p % nwaves,
+// all before any is consumed; before stage s a wave waits until only its
+// pieces that no stage <= s needs are still in flight, then the workgroup
+// synchronises and decodes the stage while later pieces keep arriving.
+template <uint32_t T, int M>
 __global__ void __launch_bounds__(512)
-gemv_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, float* __restrict__ y,
-            int K, int N, int lpr, int iters) {
+gemv_kernel(const uint8_t* __restrict__ w, size_t rb, size_t wbytes, ActView A,
+            float* __restrict__ y, int K, int N, int lpr, int tile_rows, int tile_cap) {
     using C = Chunk<T>;
-    extern __shared__ float red[];                      // [WG/64][R*M] when lpr > 64
-    const int tid = threadIdx.x;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwaves = blockDim.x >> 6;
     const int lane_in_row = tid & (lpr - 1);
     const int slot = tid / lpr;
     const int spw = blockDim.x / lpr;
-    const int nchunks = K >> 6;
-    const bool active = lane_in_row < nchunks;
-    const int c = active ? lane_in_row : 0;
+    const int nseg = lpr > 64 ? lpr >> 6 : 1;             // waves per row
+    // [tile | partial sums: tile_rows x nseg x M floats]
+    float* part_s = reinterpret_cast<float*>(smem + tile_cap);
 
+    // activations first: the tile copies must be the newest loads in flight
+    const int nchunks = K >> 6;
+    const float keep = lane_in_row < nchunks ? 1.0f : 0.0f;
+    const int c = lane_in_row < nchunks ? lane_in_row : nchunks - 1;
     typename C::Act act[M];
 #pragma unroll
     for (int m = 0; m < M; m++) load_act<T>(A, K, m, c, act[m]);
 
-    const long gstride = (long)gridDim.x * spw * R;
-    long row0 = ((long)blockIdx.x * spw + slot) * R;
-    for (int it = 0; it < iters; it++, row0 += gstride) {
-        typename C::Wt wt[R];
+    const long row_start = (long)blockIdx.x * tile_rows;
+    const uintptr_t gbeg = reinterpret_cast<uintptr_t>(w) + (uintptr_t)row_start * rb;
+    const uintptr_t g0 = gbeg & ~uintptr_t(15);
+    const int delta = (int)(gbeg - g0);
+    const uintptr_t glast = (reinterpret_cast<uintptr_t>(w) + wbytes - 1) & ~uintptr_t(15);
+    const int rows_here = (int)((long)N - row_start < tile_rows ? (long)N - row_start : tile_rows);
+    const int pieces = (delta + rows_here * (int)rb + kPiece - 1) / kPiece;
+    for (int p = wave; p < pieces; p += nwaves) {
+        uintptr_t ga = g0 + (uintptr_t)p * kPiece + (uintptr_t)lane * 16;
+        ga = ga > glast ? glast : ga;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ga),
+                                         (__attribute__((address_space(3))) void*)(smem + p * kPiece),
+                                         16, 0, 0);
+    }
+    const int mine = (pieces - wave + nwaves - 1) / nwaves;   // pieces this wave issued
+
+    const int wl = lpr < 64 ? lpr : 64;
+    const int nstages = tile_rows / spw;
+    for (int st = 0; st < nstages; st++) {
+        // pieces needed through this stage, then this wave's later ones
+        int need_rows = (st + 1) * spw;
+        need_rows = need_rows < rows_here ? need_rows : rows_here;
+        int need = (delta + need_rows * (int)rb + kPiece - 1) / kPiece;
+        need = need < pieces ? need : pieces;
+        const int done_mine = (need - wave + nwaves - 1) / nwaves;
+        wait_vm(mine - (done_mine > 0 ? done_mine : 0));
+        // plain s_barrier: __syncthreads' fence would wait for every copy
+        __builtin_amdgcn_s_barrier();
+        const int r = st * spw + slot;
+        typename C::Wt wt;
+        C::load_w_lds(smem + delta + (size_t)r * rb, c, wt);
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const long row = row0 + r;
-            if (active && row < N) C::load_w(w + row * rb, c, wt[r]);
+        for (int m = 0; m < M; m++) {
+            int is[C::NSUB];
+            C::isums(wt, act[m], is);
+            const float v = group_sum(keep * C::partial(wt, act[m], is, c), wl);
+            if (lane_in_row % 64 == wl - 1 || (lpr >= 64 && lane == 63))
+                part_s[(r * nseg + (lpr > 64 ? (tid % lpr) >> 6 : 0)) * M + m] = v;
         }
-        float part[R][M];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                float p = 0.0f;
-                if (active && row0 + r < N) {
-                    int is[C::NSUB];
-                    C::isums(wt[r], act[m], is);
-                    p = C::partial(wt[r], act[m], is, c);
-                }
-                part[r][m] = p;
-            }
-        }
-        // reduce over the lpr lanes of the row (within a wave first)
-        const int wl = lpr < 64 ? lpr : 64;
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int m = 0; m < M; m++)
-                for (int off = wl >> 1; off >= 1; off >>= 1)
-                    part[r][m] += __shfl_xor(part[r][m], off, 64);
-        if (lpr <= 64) {
-            if (lane_in_row == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    if (row0 + r < N)
-#pragma unroll
-                        for (int m = 0; m < M; m++) y[(size_t)m * N + row0 + r] = part[r][m];
-            }
-        } else {
-            const int wave = tid >> 6, nw = lpr >> 6;
-            if ((tid & 63) == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++)
-#pragma unroll
-                    for (int m = 0; m < M; m++) red[wave * R * M + r * M + m] = part[r][m];
-            }
-            __syncthreads();
-            // one lane per (r, m) of this slot's first wave finishes the sum
-            const int first = slot * nw;
-            if (wave == first && (tid & 63) < R * M) {
-                const int rm = tid & 63;
-                float s = 0.0f;
-                for (int i = 0; i < nw; i++) s += red[(first + i) * R * M + rm];
-                const int r = rm / M, m = rm % M;
-                if (row0 + r < N) y[(size_t)m * N + row0 + r] = s;
-            }
-            __syncthreads();
-        }
+    }
+    __syncthreads();
+    // y: one thread per (row, m), rows contiguous
+    for (int i = tid; i < rows_here * M; i += blockDim.x) {
+        const int m = i / rows_here, r = i - m * rows_here;
+        float s = 0.0f;
+        for (int g = 0; g < nseg; g++) s += part_s[(r * nseg + g) * M + m];
+        y[(size_t)m * N + row_start + r] = s;
     }
 }
 
-template <uint32_t T, int M, int R>
+// tile_bytes: LDS bytes for the weight tile (0 = default).
+template <uint32_t T, int M>
 static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, int K, int N,
-                                hipStream_t st) {
+                                hipStream_t st, int tile_bytes = 0) {
     const int nchunks = K >> 6;
-    int lpr = 1;
+    int lpr = 2;
     while (lpr < nchunks) lpr <<= 1;
     if (lpr > 512) return hipErrorInvalidValue;   // K > 32768: not handled here
     const int wg = lpr > 256 ? lpr : 256;
     const int spw = wg / lpr;
-    const long groups = ((long)N + R - 1) / R;           // R-row groups
-    long want = (groups + spw - 1) / spw;                // workgroups for one pass
-    const long cap = (long)device_cu_count() * (2048 / wg);   // ~8 waves per CU resident
-    const long grid = want < cap ? want : cap;
-    const int iters = (int)((groups + grid * spw - 1) / (grid * spw));
     const size_t rb = row_bytes(T, K);
-    const size_t shm = lpr > 64 ? sizeof(float) * (wg / 64) * R * M : 0;
-    hipLaunchKernelGGL((gemv_kernel<T, M, R>), dim3((unsigned)grid), dim3(wg), shm, st,
-                       w, rb, A, y, K, N, lpr, iters);
+    if (tile_bytes <= 0) tile_bytes = 24576;
+    int tile_rows = (int)((tile_bytes - 15) / rb) / spw * spw;
+    if (tile_rows < spw) tile_rows = spw;
+    if (tile_rows > N) tile_rows = (N + spw - 1) / spw * spw;
+    const int tile_cap = (int)((tile_rows * rb + 15 + kPiece - 1) / kPiece * kPiece);
+    const int pieces_per_wave = (tile_cap / kPiece + wg / 64 - 1) / (wg / 64);
+    if (pieces_per_wave > 32) return hipErrorInvalidValue;
+    const int nseg = lpr > 64 ? lpr / 64 : 1;
+    const size_t shm = tile_cap + sizeof(float) * (size_t)tile_rows * nseg * M;
+    if (shm > 160 * 1024) return hipErrorInvalidValue;
+    const long grid = ((long)N + tile_rows - 1) / tile_rows;
+    hipLaunchKernelGGL((gemv_kernel<T, M>), dim3((unsigned)grid), dim3(wg), shm, st,
+                       w, rb, rb * (size_t)N, A, y, K, N, lpr, tile_rows, tile_cap);
     return hipGetLastError();
 }
 
@@ -201,14 +232,14 @@ template <uint32_t T>
 static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y, int M, int K,
                                    int N, hipStream_t st) {
     switch (M) {
-        case 1: return launch_gemv_t<T, 1, 4>(w, A, y, K, N, st);
-        case 2: return launch_gemv_t<T, 2, 4>(w, A, y, K, N, st);
-        case 3: return launch_gemv_t<T, 3, 2>(w, A, y, K, N, st);
-        case 4: return launch_gemv_t<T, 4, 2>(w, A, y, K, N, st);
-        case 5: return launch_gemv_t<T, 5, 2>(w, A, y, K, N, st);
-        case 6: return launch_gemv_t<T, 6, 2>(w, A, y, K, N, st);
-        case 7: return launch_gemv_t<T, 7, 1>(w, A, y, K, N, st);
-        case 8: return launch_gemv_t<T, 8, 1>(w, A, y, K, N, st);
+        case 1: return launch_gemv_t<T, 1>(w, A, y, K, N, st);
+        case 2: return launch_gemv_t<T, 2>(w, A, y, K, N, st);
+        case 3: return launch_gemv_t<T, 3>(w, A, y, K, N, st);
+        case 4: return launch_gemv_t<T, 4>(w, A, y, K, N, st);
+        case 5: return launch_gemv_t<T, 5>(w, A, y, K, N, st);
+        case 6: return launch_gemv_t<T, 6>(w, A, y, K, N, st);
+        case 7: return launch_gemv_t<T, 7>(w, A, y, K, N, st);
+        case 8: return launch_gemv_t<T, 8>(w, A, y, K, N, st);
         default: return hipErrorInvalidValue;
     }
 }
