@@ -198,6 +198,55 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
     }
 
 
+def measure_gemm(g: Gpu, N, K, M, reps=20, copies=2, seed=0):
+    """Prefill GEMM (Q4_K, M tokens): one step = quantize x + fp16 planes +
+    MFMA GEMM. Timed with HIP events over graph replays on the launch stream.
+    Weight copies rotate (the weights are re-read per token tile anyway)."""
+    torch = g.torch
+    t = Q4_K
+    w = synth_weights(t, K, N, seed=seed + N + K)
+    x = synth_x(M, K, seed=seed + 2, outliers=0.01)
+    ws_list = g.copies(w, min_bytes=0, min_copies=copies)
+    ncp = len(ws_list)
+    xd = torch.from_numpy(x).to(g.dev)
+    y = torch.empty(M * N, dtype=torch.float32, device=g.dev)
+    nbws = int(g.L.lp_act_workspace_bytes(M, K))
+    ws = torch.empty(nbws, dtype=torch.uint8, device=g.dev)
+
+    def step(i):
+        g.check(g.L.lp_gemm_dev(xd.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),
+                                M, K, N, ws.data_ptr(), nbws, g.stream()), "lp_gemm_dev")
+
+    step(0)
+    torch.cuda.synchronize()
+    y0 = y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(1)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(ncp):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0) or ncp > 1, "graph replay differs from eager result"
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+    ops = 2.0 * M * N * K
+    return {"workload": f"Q4_K prefill GEMM N={N} K={K} M={M}", "us_step": round(us, 2),
+            "tops": round(ops / (us * 1e-6) / 1e12, 1),
+            "frac_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)}
+
+
 def cpu_baseline(t, w, x, N, K, budget_s=12.0):
     """Scalar fp32 path of the reference on the host, whole matrix."""
     from oracle import oracle as orc
@@ -239,6 +288,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM lines")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run N torch device copies of 256 MiB (a copy kernel of known "
                          "size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -299,6 +349,19 @@ def main():
                           "us_gemv": round(e["us_gemv"], 3)})
             g.torch.cuda.empty_cache()
     out["extra"] = extra
+    gemms = []
+    if not args.no_gemm:
+        for (n, k, m) in [(14336, 4096, 2048), (14336, 4096, 512), (4096, 4096, 2048), (4096, 4096, 512)]:
+            gemms.append(measure_gemm(g, n, k, m))
+            g.torch.cuda.empty_cache()
+        head = gemms[0]
+        out["gemm"] = {"metric": "prefill GEMM int8-equivalent TOPS (2*M*N*K / step time)",
+                       "value": head["tops"], "unit": "TOPS", "workload": head["workload"],
+                       "us_per_step": head["us_step"],
+                       "roofline": {"bound": "mfma", "achieved": head["tops"],
+                                    "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                                    "frac": head["frac_int8_peak"], "traffic": None},
+                       "all": gemms}
     print(json.dumps(out))
 
 

@@ -78,9 +78,18 @@ int device_cu_count() {
 
 static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
 
-static size_t ws_bytes(int M, int K) {
+static size_t act_bytes(int M, int K) {
     const size_t nbk = (size_t)M * (K / 32);
     return up256((size_t)M * K) + 3 * up256(nbk * 4);
+}
+
+// Activation blocks, plus the prefill GEMM's fp16 planes when M > 8.
+static size_t ws_bytes(int M, int K) {
+    return act_bytes(M, K) + (M > 8 ? gemm_planes_bytes(M, K) : 0);
+}
+
+static void* ws_planes(void* ws, int M, int K) {
+    return static_cast<uint8_t*>(ws) + act_bytes(M, K);
 }
 
 static ActView ws_view(void* ws, int M, int K) {
@@ -126,8 +135,12 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
     return LP_OK;
 }
 
-static int gemm_q(const ActView& A, const uint8_t* w, uint32_t type, float* y, int M, int K,
-                  int N, hipStream_t st) {
+static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t type, float* y,
+                  int M, int K, int N, hipStream_t st) {
+    if (planes && gemm_supported(type, M, K)) {
+        LP_HIP(launch_gemm(type, w, A, planes, y, M, K, N, st));
+        return LP_OK;
+    }
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mt = M - m0 < 8 ? M - m0 : 8;
         ActView sub;
@@ -259,7 +272,8 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
     const ActView A = ws_view(c->ws, M, K);
     LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
-    if ((rc = gemm_q(A, wd, type, c->yd, M, K, N, c->stream)) != LP_OK) return rc;
+    if ((rc = gemm_q(A, ws_planes(c->ws, M, K), wd, type, c->yd, M, K, N, c->stream)) != LP_OK)
+        return rc;
     LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
     LP_HIP(hipStreamSynchronize(c->stream));
     std::memcpy(y, c->y_pin, yb);
@@ -404,8 +418,8 @@ int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int
                   void* stream) {
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
-    return gemm_q(ws_view(const_cast<void*>(ws), M, K), w, type, y, M, K, N,
-                  static_cast<hipStream_t>(stream));
+    return gemm_q(ws_view(const_cast<void*>(ws), M, K), ws_planes(const_cast<void*>(ws), M, K), w,
+                  type, y, M, K, N, static_cast<hipStream_t>(stream));
 }
 
 int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,

@@ -29,6 +29,12 @@ int device_cu_count();
 hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st);
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
                        int N, hipStream_t st);
+// Prefill GEMM (lp_gemm.hip): Q4_K weights, M > 8. `planes` is scratch of
+// gemm_planes_bytes(M, K) bytes (fp16 activation planes).
+bool gemm_supported(uint32_t type, int M, int K);
+size_t gemm_planes_bytes(int M, int K);
+hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
+                       int M, int K, int N, hipStream_t st);
 hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, int32_t* out,
                              int M, int K, int N, hipStream_t st);
 

@@ -215,3 +215,54 @@ def test_unsupported_type_is_reported():
     y = np.zeros(1, np.float32)
     ok = _lib.lib().lp_gemm(x.ctypes.data, w.ctypes.data, 1, y.ctypes.data, 1, 256, 1)  # F16
     assert ok is False
+
+
+# ---------------------------------------------------------------------------
+# prefill GEMM (Q4_K, M > 8): MFMA path against the oracle's gemm_int
+
+
+GEMM_SHAPES = [(512, 256, 9), (512, 300, 33), (512, 256, 130), (2816, 300, 65), (4096, 512, 257)]
+
+
+@pytest.mark.parametrize("K,N,M", GEMM_SHAPES, ids=lambda v: str(v))
+def test_gemm_q4k_small(orc, K, N, M):
+    _flush(f"gemm Q4_K K={K} N={N} M={M}")
+    w = synth_weights(Q4_K, K, N, seed=K + N)
+    x = synth_x(M, K, seed=M, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    ref = orc.gemm_int(Q4_K, x, w, N)
+    err = normwise(y, ref)
+    assert err <= TOL, f"normwise {err:.3g}"
+
+
+@pytest.mark.parametrize("N,M", [(4096, 512), (4096, 2048), (14336, 512), (14336, 2048)],
+                         ids=lambda v: str(v))
+def test_gemm_q4k_prefill_configs(orc, N, M):
+    """BASELINE.json config 4 at full size (x N(0,1) with 1% outliers x20):
+    the GPU computes the whole [M, N]; the oracle checks 48 sampled tokens
+    x 96 sampled rows (outputs are independent)."""
+    K = 4096
+    _flush(f"gemm prefill N={N} M={M}")
+    w = synth_weights(Q4_K, K, N, seed=N)
+    x = synth_x(M, K, seed=M + 1, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    assert np.isfinite(y).all()
+    rng = np.random.default_rng(M + N)
+    toks = np.sort(rng.choice(M, 48, replace=False))
+    rows = np.sort(rng.choice(N, 96, replace=False))
+    rb = len(w) // N
+    ws = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    ref = orc.gemm_int(Q4_K, x[toks], ws, len(rows))
+    err = normwise(y[np.ix_(toks, rows)], ref)
+    assert err <= TOL, f"normwise {err:.3g}"
+
+
+def test_gemm_matches_gemv_rows(orc):
+    """The MFMA GEMM (M = 16) and the GEMV (M = 8, twice) agree per row."""
+    _flush("gemm vs gemv")
+    K, N = 4096, 768
+    w = synth_weights(Q4_K, K, N, seed=5)
+    x = synth_x(16, K, seed=6, outliers=0.01)
+    yg = gemm_dev(Q4_K, x, w, N)
+    yv = np.concatenate([gemm_dev(Q4_K, x[:8], w, N), gemm_dev(Q4_K, x[8:], w, N)])
+    assert normwise(yg, yv) <= TOL
