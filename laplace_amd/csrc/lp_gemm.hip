@@ -96,7 +96,8 @@ constexpr int STAGE = 2 * A_PLANE + B_TILE;   // 40 KB
 constexpr int HDR = BN * 16;                  // 4 KB super-block headers
 constexpr int XS = BM * 16;                   // 2 KB per xs plane
 constexpr int SB_STAGE = HDR + 2 * XS;        // 8 KB
-constexpr int GEMM_LDS = 2 * STAGE + 2 * SB_STAGE;   // 96 KB
+constexpr int NSTAGE = 3;                     // K-step buffers in flight
+constexpr int GEMM_LDS = NSTAGE * STAGE + 2 * SB_STAGE;   // 136 KB
 
 __device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -114,59 +115,81 @@ struct GemmArgs {
     int M, N, K;
 };
 
-// Copies for K step kt of tile (m0, n0) into stage buffer `st` (and, at a
-// super-block start, its headers and activation sums into `sbb`). Returns
-// the number of DMA instructions this wave issued.
-__device__ __forceinline__ int issue_kstep(const GemmArgs& g, int m0, int n0, int kt, uint8_t* st,
-                                           uint8_t* sbb, int wave, int lane) {
-    const int k0 = kt * BK;
-    const int sb = kt >> 2, jb = kt & 3;
-    int n = 0;
-    // activation planes: 16 instructions each, 8 rows x 128 B per instruction,
-    // 16-byte pieces XOR-swizzled by (row & 7)
+// LDS layouts (per stage):
+//   activation plane: row r (token) at r*128, its eight 16-byte pieces
+//     stored at slot piece ^ ((r >> 1) & 7) - any 16 consecutive rows read
+//     the same piece from 16 distinct 16-byte bank groups;
+//   weight codes: 32-row groups of 1 KiB, [half 0: 32 x 16 B][half 1: 32 x 16 B].
+__device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 7; }
+
+// Per-lane source offsets of this wave's copies, fixed for the whole tile;
+// a K step only adds a wave-uniform offset.
+struct DmaPlan {
+    uint32_t a_off[4];      // element offset into the hi or lo plane
+    const _Float16* a_plane[4];
+    uint32_t a_lds[4];      // LDS byte offset inside a stage
+    const uint8_t* b_src;   // weight codes: row base + 16 + 16 * half
+    const uint8_t* sb_src;  // header row base (waves 0-3) or xs row base (waves 4-7)
+    uint32_t sb_lds;
+};
+
+__device__ __forceinline__ DmaPlan make_plan(const GemmArgs& g, int m0, int n0, int wave, int lane) {
+    DmaPlan d;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int p = wave * 4 + i;                  // 0..31
+        const int p = wave * 4 + i;                   // 0..31: 16 per plane
         const int plane = p >> 4, pp = p & 15;
         const int row = pp * 8 + (lane >> 3);
-        const int piece = (lane & 7) ^ (row & 7);
+        const int piece = (lane & 7) ^ a_swz(row);
         int gm = m0 + row;
         gm = gm < g.M ? gm : g.M - 1;
-        const _Float16* src = (plane ? g.lo : g.hi) + (size_t)gm * g.K + k0 + piece * 8;
-        dma16(src, st + plane * A_PLANE + pp * 1024);
-        n++;
+        d.a_off[i] = (uint32_t)gm * (uint32_t)g.K + (uint32_t)piece * 8;
+        d.a_plane[i] = plane ? g.lo : g.hi;
+        d.a_lds[i] = plane * A_PLANE + pp * 1024;
     }
-    // weight codes: 32 rows x 32 B per instruction
     {
-        const int row = wave * 32 + (lane >> 1);
-        int gn = n0 + row;
+        int gn = n0 + wave * 32 + (lane & 31);
         gn = gn < g.N ? gn : g.N - 1;
-        const uint8_t* src = g.w + (size_t)gn * g.rb + (size_t)sb * 144 + 16 + 32 * jb + 16 * (lane & 1);
-        dma16(src, st + 2 * A_PLANE + wave * 1024);
-        n++;
+        d.b_src = g.w + (size_t)gn * g.rb + 16 + 16 * (lane >> 5);
     }
+    if (wave < 4) {
+        int gn = n0 + wave * 64 + lane;
+        gn = gn < g.N ? gn : g.N - 1;
+        d.sb_src = g.w + (size_t)gn * g.rb;
+        d.sb_lds = wave * 1024;
+    } else {
+        const int plane = (wave - 4) >> 1, part = (wave - 4) & 1;
+        int gm = m0 + part * 64 + lane;
+        gm = gm < g.M ? gm : g.M - 1;
+        d.sb_src = reinterpret_cast<const uint8_t*>((plane ? g.slo : g.shi) + (size_t)gm * (g.K >> 5));
+        d.sb_lds = HDR + plane * XS + part * 1024;
+    }
+    return d;
+}
+
+// Copies of K step kt into stage `st` (+ super-block data into `sbb` when
+// kt starts a super-block). Returns the number of DMA instructions issued.
+__device__ __forceinline__ int issue_kstep(const DmaPlan& d, int wave, int kt, uint8_t* st,
+                                           uint8_t* sbb) {
+    const int sb = kt >> 2, jb = kt & 3;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(d.a_plane[i] + d.a_off[i] + kt * BK, st + d.a_lds[i]);
+    dma16(d.b_src + sb * 144 + 32 * jb, st + 2 * A_PLANE + wave * 1024);
     if (jb == 0) {
-        if (wave < 4) {                              // headers: 64 rows x 16 B
-            int gn = n0 + wave * 64 + lane;
-            gn = gn < g.N ? gn : g.N - 1;
-            dma16(g.w + (size_t)gn * g.rb + (size_t)sb * 144, sbb + wave * 1024);
-        } else {                                     // xs hi/lo: 64 tokens x 16 B
-            const int plane = (wave - 4) >> 1, part = (wave - 4) & 1;
-            int gm = m0 + part * 64 + lane;
-            gm = gm < g.M ? gm : g.M - 1;
-            const _Float16* src = (plane ? g.slo : g.shi) + (size_t)gm * (g.K >> 5) + sb * 8;
-            dma16(src, sbb + HDR + plane * XS + part * 1024);
-        }
-        n++;
+        dma16(d.sb_src + (wave < 4 ? sb * 144 : sb * 16), sbb + d.sb_lds);
+        return 6;
     }
-    return n;
+    return 5;
 }
 
 __device__ __forceinline__ void wait_dma(int outstanding) {
     // gfx9 s_waitcnt: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
-    if (outstanding >= 6) __builtin_amdgcn_s_waitcnt(6 | (7 << 4) | (15 << 8));
-    else if (outstanding == 5) __builtin_amdgcn_s_waitcnt(5 | (7 << 4) | (15 << 8));
-    else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+    switch (outstanding) {
+#define LP_W(i) case i: __builtin_amdgcn_s_waitcnt(((i) & 15) | (7 << 4) | (15 << 8) | (((i) >> 4) << 14)); break;
+        LP_W(5) LP_W(6) LP_W(10) LP_W(11) LP_W(12)
+#undef LP_W
+        default: __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); break;
+    }
 }
 
 __device__ __forceinline__ uint32_t pick2(uint32_t u, int a) {
@@ -190,6 +213,79 @@ __device__ __forceinline__ h8 decode_v(uint32_t u0, uint32_t u1, bool hi_nib, h2
     return out;
 }
 
+// LDS reads are issued as inline assembly with explicit lgkmcnt waits. A
+// compiler-generated ds_read after direct-to-LDS copies makes the compiler
+// wait for every outstanding copy (vmcnt(0)), including the prefetches of
+// later K steps, which serialises the copy pipeline; the copies a read
+// depends on are instead waited for explicitly (wait_dma + s_barrier).
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
+}
+template <int OFF>
+__device__ __forceinline__ void lds_rd128(h8& out, uint32_t a) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(out) : "v"(a), "n"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void lds_rd128u(u32x4& out, uint32_t a) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(out) : "v"(a), "n"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void lds_rd64(uint2& out, uint32_t a) {
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(out) : "v"(a), "n"(OFF));
+}
+
+// Operands of one K=16 sub-step: activation hi/lo fragments of the wave's two
+// token tiles and the 4-bit codes of its two weight-row tiles.
+struct SubOps {
+    h8 ahi[2], alo[2];
+    uint2 u[2];
+};
+
+__device__ __forceinline__ void wait_sub(SubOps& o) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.ahi[0]), "+v"(o.ahi[1]), "+v"(o.alo[0]), "+v"(o.alo[1]), "+v"(o.u[0]), "+v"(o.u[1]));
+}
+
+// a_base[tt]: LDS address of token row (wm*64 + tt*32 + lane%32) in stage 0;
+// a_x: the row's swizzle; b_base: code address of (tile 0, half 0) in stage 0.
+template <int S>
+__device__ __forceinline__ void read_sub(SubOps& o, uint32_t stage_off, const uint32_t a_base[2], const int a_x[2],
+                                         uint32_t b_base) {
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        // piece (2S + lane/32) ^ swz: the lane/32 term is folded into a_x
+        const uint32_t a = a_base[tt] + stage_off + (uint32_t)(((2 * S) ^ a_x[tt]) * 16);
+        lds_rd128<0>(o.ahi[tt], a);
+        lds_rd128<A_PLANE>(o.alo[tt], a);
+    }
+    const uint32_t b = b_base + stage_off + (S & 1) * 512;
+    lds_rd64<0>(o.u[0], b);
+    lds_rd64<1024>(o.u[1], b);
+}
+
+__device__ __forceinline__ void scale_pair(uint32_t hy, uint32_t hw, int j, h2& mul, h2& add) {
+    uint32_t sc;
+    if (j < 4) sc = __builtin_amdgcn_ubfe(hy, 8 * j, 6);
+    else sc = __builtin_amdgcn_ubfe(hw, 8 * (j - 4), 4) | (__builtin_amdgcn_ubfe(hy, 8 * (j - 4) + 6, 2) << 4);
+    // even blocks use low nibbles (1024 + n), odd high (1024 + 16n)
+    const float s = (j & 1) ? (float)sc * 0.0625f : (float)sc;
+    const _Float16 h = (_Float16)s, a = (_Float16)(-1024.0f * s);
+    mul = h2{h, h};
+    add = h2{a, a};
+}
+
+__device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
+    h8 mm;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t mn;
+        if (j < 4) mn = __builtin_amdgcn_ubfe(hz, 8 * j, 6);
+        else mn = __builtin_amdgcn_ubfe(hw, 8 * (j - 4) + 4, 4) | (__builtin_amdgcn_ubfe(hz, 8 * (j - 4) + 6, 2) << 4);
+        mm[j] = (_Float16)(float)mn;
+    }
+    return mm;
+}
+
 __global__ void __launch_bounds__(kGemmThreads)
 gemm_q4k_kernel(GemmArgs g, int ntn) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -199,8 +295,22 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
     const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * BN;
     // stage buffer i at smem + i * STAGE; super-block buffer i after them
     auto stage = [&](int i) { return smem + i * STAGE; };
-    auto sbuf = [&](int i) { return smem + 2 * STAGE + i * SB_STAGE; };
+    auto sbuf = [&](int i) { return smem + NSTAGE * STAGE + i * SB_STAGE; };
     const int nk = g.K / BK;
+    const DmaPlan plan = make_plan(g, m0, n0, wave, lane);
+
+    const uint32_t lds0 = lds_addr(smem);
+    uint32_t a_base[2];
+    int a_x[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        const int row = wm * 64 + tt * 32 + (lane & 31);
+        a_base[tt] = lds0 + row * 128;
+        a_x[tt] = (lane >> 5) ^ a_swz(row);
+    }
+    const uint32_t b_base = lds0 + 2 * A_PLANE + (wn * 2) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
+    const uint32_t hdr_base = lds0 + NSTAGE * STAGE + (wn * 64 + (lane & 31)) * 16;
+    const uint32_t xs_base = lds0 + NSTAGE * STAGE + HDR + (wm * 64 + (lane & 31)) * 16;
 
     f16v acc[2][2], main_[2][2];
 #pragma unroll
@@ -208,109 +318,117 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
         for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) { acc[a][b][r] = 0.0f; main_[a][b][r] = 0.0f; }
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+    const f16v zero = {};
 
-    // per super-block weight scales of this lane's two weight rows
-    h2 vmul[2][8], vadd[2][8];
-    h8 bmin[2];
+    // header words of the lane's two weight rows for the current super-block
+    uint32_t hy[2], hz[2], hw[2];
     float dsc[2], dmn[2];
 
-    (void)issue_kstep(g, m0, n0, 0, stage(0), sbuf(0), wave, lane);
+    // steps kt+1 and kt+2 are in flight while step kt is computed
+    int cnt_next = 0;                                 // DMA count of step kt+1
+    (void)issue_kstep(plan, wave, 0, stage(0), sbuf(0));
+    if (nk > 1) cnt_next = issue_kstep(plan, wave, 1, stage(1), sbuf(0));
     const int nsb = nk >> 2;
     for (int sb = 0; sb < nsb; sb++) {
+        const uint32_t sb_off = (uint32_t)((sb & 1) * SB_STAGE);
         // jb unrolled so every register-array index below is a constant
 #pragma unroll
         for (int jb = 0; jb < 4; jb++) {
-        const int kt = 4 * sb + jb;
-        int nnext = 0;
-        if (kt + 1 < nk)
-            nnext = issue_kstep(g, m0, n0, kt + 1, stage((jb + 1) & 1), sbuf(((kt + 1) >> 2) & 1), wave, lane);
-        wait_dma(nnext);
-        __builtin_amdgcn_s_barrier();
-        const uint8_t* st = stage(jb & 1);
-        const uint8_t* sbb = sbuf(sb & 1);
-        if (jb == 0) {
-            // decode the two weight rows' headers: d, dmin, 8 x (sc, m)
-#pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
-                const int row = wn * 64 + ct * 32 + (lane & 31);
-                const u32x4 h = *reinterpret_cast<const u32x4*>(sbb + row * 16);
-                dsc[ct] = fp16_bits_to_f32(h.x);
-                dmn[ct] = fp16_bits_to_f32(h.x >> 16);
-                h8 mm;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    uint32_t sc, mn;
-                    if (j < 4) {
-                        sc = __builtin_amdgcn_ubfe(h.y, 8 * j, 6);
-                        mn = __builtin_amdgcn_ubfe(h.z, 8 * j, 6);
-                    } else {
-                        sc = __builtin_amdgcn_ubfe(h.w, 8 * (j - 4), 4) | (__builtin_amdgcn_ubfe(h.y, 8 * (j - 4) + 6, 2) << 4);
-                        mn = __builtin_amdgcn_ubfe(h.w, 8 * (j - 4) + 4, 4) | (__builtin_amdgcn_ubfe(h.z, 8 * (j - 4) + 6, 2) << 4);
-                    }
-                    // even blocks use low nibbles (1024 + n), odd high (1024 + 16n)
-                    const _Float16 s = (j & 1) ? (_Float16)((float)sc * 0.0625f) : (_Float16)(float)sc;
-                    vmul[ct][j] = h2{s, s};
-                    vadd[ct][j] = h2{(_Float16)(-1024.0f) * s, (_Float16)(-1024.0f) * s};
-                    mm[j] = (_Float16)(float)mn;
-                }
-                // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
-                bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-        }
+            const int kt = 4 * sb + jb;
+            wait_dma(cnt_next);                         // step kt has landed
+            // after this barrier every wave has finished step kt-1, whose
+            // stage buffer is the one step kt+2 is copied into
+            __builtin_amdgcn_s_barrier();
+            cnt_next = 0;
+            if (kt + 2 < nk)
+                cnt_next = issue_kstep(plan, wave, kt + 2, stage((kt + 2) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
+            const uint32_t st_off = (uint32_t)((kt % NSTAGE) * STAGE);
 
-        // four K=16 sub-steps
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            h8 ahi[2], alo[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                const int row = wm * 64 + tt * 32 + (lane & 31);
-                const int piece = (2 * s + (lane >> 5)) ^ (row & 7);
-                ahi[tt] = *reinterpret_cast<const h8*>(st + row * 128 + piece * 16);
-                alo[tt] = *reinterpret_cast<const h8*>(st + A_PLANE + row * 128 + piece * 16);
-            }
-            const int blk = 2 * jb + (s >> 1);          // block within the super-block
-            const bool hi_nib = (s >> 1) != 0;
-            const int half = s & 1;
-#pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
-                const int row = wn * 64 + ct * 32 + (lane & 31);
-                const uint2 u = *reinterpret_cast<const uint2*>(st + 2 * A_PLANE + row * 32 + 16 * half + 8 * (lane >> 5));
-                const h8 v = decode_v(u.x, u.y, hi_nib, vmul[ct][blk], vadd[ct][blk]);
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
-                    main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[tt], v, main_[tt][ct], 0, 0, 0);
-                    main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[tt], v, main_[tt][ct], 0, 0, 0);
-                }
-            }
-        }
-
-        if (jb == 3) {
-            // min term of this super-block and the per-super-block epilogue
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                const int tok = wm * 64 + tt * 32 + (lane & 31);
-                h8 shv = *reinterpret_cast<const h8*>(sbb + HDR + tok * 16);
-                h8 slv = *reinterpret_cast<const h8*>(sbb + HDR + XS + tok * 16);
-                if (lane >= 32) { shv = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv = shv; }
+            if (jb == 0) {
+                u32x4 h[2];
+                lds_rd128u<0>(h[0], hdr_base + sb_off);
+                lds_rd128u<512>(h[1], hdr_base + sb_off);
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(h[0]), "+v"(h[1]));
 #pragma unroll
                 for (int ct = 0; ct < 2; ct++) {
-                    f16v mn = {0};
-                    mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv, bmin[ct], mn, 0, 0, 0);
-                    mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv, bmin[ct], mn, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
-                        acc[tt][ct][r] = fmaf(-dmn[ct], mn[r], acc[tt][ct][r]);
-                        main_[tt][ct][r] = 0.0f;
-                    }
+                    dsc[ct] = fp16_bits_to_f32(h[ct].x);
+                    dmn[ct] = fp16_bits_to_f32(h[ct].x >> 16);
+                    hy[ct] = h[ct].y;
+                    hz[ct] = h[ct].z;
+                    hw[ct] = h[ct].w;
                 }
             }
-        }
-        // every wave is done reading this stage before it is refilled
-        __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
+            h2 vmul[2][2], vadd[2][2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) scale_pair(hy[ct], hw[ct], 2 * jb + i, vmul[ct][i], vadd[ct][i]);
+
+            // four K=16 sub-steps; operands of sub-step s+1 are read while
+            // sub-step s computes. The hi and lo MFMAs of one tile are four
+            // instructions apart (no back-to-back accumulator dependency).
+            SubOps ops[2];
+            read_sub<0>(ops[0], st_off, a_base, a_x, b_base);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                SubOps& o = ops[s & 1];
+                wait_sub(o);
+                if (s == 0) read_sub<1>(ops[1], st_off, a_base, a_x, b_base);
+                if (s == 1) read_sub<2>(ops[0], st_off, a_base, a_x, b_base);
+                if (s == 2) read_sub<3>(ops[1], st_off, a_base, a_x, b_base);
+                const bool hi_nib = (s >> 1) != 0;
+                h8 v[2];
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) v[ct] = decode_v(o.u[ct].x, o.u[ct].y, hi_nib, vmul[ct][s >> 1], vadd[ct][s >> 1]);
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++)
+                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            o.ahi[tt], v[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++)
+                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.alo[tt], v[ct], main_[tt][ct], 0, 0, 0);
+            }
+
+            if (jb == 3) {
+                // min term of this super-block and the per-super-block epilogue
+                h8 shv[2], slv[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    lds_rd128<0>(shv[tt], xs_base + sb_off + tt * 512);
+                    lds_rd128<XS>(slv[tt], xs_base + sb_off + tt * 512);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(shv[0]), "+v"(shv[1]), "+v"(slv[0]), "+v"(slv[1]));
+                h8 bmin[2];
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
+                    const h8 mm = min_codes(hy[ct], hz[ct], hw[ct]);
+                    bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    if (lane >= 32) { shv[tt] = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv[tt] = shv[tt]; }
+                    f16v mn[2];
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++)
+                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin[ct], zero, 0, 0, 0);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++)
+                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin[ct], mn[ct], 0, 0, 0);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
+                            acc[tt][ct][r] = fmaf(-dmn[ct], mn[ct][r], acc[tt][ct][r]);
+                        }
+                }
+            }
         }
     }
 
