@@ -113,6 +113,32 @@ int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int
 int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M,
                       int K, int N, void* stream);
 
+/* ---- 3. grouped MoE dispatch ---------------------------------------------- */
+
+/* The MoE layer of T tokens, each routed to topk experts of a stacked weight
+ * tensor w = n_experts x (N rows of K elements of `type`). Pair
+ * p = t*topk + j uses expert topk_idx[p] and writes y[p*N .. p*N + N):
+ *   multi == 0: y[p*N + n] = dot(x[t*K ..], W_{topk_idx[p]} row n)     (x is T x K)
+ *   multi != 0: y[p*N + n] = dot(x[p*K ..], W_{topk_idx[p]} row n)     (x is T*topk x K)
+ * Each pair's result equals the reference's per-token call for that token:
+ * fused_moe_gemm_idx / fused_moe_gemm_multi (src/matmul.cpp:456-500, called
+ * per token from src/arch_gemma4.cpp:604 and :626), i.e. moe_gemv_int /
+ * moe_gemv_multi_int (src/matmul_simd.cpp:506-544). Pairs are grouped by
+ * expert on the device so an expert's weights are streamed once per group
+ * instead of once per pair. No reference counterpart as a single entry: the
+ * reference loops over tokens. */
+size_t lp_moe_workspace_bytes(int T, int topk, int n_experts, int K, int multi);
+
+/* Device pointers, stream-ordered. Indices outside [0, n_experts) are
+ * dropped on the device (their y rows are left unwritten). */
+int lp_moe_grouped_dev(const float* x, int multi, const int* topk_idx, const uint8_t* w,
+                       uint32_t type, float* y, int T, int topk, int n_experts, int K, int N,
+                       void* ws, size_t ws_bytes, void* stream);
+
+/* Host pointers, synchronous; false (with lp_last_error) on a bad index. */
+bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_t* w,
+                    uint32_t type, float* y, int T, int topk, int n_experts, int K, int N);
+
 /* ---- diagnostics ----------------------------------------------------------- */
 
 /* Text of the last error on this thread ("" if none). */

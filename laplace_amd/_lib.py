@@ -34,6 +34,7 @@ SIGNATURES = {
     "lp_block_sums_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
     "lp_moe_grouped_dev": (_i, [_vp, _i, _vp, _vp, _u32, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "lp_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "lp_moe_grouped": (_b, [_vp, _i, _vp, _vp, _u32, _vp, _i, _i, _i, _i, _i]),
     "lp_last_error": (C.c_char_p, []),
     "lp_device_ok": (_i, []),
 }

@@ -280,21 +280,105 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     return LP_OK;
 }
 
-static int host_moe(const float* x, const uint8_t* w, uint32_t type, const int* idx, int n_exp,
-                    float* y, int K, int N, bool multi) {
+// Workspace of the grouped MoE call: activation rows (T, or T*topk in the
+// multi form), then the route table.
+static size_t moe_ws_bytes(int T, int topk, int E, int K, int multi) {
+    const int P = T * topk;
+    return act_bytes(multi ? P : T, K) + up256(moe_route_bytes(P, E));
+}
+
+static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K, int N) {
     int st = check_shape(type, w, 1, K, N);
     if (st != LP_OK) return st;
-    if (n_exp <= 0 || N == 0) return LP_OK;
-    const size_t rb = row_bytes(type, K), per_expert = rb * (size_t)N;
-    // Each selected expert is a GEMM over its slice of the stacked tensor
-    // (the sequential fallback of src/matmul.cpp:469-476, :493-499).
-    for (int k = 0; k < n_exp; k++) {
-        const uint8_t* we = w + (size_t)idx[k] * per_expert;
-        const float* xk = multi ? x + (size_t)k * K : x;
-        int rc = host_gemm(xk, we, type, y + (size_t)k * N, 1, K, N);
-        if (rc != LP_OK) return rc;
+    if (T < 0 || topk < 0 || (T > 0 && topk > 0 && (E <= 0 || E > kMoeMaxExperts))) {
+        set_err("bad MoE shape T=%d topk=%d n_experts=%d (at most %d experts)", T, topk, E,
+                kMoeMaxExperts);
+        return LP_EINVAL;
+    }
+    if ((long)T * topk > (1L << 24)) {
+        set_err("too many (token, expert) pairs: %ld", (long)T * topk);
+        return LP_EINVAL;
     }
     return LP_OK;
+}
+
+static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, uint32_t type,
+                 float* y, int T, int topk, int E, int K, int N, void* ws, hipStream_t st) {
+    const int P = T * topk, rows = multi ? P : T;
+    const ActView A = ws_view(ws, rows, K);
+    LP_HIP(launch_quantize(x, rows, K, A, st));
+    void* route = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
+    LP_HIP(launch_moe_grouped(type, w, A, idx, P, E, multi, topk, route, y, K, N, st));
+    return LP_OK;
+}
+
+// Host-pointer grouped MoE: T tokens x topk experts; idx[T*topk] is checked
+// on the host (a pair naming an expert outside [0, E) is an error).
+static int host_moe_grouped(const float* x, int multi, const int* idx, const uint8_t* w,
+                            uint32_t type, float* y, int T, int topk, int E, int K, int N) {
+    int st = check_moe(type, w, T, topk, E, K, N);
+    if (st != LP_OK) return st;
+    const int P = T * topk;
+    if (P == 0 || N == 0) return LP_OK;
+    for (int p = 0; p < P; p++) {
+        if (idx[p] < 0 || idx[p] >= E) {
+            set_err("expert index %d at pair %d outside [0, %d)", idx[p], p, E);
+            return LP_EINVAL;
+        }
+    }
+    if (!dev_info().ok) {
+        set_err("no gfx950 device");
+        return LP_ENODEV;
+    }
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) {
+        set_err("no HIP device/stream");
+        return LP_ENODEV;
+    }
+    const int rows = multi ? P : T;
+    const size_t xb = sizeof(float) * (size_t)rows * K, yb = sizeof(float) * (size_t)P * N;
+    const uint8_t* wd = nullptr;
+    int rc;
+    if ((rc = resolve_weights(*c, w, row_bytes(type, K) * (size_t)N * E, &wd)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->xd, c->xd_cap, xb)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->yd, c->yd_cap, yb)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->ws, c->ws_cap, moe_ws_bytes(T, topk, E, K, multi))) != LP_OK) return rc;
+    if ((rc = grow_dev(c->idx_d, c->idx_cap, sizeof(int) * (size_t)P)) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->x_pin, c->x_pin_cap, xb + sizeof(int) * (size_t)P)) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, yb)) != LP_OK) return rc;
+    std::memcpy(c->x_pin, x, xb);
+    int* idx_pin = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(c->x_pin) + xb);
+    std::memcpy(idx_pin, idx, sizeof(int) * (size_t)P);
+    LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
+    LP_HIP(hipMemcpyAsync(c->idx_d, idx_pin, sizeof(int) * (size_t)P, hipMemcpyHostToDevice, c->stream));
+    if ((rc = moe_q(c->xd, multi, c->idx_d, wd, type, c->yd, T, topk, E, K, N, c->ws, c->stream)) != LP_OK)
+        return rc;
+    LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipStreamSynchronize(c->stream));
+    std::memcpy(y, c->y_pin, yb);
+    return LP_OK;
+}
+
+// The reference's per-token MoE entry (src/kernels.h:100-112): one token,
+// n_exp selected experts. The stacked tensor's expert count is not passed,
+// so the selected indices bound the device copy.
+static int host_moe(const float* x, const uint8_t* w, uint32_t type, const int* idx, int n_exp,
+                    float* y, int K, int N, bool multi) {
+    if (n_exp <= 0 || N == 0) return check_shape(type, w, 1, K, N);
+    int E = 0;
+    for (int k = 0; k < n_exp; k++) {
+        if (idx[k] < 0) {
+            set_err("negative expert index %d", idx[k]);
+            return LP_EINVAL;
+        }
+        E = idx[k] + 1 > E ? idx[k] + 1 : E;
+    }
+    if (E > kMoeMaxExperts) {
+        set_err("expert index %d beyond %d", E - 1, kMoeMaxExperts);
+        return LP_UNSUPPORTED;
+    }
+    return host_moe_grouped(x, multi ? 1 : 0, idx, w, type, y, 1, n_exp, E, K, N);
 }
 
 }  // namespace lp
@@ -437,6 +521,40 @@ int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* 
     LP_HIP(launch_block_sums(type, w, ws_view(const_cast<void*>(ws), M, K), out, M, K, N,
                              static_cast<hipStream_t>(stream)));
     return LP_OK;
+}
+
+size_t lp_moe_workspace_bytes(int T, int topk, int n_experts, int K, int multi) {
+    if (T < 0 || topk < 0 || n_experts < 0 || K < 0) return 0;
+    return moe_ws_bytes(T, topk, n_experts, K, multi);
+}
+
+int lp_moe_grouped_dev(const float* x, int multi, const int* topk_idx, const uint8_t* w,
+                       uint32_t type, float* y, int T, int topk, int n_experts, int K, int N,
+                       void* ws, size_t wsb, void* stream) {
+    int rc = check_moe(type, w, T, topk, n_experts, K, N);
+    if (rc != LP_OK) return rc;
+    if (T == 0 || topk == 0 || N == 0) return LP_OK;
+    if (!x || !topk_idx || !w || !y || !ws) {
+        set_err("null pointer");
+        return LP_EINVAL;
+    }
+    if (wsb < moe_ws_bytes(T, topk, n_experts, K, multi)) {
+        set_err("workspace %zu < %zu bytes", wsb, moe_ws_bytes(T, topk, n_experts, K, multi));
+        return LP_EINVAL;
+    }
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+        set_err("x must be 16-byte aligned");
+        return LP_EINVAL;
+    }
+    return moe_q(x, multi ? 1 : 0, topk_idx, w, type, y, T, topk, n_experts, K, N, ws,
+                 static_cast<hipStream_t>(stream));
+}
+
+bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_t* w,
+                    uint32_t type, float* y, int T, int topk, int n_experts, int K, int N) {
+    int rc = host_moe_grouped(x, multi ? 1 : 0, topk_idx, w, type, y, T, topk, n_experts, K, N);
+    if (rc != LP_OK && rc != LP_UNSUPPORTED) fprintf(stderr, "[laplace_hip] %s\n", g_err);
+    return rc == LP_OK;
 }
 
 const char* lp_last_error(void) { return g_err; }

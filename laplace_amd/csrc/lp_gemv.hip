@@ -128,12 +128,17 @@ __device__ __forceinline__ void wait_vm(int n) {
 // all before any is consumed; before stage s a wave waits until only its
 // pieces that no stage <= s needs are still in flight, then the workgroup
 // synchronises and decodes the stage while later pieces keep arriving.
+//
+// gemv_tile computes tile `tile` of one weight matrix for M activation rows:
+// activation row arow[m] of A goes with output row yrow[m] of y. The plain
+// GEMV uses arow = yrow = m; the grouped MoE dispatch maps a group of
+// (token, expert) pairs onto the same code.
 template <uint32_t T, int M>
-__global__ void __launch_bounds__(512)
-gemv_kernel(const uint8_t* __restrict__ w, size_t rb, size_t wbytes, ActView A,
-            float* __restrict__ y, int K, int N, int lpr, int tile_rows, int tile_cap) {
+__device__ __forceinline__ void gemv_tile(uint8_t* smem, const uint8_t* __restrict__ w, size_t rb,
+                                          size_t wbytes, const ActView& A, const int (&arow)[M],
+                                          float* __restrict__ y, const int (&yrow)[M], int K, int N,
+                                          int lpr, int tile_rows, int tile_cap, int tile) {
     using C = Chunk<T>;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = blockDim.x >> 6;
     const int lane_in_row = tid & (lpr - 1);
@@ -149,9 +154,9 @@ gemv_kernel(const uint8_t* __restrict__ w, size_t rb, size_t wbytes, ActView A,
     const int c = lane_in_row < nchunks ? lane_in_row : nchunks - 1;
     typename C::Act act[M];
 #pragma unroll
-    for (int m = 0; m < M; m++) load_act<T>(A, K, m, c, act[m]);
+    for (int m = 0; m < M; m++) load_act<T>(A, K, arow[m], c, act[m]);
 
-    const long row_start = (long)blockIdx.x * tile_rows;
+    const long row_start = (long)tile * tile_rows;
     const uintptr_t gbeg = reinterpret_cast<uintptr_t>(w) + (uintptr_t)row_start * rb;
     const uintptr_t g0 = gbeg & ~uintptr_t(15);
     const int delta = (int)(gbeg - g0);
@@ -193,22 +198,39 @@ gemv_kernel(const uint8_t* __restrict__ w, size_t rb, size_t wbytes, ActView A,
     }
     __syncthreads();
     // y: one thread per (row, m), rows contiguous
-    for (int i = tid; i < rows_here * M; i += blockDim.x) {
-        const int m = i / rows_here, r = i - m * rows_here;
-        float s = 0.0f;
-        for (int g = 0; g < nseg; g++) s += part_s[(r * nseg + g) * M + m];
-        y[(size_t)m * N + row_start + r] = s;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        float* yr = y + (size_t)yrow[m] * N + row_start;
+        for (int r = tid; r < rows_here; r += blockDim.x) {
+            float s = 0.0f;
+            for (int g = 0; g < nseg; g++) s += part_s[(r * nseg + g) * M + m];
+            yr[r] = s;
+        }
     }
 }
 
-// tile_bytes: LDS bytes for the weight tile (0 = default).
 template <uint32_t T, int M>
-static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, int K, int N,
-                                hipStream_t st, int tile_bytes = 0) {
+__global__ void __launch_bounds__(512)
+gemv_kernel(const uint8_t* __restrict__ w, size_t rb, size_t wbytes, ActView A,
+            float* __restrict__ y, int K, int N, int lpr, int tile_rows, int tile_cap) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int rows[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) rows[m] = m;
+    gemv_tile<T, M>(smem, w, rb, wbytes, A, rows, y, rows, K, N, lpr, tile_rows, tile_cap, blockIdx.x);
+}
+
+// Launch geometry shared by the GEMV and the grouped MoE kernels.
+struct GemvGeom {
+    int lpr, wg, tile_rows, tile_cap, ntiles;
+    size_t shm;
+};
+
+static bool gemv_geom(uint32_t T, int M, int K, int N, int tile_bytes, GemvGeom& g) {
     const int nchunks = K >> 6;
     int lpr = 2;
     while (lpr < nchunks) lpr <<= 1;
-    if (lpr > 512) return hipErrorInvalidValue;   // K > 32768: not handled here
+    if (lpr > 512) return false;                  // K > 32768: not handled here
     const int wg = lpr > 256 ? lpr : 256;
     const int spw = wg / lpr;
     const size_t rb = row_bytes(T, K);
@@ -218,13 +240,27 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
     if (tile_rows > N) tile_rows = (N + spw - 1) / spw * spw;
     const int tile_cap = (int)((tile_rows * rb + 15 + kPiece - 1) / kPiece * kPiece);
     const int pieces_per_wave = (tile_cap / kPiece + wg / 64 - 1) / (wg / 64);
-    if (pieces_per_wave > 32) return hipErrorInvalidValue;
+    if (pieces_per_wave > 32) return false;
     const int nseg = lpr > 64 ? lpr / 64 : 1;
-    const size_t shm = tile_cap + sizeof(float) * (size_t)tile_rows * nseg * M;
-    if (shm > 160 * 1024) return hipErrorInvalidValue;
-    const long grid = ((long)N + tile_rows - 1) / tile_rows;
-    hipLaunchKernelGGL((gemv_kernel<T, M>), dim3((unsigned)grid), dim3(wg), shm, st,
-                       w, rb, rb * (size_t)N, A, y, K, N, lpr, tile_rows, tile_cap);
+    g.shm = tile_cap + sizeof(float) * (size_t)tile_rows * nseg * M;
+    if (g.shm > 160 * 1024) return false;
+    g.lpr = lpr;
+    g.wg = wg;
+    g.tile_rows = tile_rows;
+    g.tile_cap = tile_cap;
+    g.ntiles = (int)(((long)N + tile_rows - 1) / tile_rows);
+    return true;
+}
+
+// tile_bytes: LDS bytes for the weight tile (0 = default).
+template <uint32_t T, int M>
+static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, int K, int N,
+                                hipStream_t st, int tile_bytes = 0) {
+    GemvGeom g;
+    if (!gemv_geom(T, M, K, N, tile_bytes, g)) return hipErrorInvalidValue;
+    const size_t rb = row_bytes(T, K);
+    hipLaunchKernelGGL((gemv_kernel<T, M>), dim3((unsigned)g.ntiles), dim3(g.wg), g.shm, st,
+                       w, rb, rb * (size_t)N, A, y, K, N, g.lpr, g.tile_rows, g.tile_cap);
     return hipGetLastError();
 }
 
@@ -254,6 +290,170 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float*
         case T_Q6_K: return launch_gemv_type<T_Q6_K>(w, A, y, M, K, N, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped MoE dispatch.
+//
+// The reference runs every (token, expert) pair as its own GEMV
+// (moe_gemv_int / moe_gemv_multi_int, src/matmul_simd.cpp:506-544, called
+// per token from src/arch_gemma4.cpp:604 and :626), so an expert chosen by
+// n tokens is streamed n times. Here the pairs are grouped by expert on the
+// device and each expert's weights are streamed once per group of up to
+// kMoeGroup pairs, through the GEMV tile code above. Every pair's output is
+// the same dot product the per-pair GEMV computes (each activation row is
+// reduced on its own, so grouping does not change the arithmetic).
+//
+// Pair p = t * topk + j (token t, slot j) uses expert idx[p], activation row
+// t (or p when every pair has its own activation, the "multi" form), and
+// writes output row p.
+
+constexpr int kMoeGroup = 4;        // pairs per group (GEMV M)
+constexpr int kRouteThreads = 1024;
+
+// Route table in the workspace: [count: 1 int][pad to 16 B][groups:
+// max_groups x int4 (expert, first, n, 0)][pairs: P ints (pair ids sorted by
+// expert)].
+size_t moe_route_bytes(int P, int E) {
+    const size_t g = (size_t)moe_max_groups(P, E);
+    return 16 + g * 16 + (size_t)P * 4;
+}
+
+int moe_max_groups(int P, int E) {
+    // sum_e ceil(c_e / G) <= P / G + (number of non-empty experts)
+    const int ne = P < E ? P : E;
+    return (P + kMoeGroup - 1) / kMoeGroup + ne;
+}
+
+// One workgroup: histogram of experts (LDS atomics), exclusive scans of the
+// counts and group counts, scatter of pair ids, group table. Pairs whose
+// expert index is outside [0, E) are dropped (their outputs are not written).
+__global__ void __launch_bounds__(kRouteThreads)
+moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict__ route,
+                 int max_groups) {
+    extern __shared__ int rs[];
+    int* cnt = rs;                 // E
+    int* off = rs + E;             // E: first pair slot of expert e
+    int* goff = rs + 2 * E;        // E: first group of expert e
+    int* part = rs + 3 * E;        // kRouteThreads x 2 scan partials
+    int* ngroups = reinterpret_cast<int*>(route);
+    int4* groups = reinterpret_cast<int4*>(route + 16);
+    int* pairs = reinterpret_cast<int*>(route + 16 + (size_t)max_groups * 16);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < E; e += nt) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += nt) {
+        const int e = idx[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // block scan: thread i owns experts [i*per, (i+1)*per)
+    const int per = (E + nt - 1) / nt;
+    const int e0 = tid * per, e1 = e0 + per < E ? e0 + per : E;
+    int sc = 0, sg = 0;
+    for (int e = e0; e < e1; e++) {
+        sc += cnt[e];
+        sg += (cnt[e] + kMoeGroup - 1) / kMoeGroup;
+    }
+    part[2 * tid] = sc;
+    part[2 * tid + 1] = sg;
+    __syncthreads();
+    for (int o = 1; o < nt; o <<= 1) {
+        const int a = tid >= o ? part[2 * (tid - o)] : 0;
+        const int b = tid >= o ? part[2 * (tid - o) + 1] : 0;
+        __syncthreads();
+        part[2 * tid] += a;
+        part[2 * tid + 1] += b;
+        __syncthreads();
+    }
+    sc = part[2 * tid] - sc;        // exclusive prefix
+    sg = part[2 * tid + 1] - sg;
+    for (int e = e0; e < e1; e++) {
+        off[e] = sc;
+        goff[e] = sg;
+        const int c = cnt[e];
+        for (int g = 0; g * kMoeGroup < c; g++) {
+            const int n = c - g * kMoeGroup < kMoeGroup ? c - g * kMoeGroup : kMoeGroup;
+            groups[sg + g] = make_int4(e, sc + g * kMoeGroup, n, 0);
+        }
+        sc += c;
+        sg += (c + kMoeGroup - 1) / kMoeGroup;
+    }
+    if (tid == nt - 1) ngroups[0] = part[2 * tid + 1];
+    __syncthreads();
+    // scatter: slot within the expert from a second round of atomics
+    for (int e = tid; e < E; e += nt) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += nt) {
+        const int e = idx[p];
+        if (e >= 0 && e < E) pairs[off[e] + atomicAdd(&cnt[e], 1)] = p;
+    }
+}
+
+template <uint32_t T, int M>
+__device__ __forceinline__ void moe_group(uint8_t* smem, const uint8_t* w, size_t rb, size_t ebytes,
+                                          const ActView& A, const int* pairs, int first, int multi,
+                                          int topk, float* y, int K, int N, int lpr, int tile_rows,
+                                          int tile_cap) {
+    int arow[M], yrow[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int p = pairs[first + m];
+        yrow[m] = p;
+        arow[m] = multi ? p : p / topk;
+    }
+    gemv_tile<T, M>(smem, w, rb, ebytes, A, arow, y, yrow, K, N, lpr, tile_rows, tile_cap, blockIdx.x);
+}
+
+// grid: (row tiles of one expert, max_groups); groups beyond the routed
+// count exit at once.
+template <uint32_t T>
+__global__ void __launch_bounds__(512)
+moe_gemv_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, const uint8_t* __restrict__ route,
+                int max_groups, int multi, int topk, float* __restrict__ y, int K, int N, int lpr,
+                int tile_rows, int tile_cap) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int grp = blockIdx.y;
+    if (grp >= *reinterpret_cast<const int*>(route)) return;
+    const int4 g = reinterpret_cast<const int4*>(route + 16)[grp];
+    const int* pairs = reinterpret_cast<const int*>(route + 16 + (size_t)max_groups * 16);
+    const size_t ebytes = rb * (size_t)N;
+    const uint8_t* we = w + (size_t)g.x * ebytes;
+    switch (g.z) {
+        case 1: moe_group<T, 1>(smem, we, rb, ebytes, A, pairs, g.y, multi, topk, y, K, N, lpr, tile_rows, tile_cap); break;
+        case 2: moe_group<T, 2>(smem, we, rb, ebytes, A, pairs, g.y, multi, topk, y, K, N, lpr, tile_rows, tile_cap); break;
+        case 3: moe_group<T, 3>(smem, we, rb, ebytes, A, pairs, g.y, multi, topk, y, K, N, lpr, tile_rows, tile_cap); break;
+        default: moe_group<T, 4>(smem, we, rb, ebytes, A, pairs, g.y, multi, topk, y, K, N, lpr, tile_rows, tile_cap); break;
+    }
+}
+
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const int* idx,
+                              int P, int E, int multi, int topk, void* route, float* y, int K, int N,
+                              hipStream_t st) {
+    if (P <= 0 || N <= 0) return hipSuccess;
+    if (E <= 0 || E > kMoeMaxExperts || topk <= 0) return hipErrorInvalidValue;
+    const int mg = moe_max_groups(P, E);
+    const size_t rshm = sizeof(int) * (3 * (size_t)E + 2 * kRouteThreads);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), rshm, st, idx, P, E,
+                       static_cast<uint8_t*>(route), mg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GemvGeom g;
+    if (!gemv_geom(type, kMoeGroup, K, N, 0, g)) return hipErrorInvalidValue;
+    const size_t rb = row_bytes(type, K);
+    const dim3 grid((unsigned)g.ntiles, (unsigned)mg);
+    const uint8_t* r = static_cast<const uint8_t*>(route);
+#define LP_MOE(TT) hipLaunchKernelGGL(moe_gemv_kernel<TT>, grid, dim3(g.wg), g.shm, st, w, rb, A, r, mg, \
+                                      multi, topk, y, K, N, g.lpr, g.tile_rows, g.tile_cap)
+    switch (type) {
+        case T_Q8_0: LP_MOE(T_Q8_0); break;
+        case T_Q4_0: LP_MOE(T_Q4_0); break;
+        case T_Q4_K: LP_MOE(T_Q4_K); break;
+        case T_Q6_K: LP_MOE(T_Q6_K); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_MOE
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

@@ -35,6 +35,14 @@ bool gemm_supported(uint32_t type, int M, int K);
 size_t gemm_planes_bytes(int M, int K);
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
                        int M, int K, int N, hipStream_t st);
+// Grouped MoE dispatch (lp_gemv.hip). P = T * topk pairs, E experts stacked
+// in w (E x N rows). `route` is scratch of moe_route_bytes(P, E) bytes.
+constexpr int kMoeMaxExperts = 8192;
+int moe_max_groups(int P, int E);
+size_t moe_route_bytes(int P, int E);
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const int* idx,
+                              int P, int E, int multi, int topk, void* route, float* y, int K, int N,
+                              hipStream_t st);
 hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, int32_t* out,
                              int M, int K, int N, hipStream_t st);
 

@@ -148,7 +148,7 @@ def matmul_register_weights(buf: np.ndarray) -> None:
 
 def _moe(x, w: Tensor, y, expert_idx, n_experts: int, K: int, N: int, multi: bool) -> None:
     if _is_torch(x):
-        raise TypeError("device MoE goes through laplace_amd.moe.moe_grouped")
+        raise TypeError("device MoE goes through laplace_amd.moe.moe_grouped (T = 1)")
     idx = np.ascontiguousarray(expert_idx, dtype=np.int32)
     fn = lib().lp_moe_gemv_multi if multi else lib().lp_moe_gemv
     if not fn(_ptr(x), _ptr(w.data), int(w.type), idx.ctypes.data, n_experts, _ptr(y), K, N):

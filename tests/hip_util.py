@@ -132,3 +132,29 @@ def normwise(y, ref) -> float:
     tests/test_metal.cpp:200-203)."""
     den = float(np.abs(ref).max())
     return float(np.abs(y - ref).max()) / (den if den > 0 else 1.0)
+
+
+def moe_dev(t: int, x: np.ndarray, w: np.ndarray, idx: np.ndarray, n_experts: int, N: int,
+            multi: bool) -> np.ndarray:
+    """Grouped MoE on device pointers: y[T*topk, N]."""
+    torch = torch_dev()
+    T, topk = idx.shape
+    x = np.ascontiguousarray(x, np.float32)
+    K = x.shape[1]
+    xd, wd = to_dev(x), to_dev(w)
+    idd = to_dev(np.ascontiguousarray(idx, np.int32))
+    y = torch.full((T * topk * N,), float("nan"), dtype=torch.float32, device="cuda")
+    nb = int(L().lp_moe_workspace_bytes(T, topk, n_experts, K, 1 if multi else 0))
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    _lib.check(L().lp_moe_grouped_dev(xd.data_ptr(), 1 if multi else 0, idd.data_ptr(), wd.data_ptr(), t,
+                                      y.data_ptr(), T, topk, n_experts, K, N, ws.data_ptr(), nb,
+                                      stream()), "lp_moe_grouped_dev")
+    torch.cuda.synchronize()
+    return y.cpu().numpy().reshape(T * topk, N)
+
+
+def routing(T: int, topk: int, n_experts: int, seed: int) -> np.ndarray:
+    """Top-k expert choice per token: distinct experts, uniform without
+    replacement (the MoE benchmark configuration's routing)."""
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.choice(n_experts, topk, replace=False) for _ in range(T)]).astype(np.int32)
