@@ -22,8 +22,8 @@ cpu_baseline: the reference's portable scalar path (gemm_scalar<dot_row_q4_k>,
 src/matmul.cpp:137-167, :320-334) as restated in oracle/liboracle.so, on the
 host cores, same weights, whole matrix, median of repeated runs.
 
-Extra lines (also in the JSON, key "extra"): the other BASELINE.json GEMV
-configs, and the prefill GEMM when it is built.
+Extra lines (also in the JSON): the other BASELINE.json GEMV configs
+("extra"), the prefill GEMM ("gemm") and the grouped MoE layer ("moe").
 """
 from __future__ import annotations
 
@@ -247,6 +247,82 @@ def measure_gemm(g: Gpu, N, K, M, reps=20, copies=2, seed=0):
             "frac_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)}
 
 
+def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
+    """MoE layer dispatch: 128 Q4_K experts, 64
+    tokens, top-8 routing (distinct experts per token, uniform). One step =
+    grouped gate/up (N=1536, K=2048, one activation row per token) + grouped
+    down (N=2048, K=768, one activation row per pair), each with its
+    quantization and routing. Layer copies rotate so every step streams its
+    experts from HBM. value = (unique-expert weight bytes + x + y bytes) /
+    step time."""
+    torch = g.torch
+    t, E, T, topk = Q4_K, 128, 64, 8
+    P = T * topk
+    Ngu, Kgu, Nd, Kd = 1536, 2048, 2048, 768
+    rng = np.random.default_rng(seed + 77)
+    idx = np.stack([rng.choice(E, topk, replace=False) for _ in range(T)]).astype(np.int32)
+    wgu = synth_weights(t, Kgu, Ngu * E, seed=seed + 5)
+    wd = synth_weights(t, Kd, Nd * E, seed=seed + 6)
+    gu_list = g.copies(wgu, min_bytes=0, min_copies=copies)
+    d_list = g.copies(wd, min_bytes=0, min_copies=copies)
+    ncp = len(gu_list)
+    xgu = torch.from_numpy(synth_x(T, Kgu, seed + 7)).to(g.dev)
+    xdn = torch.from_numpy(synth_x(P, Kd, seed + 8)).to(g.dev)
+    ygu = torch.empty(P * Ngu, dtype=torch.float32, device=g.dev)
+    ydn = torch.empty(P * Nd, dtype=torch.float32, device=g.dev)
+    idd = torch.from_numpy(idx).to(g.dev)
+    nb1 = int(g.L.lp_moe_workspace_bytes(T, topk, E, Kgu, 0))
+    nb2 = int(g.L.lp_moe_workspace_bytes(T, topk, E, Kd, 1))
+    ws1 = torch.empty(nb1, dtype=torch.uint8, device=g.dev)
+    ws2 = torch.empty(nb2, dtype=torch.uint8, device=g.dev)
+
+    def step(i):
+        g.check(g.L.lp_moe_grouped_dev(xgu.data_ptr(), 0, idd.data_ptr(), gu_list[i % ncp].data_ptr(), t,
+                                       ygu.data_ptr(), T, topk, E, Kgu, Ngu, ws1.data_ptr(), nb1,
+                                       g.stream()), "moe gate_up")
+        g.check(g.L.lp_moe_grouped_dev(xdn.data_ptr(), 1, idd.data_ptr(), d_list[i % ncp].data_ptr(), t,
+                                       ydn.data_ptr(), T, topk, E, Kd, Nd, ws2.data_ptr(), nb2,
+                                       g.stream()), "moe down")
+
+    step(0)
+    torch.cuda.synchronize()
+    y0 = (ygu.clone(), ydn.clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(1)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(ncp):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    if ncp == 1:
+        assert torch.equal(ygu, y0[0]) and torch.equal(ydn, y0[1]), "graph replay differs"
+    for _ in range(3):
+        graph.replay()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+    uniq = len(np.unique(idx))
+    wbytes = uniq * (row_bytes(t, Kgu) * Ngu + row_bytes(t, Kd) * Nd)
+    alg = wbytes + 4 * (T * Kgu + P * Kd) + 4 * P * (Ngu + Nd)
+    per_pair = P * (row_bytes(t, Kgu) * Ngu + row_bytes(t, Kd) * Nd)
+    return {"workload": "Q4_K MoE layer: 128 experts, 64 tokens, top-8; gate_up 1536x2048 + "
+                        "down 2048x768 (grouped by expert)",
+            "unique_experts": uniq, "alg_bytes": int(alg), "us_step": round(us, 2),
+            "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_pair_bytes_reference": int(per_pair)}
+
+
 def cpu_baseline(t, w, x, N, K, budget_s=12.0):
     """Scalar fp32 path of the reference on the host, whole matrix."""
     from oracle import oracle as orc
@@ -289,6 +365,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM lines")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE dispatch line")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run N torch device copies of 256 MiB (a copy kernel of known "
                          "size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -362,6 +439,9 @@ def main():
                                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                                     "frac": head["frac_int8_peak"], "traffic": None},
                        "all": gemms}
+    if not args.no_moe:
+        out["moe"] = measure_moe(g)
+        g.torch.cuda.empty_cache()
     print(json.dumps(out))
 
 
