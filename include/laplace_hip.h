@@ -85,6 +85,14 @@ void lp_release_weights(void);
 int lp_quantize_act(const float* x, int M, int K, float* d, float* sum, int16_t* sum_lo,
                     int16_t* sum_hi, int8_t* qs);
 
+/* dst[0..n) = the first n elements of w, dequantized to fp32. Types: F32,
+ * F16, BF16, Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K; n a multiple of
+ * the block size. Each value equals the reference's scalar dequantize
+ * (same operation order, no contraction). Replaces Laplace::dequantize
+ * (src/matmul.h:44, src/matmul.cpp:504-675); host pointers, synchronous; the
+ * weights resolve through lp_register_weights like the matmul entries. */
+int lp_dequantize(const uint8_t* w, uint32_t type, float* dst, long n);
+
 /* ---- 2. device-pointer, stream-ordered API ------------------------------- */
 
 /* Bytes of workspace holding M rows of quantized activations of length K. */
@@ -112,6 +120,9 @@ int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int
  * out[(m*N + j)*S + s], S = K/32 (K/16 for Q6_K). */
 int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M,
                       int K, int N, void* stream);
+
+/* Device-pointer dequantize, stream-ordered. */
+int lp_dequantize_dev(const uint8_t* w, uint32_t type, float* dst, long n, void* stream);
 
 /* ---- 3. grouped MoE dispatch ---------------------------------------------- */
 

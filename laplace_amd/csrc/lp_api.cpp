@@ -557,6 +557,49 @@ bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_
     return rc == LP_OK;
 }
 
+int lp_dequantize_dev(const uint8_t* w, uint32_t type, float* dst, long n, void* stream) {
+    const int epb = dequant_block_elems(type);
+    if (epb == 0) {
+        set_err("type %u not handled by dequantize", type);
+        return LP_UNSUPPORTED;
+    }
+    if (n < 0 || n % epb != 0 || (n > 0 && (!w || !dst))) {
+        set_err("n=%ld must be a non-negative multiple of %d", n, epb);
+        return LP_EINVAL;
+    }
+    LP_HIP(launch_dequant(type, w, dst, n, static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
+int lp_dequantize(const uint8_t* w, uint32_t type, float* dst, long n) {
+    const int epb = dequant_block_elems(type);
+    if (epb == 0) {
+        set_err("type %u not handled by dequantize", type);
+        return LP_UNSUPPORTED;
+    }
+    if (n < 0 || n % epb != 0) {
+        set_err("n=%ld must be a non-negative multiple of %d", n, epb);
+        return LP_EINVAL;
+    }
+    if (n == 0) return LP_OK;
+    if (!dev_info().ok) {
+        set_err("no gfx950 device");
+        return LP_ENODEV;
+    }
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) return LP_ENODEV;
+    const size_t src = dequant_src_bytes(type, n), yb = sizeof(float) * (size_t)n;
+    const uint8_t* wd = nullptr;
+    int rc;
+    if ((rc = resolve_weights(*c, w, src, &wd)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->yd, c->yd_cap, yb)) != LP_OK) return rc;
+    LP_HIP(launch_dequant(type, wd, c->yd, n, c->stream));
+    LP_HIP(hipMemcpyAsync(dst, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipStreamSynchronize(c->stream));
+    return LP_OK;
+}
+
 const char* lp_last_error(void) { return g_err; }
 
 int lp_device_ok(void) { return dev_info().ok ? 1 : 0; }

@@ -43,6 +43,11 @@ size_t moe_route_bytes(int P, int E);
 hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const int* idx,
                               int P, int E, int multi, int topk, void* route, float* y, int K, int N,
                               hipStream_t st);
+// dequantize (lp_dequant.hip): elements per block (0 = type not handled)
+// and source bytes of n elements.
+int dequant_block_elems(uint32_t type);
+size_t dequant_src_bytes(uint32_t type, long n);
+hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, hipStream_t st);
 hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, int32_t* out,
                              int M, int K, int N, hipStream_t st);
 

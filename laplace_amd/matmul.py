@@ -8,6 +8,7 @@ Same entry points, argument meaning and output layout as the reference:
   fused_moe_gemm_idx(x, w, y, idx, n, K, N)    y[k*N + j] = expert idx[k] on x
   fused_moe_gemm_multi(x, w, y, idx, n, K, N)  y[k*N + j] = expert idx[k] on x[k]
   matmul_register_weights(buf)         device residency for a weight region
+  dequantize(w, dst, n)                dst[i] = element i of w as fp32
 
 ``x``/``y`` are either numpy float32 arrays (host path: the C ABI stages
 them through pinned memory and returns synchronously, like the reference)
@@ -165,6 +166,18 @@ def fused_moe_gemm_multi(x, w: Tensor, y, expert_idx, n_experts: int, K: int, N:
     _moe(x, w, y, expert_idx, n_experts, K, N, True)
 
 
+def dequantize(w: Tensor, dst, n: int) -> None:
+    """src/matmul.cpp:504-675: the first n elements of w as fp32 into dst."""
+    if _is_torch(dst):
+        rc = lib().lp_dequantize_dev(_ptr(w.data), int(w.type), _ptr(dst), n, _stream_ptr())
+    else:
+        assert dst.dtype == np.float32
+        rc = lib().lp_dequantize(_ptr(w.data), int(w.type), _ptr(dst), n)
+    if rc == LP_UNSUPPORTED:
+        raise NotImplementedError(lib().lp_last_error().decode())
+    check(rc, "lp_dequantize")
+
+
 def matmul_gemm_batch(specs) -> bool:
     """src/matmul.cpp:450-454: each spec (x, w, y, K, N) is an M = 1 matmul."""
     for x, w, y, K, N in specs:
@@ -191,5 +204,5 @@ def quantize_act(x: np.ndarray):
 
 __all__ = ["GGMLType", "Tensor", "matmul_row", "matmul_rows", "matmul_lm_head",
            "matmul_register_weights", "fused_moe_gemm_idx", "fused_moe_gemm_multi",
-           "matmul_gemm_batch", "quantize_act", "bytes_per_block", "elements_per_block",
+           "matmul_gemm_batch", "quantize_act", "dequantize", "bytes_per_block", "elements_per_block",
            "row_bytes", "GPU_TYPES", "LaplaceHipError", "LP_OK"]
