@@ -323,6 +323,28 @@ def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
             "per_pair_bytes_reference": int(per_pair)}
 
 
+def measure_host_api(g: Gpu, w, x, t, N, K, reps=200):
+    """The drop-in host-pointer entry (lp_gemm, the gemm_fn contract):
+    weights registered once (device-resident), x and y staged over PCIe
+    through pinned buffers, synchronous return. Median wall time per call."""
+    M = x.shape[0]
+    y = np.zeros((M, N), np.float32)
+    g.check(g.L.lp_register_weights(w.ctypes.data, w.nbytes), "lp_register_weights")
+    times = []
+    for i in range(reps + 10):
+        t0 = time.perf_counter()
+        ok = g.L.lp_gemm(x.ctypes.data, w.ctypes.data, t, y.ctypes.data, M, K, N)
+        dt = time.perf_counter() - t0
+        assert ok, "lp_gemm failed"
+        if i >= 10:
+            times.append(dt)
+    g.L.lp_release_weights()
+    med = statistics.median(times)
+    alg = w.nbytes + 4 * M * K + 4 * M * N
+    return {"us_per_call": round(med * 1e6, 2), "gbs": round(alg / med / 1e9, 1),
+            "note": "host x/y over PCIe, registered device weights, synchronous (lp_gemm)"}
+
+
 def cpu_baseline(t, w, x, N, K, budget_s=12.0):
     """Scalar fp32 path of the reference on the host, whole matrix."""
     from oracle import oracle as orc
@@ -410,6 +432,7 @@ def main():
                      "traffic": load_traffic(name),
                      "kernel": "gemv_kernel<Q4_K,M=1>", "us_per_launch": round(r["us_gemv"], 3)},
     }
+    out["host_api"] = measure_host_api(g, r["w_host"], r["x_host"], t, N, K)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(t, r["w_host"], r["x_host"], N, K)
     extra = []
