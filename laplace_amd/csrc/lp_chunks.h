@@ -32,12 +32,10 @@ template <> struct Chunk<T_Q8_0> {
 #pragma unroll
         for (int i = 0; i < 17; i++) w.w[i] = __builtin_nontemporal_load(p + i);
     }
-    // row: LDS copy of the row, 4-byte aligned
-    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * c);
-#pragma unroll
-        for (int i = 0; i < 17; i++) w.w[i] = p[i];
-    }
+    // row: LDS address of the row copy, 4-byte aligned; results valid after wait()
+    using Raw = Wt;
+    __device__ static void load_w_lds(uint32_t row, int c, Raw& w) { lds_dwords<17>(row + 68 * c, w.w); }
+    __device__ static void wait(Raw& r, Wt& w) { lds_wait(r.w); w = r; }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s0 = 0, s1 = 0;
 #pragma unroll
@@ -71,11 +69,9 @@ template <> struct Chunk<T_Q4_0> {
 #pragma unroll
         for (int i = 0; i < 9; i++) w.w[i] = __builtin_nontemporal_load(p + i);
     }
-    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 36 * c);
-#pragma unroll
-        for (int i = 0; i < 9; i++) w.w[i] = p[i];
-    }
+    using Raw = Wt;
+    __device__ static void load_w_lds(uint32_t row, int c, Raw& w) { lds_dwords<9>(row + 36 * c, w.w); }
+    __device__ static void wait(Raw& r, Wt& w) { lds_wait(r.w); w = r; }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s0 = 0, s1 = 0;
 #pragma unroll
@@ -123,13 +119,21 @@ template <> struct Chunk<T_Q4_K> {
         w.q0 = ld_nt16(blk + 16 + 32 * jb);
         w.q1 = ld_nt16(blk + 32 + 32 * jb);
     }
-    // row: LDS copy of the row, 16-byte aligned
-    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
-        const uint8_t* blk = row + 144 * (c >> 2);
-        const int jb = c & 3;
-        w.h = *reinterpret_cast<const u32x4*>(blk);
-        w.q0 = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * jb);
-        w.q1 = *reinterpret_cast<const u32x4*>(blk + 32 + 32 * jb);
+    // row: LDS address of the row copy, 16-byte aligned
+    using Raw = Wt;
+    __device__ static void load_w_lds(uint32_t row, int c, Raw& w) {
+        const uint32_t blk = row + 144 * (c >> 2);
+        const uint32_t q = blk + 32 * (c & 3);
+        lds_b128<0>(w.h, blk);
+        lds_b128<16>(w.q0, q);
+        lds_b128<32>(w.q1, q);
+    }
+    __device__ static void wait(Raw& r, Wt& w) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_wait_v(r.h);
+        lds_wait_v(r.q0);
+        lds_wait_v(r.q1);
+        w = r;
     }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
@@ -182,15 +186,39 @@ template <> struct Chunk<T_Q6_K> {
         load_window<2>(blk + 192 + 8 * h, w.sc);
         w.d = load_u16(blk + 208);
     }
-    // row: LDS copy of the row, 2-byte aligned
-    __device__ static void load_w_lds(const uint8_t* row, int c, Wt& w) {
-        const uint8_t* blk = row + 210 * (c >> 2);
+    // row: LDS address of the row copy, 2-byte aligned. Every field of the
+    // chunk sits at a multiple of 4 bytes from ql's window start p, so all
+    // windows share one byte shift sh = p & 3; the raw dwords are kept in
+    // Wt::raw until wait() funnel-shifts them.
+    struct Raw { uint32_t la[5], lb[5], qh[5], sc[3], d[1]; uint32_t sh; };
+    __device__ static void load_w_lds(uint32_t row, int c, Raw& r) {
+        const uint32_t blk = row + 210 * (c >> 2);
         const int h = (c >> 1) & 1, lr = c & 1;
-        lds_window<4>(blk + 64 * h + 16 * lr, w.la);
-        lds_window<4>(blk + 64 * h + 32 + 16 * lr, w.lb);
-        lds_window<4>(blk + 128 + 32 * h + 16 * lr, w.qh);
-        lds_window<2>(blk + 192 + 8 * h, w.sc);
-        w.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+        const uint32_t p = blk + 64 * h + 16 * lr;
+        const uint32_t a = p & ~3u;
+        r.sh = p & 3u;
+        lds_dwords<5>(a, r.la);
+        lds_dwords<5, 32>(a, r.lb);
+        lds_dwords<5>(a + 128 - 32 * h, r.qh);
+        lds_dwords<3>(a + 192 - 56 * h - 16 * lr, r.sc);
+        lds_dwords<1>((blk + 208) & ~3u, r.d);   // d: same byte shift (208 = 4 * 52)
+    }
+    __device__ static void wait(Raw& r, Wt& w) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_wait(r.la);
+        lds_wait(r.lb);
+        lds_wait(r.qh);
+        lds_wait(r.sc);
+        lds_wait(r.d);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w.la[i] = alignb(r.la[i + 1], r.la[i], r.sh);
+            w.lb[i] = alignb(r.lb[i + 1], r.lb[i], r.sh);
+            w.qh[i] = alignb(r.qh[i + 1], r.qh[i], r.sh);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) w.sc[i] = alignb(r.sc[i + 1], r.sc[i], r.sh);
+        w.d = (r.d[0] >> (8 * r.sh)) & 0xffffu;   // sh is 0 or 2: d never straddles a dword
     }
     __device__ static void isums(const Wt& w, const Act& a, int (&is)[NSUB]) {
         int s[4] = {0, 0, 0, 0};
@@ -270,6 +298,93 @@ __device__ __forceinline__ void load_act(const ActView& A, int K, int m, int c,
 #pragma unroll
         for (int i = 0; i < 4; i++) a.qsum[i] = 0;
     }
+}
+
+// The same activation registers through loads the compiler does not track
+// (inline assembly), for kernels that issue direct-to-LDS copies after them:
+// a compiler-tracked load would make its first use wait for every later copy
+// (vmcnt(0)). Protocol: act_issue(); ...later loads...; an explicit
+// s_waitcnt vmcnt(n) that covers these loads; act_finish(), which fences the
+// raw registers and only then reads them.
+struct ActRaw {
+    u32x4 q[4];
+    float d[4];
+};
+
+__device__ __forceinline__ void gld_b128(u32x4& v, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+}
+__device__ __forceinline__ void gld_b32(float& v, const void* p) {
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p));
+}
+
+// q[] holds the codes (Q6_K: four 16-byte halves; others: blocks 2c, 2c+1 as
+// 2 x 32 bytes); d[] the block scales (Q6_K) or d0, d1, sum0, sum1.
+template <uint32_t T>
+__device__ __forceinline__ void act_issue(const ActView& A, int K, int m, int c, ActRaw& r) {
+    const int nb = K >> 5;
+    const int8_t* qrow = A.qs + (size_t)m * K;
+    const float* drow = A.d + (size_t)m * nb;
+    const float* srow = A.sum + (size_t)m * nb;
+    if constexpr (T == T_Q6_K) {
+        const int sb = c >> 2, h = (c >> 1) & 1, lr = c & 1;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int blk = 8 * sb + 4 * h + g;
+            gld_b128(r.q[g], qrow + 32 * blk + 16 * lr);
+            gld_b32(r.d[g], drow + blk);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) gld_b128(r.q[i], qrow + 64 * c + 16 * i);
+        gld_b32(r.d[0], drow + 2 * c);
+        gld_b32(r.d[1], drow + 2 * c + 1);
+        gld_b32(r.d[2], srow + 2 * c);
+        gld_b32(r.d[3], srow + 2 * c + 1);
+    }
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void act_finish(ActRaw& r, typename Chunk<T>::Act& a) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) asm volatile("" : "+v"(r.q[i]), "+v"(r.d[i]));
+    if constexpr (T == T_Q6_K) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            a.q[g][0] = r.q[g].x; a.q[g][1] = r.q[g].y; a.q[g][2] = r.q[g].z; a.q[g][3] = r.q[g].w;
+            a.d[g] = r.d[g];
+            a.qsum[g] = qsum16(a.q[g]);
+        }
+        a.s[0] = a.s[1] = 0.0f;
+    } else {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const u32x4 lo = r.q[2 * b], hi = r.q[2 * b + 1];
+            a.q[b][0] = lo.x; a.q[b][1] = lo.y; a.q[b][2] = lo.z; a.q[b][3] = lo.w;
+            a.q[b][4] = hi.x; a.q[b][5] = hi.y; a.q[b][6] = hi.z; a.q[b][7] = hi.w;
+            a.d[b] = r.d[b];
+            a.s[b] = r.d[2 + b];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) a.qsum[i] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Quantizer helpers (src/matmul_simd.cpp:348-410).
+
+__device__ __forceinline__ int32_t cvt_rne_sat(float v) {
+    // vcvtnq_s32_f32: ties to even, saturating, NaN -> 0.
+    const float r = __builtin_rintf(v);
+    if (r != r) return 0;
+    if (r >= 2147483648.0f) return 2147483647;
+    if (r < -2147483648.0f) return (int32_t)0x80000000u;
+    return (int32_t)r;
+}
+
+__device__ __forceinline__ uint32_t sat8_byte(int32_t q) {
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    return (uint32_t)(q & 0xff);
 }
 
 }  // namespace lp

@@ -136,4 +136,40 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// ---------------------------------------------------------------------------
+// LDS reads as inline assembly. A compiler-generated ds_read that follows
+// direct-to-LDS copies (global_load_lds) makes the compiler wait for every
+// copy still in flight (vmcnt(0)), so a stage of a tile could not be read
+// while later stages are still arriving. These reads carry no such implicit
+// wait: the caller orders them after the copies they need with an explicit
+// s_waitcnt vmcnt + s_barrier, and waits for their results with lds_wait().
+
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+template <int OFF>
+__device__ __forceinline__ void lds_b32(uint32_t& v, uint32_t a) {
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void lds_b128(u32x4& v, uint32_t a) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF));
+}
+template <int N, int BASE = 0, int I = 0>
+__device__ __forceinline__ void lds_dwords(uint32_t a, uint32_t (&w)[N]) {
+    if constexpr (I < N) {
+        lds_b32<BASE + 4 * I>(w[I], a);
+        lds_dwords<N, BASE, I + 1>(a, w);
+    }
+}
+// Wait for all of this wave's LDS reads; every register they fill is passed
+// so no use is scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void lds_wait(uint32_t (&w)[N]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(w[i]));
+}
+__device__ __forceinline__ void lds_wait_v(u32x4& v) { asm volatile("" : "+v"(v)); }
+
 }  // namespace lp

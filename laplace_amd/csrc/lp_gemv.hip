@@ -27,15 +27,6 @@ namespace lp {
 // ---------------------------------------------------------------------------
 // Quantizer: 8 lanes per 32-element block, one float4 per lane.
 
-__device__ __forceinline__ int32_t cvt_rne_sat(float v) {
-    // vcvtnq_s32_f32: ties to even, saturating, NaN -> 0.
-    const float r = __builtin_rintf(v);
-    if (r != r) return 0;
-    if (r >= 2147483648.0f) return 2147483647;
-    if (r < -2147483648.0f) return (int32_t)0x80000000u;
-    return (int32_t)r;
-}
-
 __global__ void __launch_bounds__(256)
 quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
     const int nb = K >> 5;
@@ -152,9 +143,9 @@ __device__ __forceinline__ void gemv_tile(uint8_t* smem, const uint8_t* __restri
     const int nchunks = K >> 6;
     const float keep = lane_in_row < nchunks ? 1.0f : 0.0f;
     const int c = lane_in_row < nchunks ? lane_in_row : nchunks - 1;
-    typename C::Act act[M];
+    ActRaw araw[M];
 #pragma unroll
-    for (int m = 0; m < M; m++) load_act<T>(A, K, arow[m], c, act[m]);
+    for (int m = 0; m < M; m++) act_issue<T>(A, K, arow[m], c, araw[m]);
 
     const long row_start = (long)tile * tile_rows;
     const uintptr_t gbeg = reinterpret_cast<uintptr_t>(w) + (uintptr_t)row_start * rb;
@@ -171,8 +162,14 @@ __device__ __forceinline__ void gemv_tile(uint8_t* smem, const uint8_t* __restri
                                          16, 0, 0);
     }
     const int mine = (pieces - wave + nwaves - 1) / nwaves;   // pieces this wave issued
+    // the activation loads are older than every copy: vmcnt <= mine covers them
+    wait_vm(mine);
+    typename C::Act act[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) act_finish<T>(araw[m], act[m]);
 
     const int wl = lpr < 64 ? lpr : 64;
+    const uint32_t lds0 = lds_addr_of(smem);
     const int nstages = tile_rows / spw;
     for (int st = 0; st < nstages; st++) {
         // pieces needed through this stage, then this wave's later ones
@@ -185,8 +182,10 @@ __device__ __forceinline__ void gemv_tile(uint8_t* smem, const uint8_t* __restri
         // plain s_barrier: __syncthreads' fence would wait for every copy
         __builtin_amdgcn_s_barrier();
         const int r = st * spw + slot;
+        typename C::Raw raw;
         typename C::Wt wt;
-        C::load_w_lds(smem + delta + (size_t)r * rb, c, wt);
+        C::load_w_lds(lds0 + delta + (uint32_t)(r * rb), c, raw);
+        C::wait(raw, wt);
 #pragma unroll
         for (int m = 0; m < M; m++) {
             int is[C::NSUB];
@@ -264,11 +263,153 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K GEMV for one activation row, one super-block per lane.
+//
+// A row of K elements is nsb = K/256 super-blocks of 144 bytes. Lane l of a
+// group of L lanes (L = next power of two >= nsb) owns super-block l of every
+// row the group visits: it keeps the 256 activation codes, 8 block scales
+// and 8 block sums of that super-block in registers for the whole kernel,
+// and per row loads its 144 bytes as nine 16-byte loads. Across a wave the
+// nine loads cover 64/L rows of contiguous bytes, so every fetched line is
+// used completely (cached loads: the lines are re-hit by the neighbouring
+// lanes' later loads). Per super-block: 64 v_dot4 on the unpacked nibbles,
+// eight fp32 block-scale terms in the reference's order
+// (src/matmul_simd.cpp:226-283), then a DPP sum over the L lanes of the row.
+// No LDS, no barriers; each wave strides over row groups.
+
+// ACT_LDS: the activation codes live in LDS (one padded copy per
+// workgroup, 272-byte super-block stride: the 16 super-blocks of a read hit
+// distinct banks) instead of 64 registers per lane, for occupancy.
+template <int L, bool ACT_LDS>
+__global__ void __launch_bounds__(256)
+gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int K, int N) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int RPW = 64 / L;                   // rows per wave per step
+    const int lane = threadIdx.x & 63;
+    const int nsb = K >> 8;
+    const size_t rb = (size_t)nsb * 144;
+    const int sl = lane & (L - 1);
+    const int rsub = lane / L;
+    const bool active = sl < nsb;
+    const int sb = active ? sl : nsb - 1;
+
+    // activation block 8*sb + k: codes (32 bytes), scale xd[k], sum xs[k]
+    u32x4 a[ACT_LDS ? 1 : 16];
+    float xd[8], xs[8];
+    if constexpr (ACT_LDS) {
+        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
+        }
+    } else {
+        const u32x4* q = reinterpret_cast<const u32x4*>(A.qs + (size_t)sb * 256);
+#pragma unroll
+        for (int i = 0; i < 16; i++) a[i] = q[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        xd[k] = A.d[8 * sb + k];
+        xs[k] = A.sum[8 * sb + k];
+    }
+    if constexpr (ACT_LDS) __syncthreads();
+    const uint32_t act_l = lds_addr_of(smem) + sb * 272;
+
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    for (long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g * RPW < N; g += nwaves) {
+        const long row = g * RPW + rsub;
+        const long rr = row < N ? row : N - 1;
+        const uint8_t* blk = w + rr * rb + (size_t)sb * 144;
+        u32x4 v[9];
+#pragma unroll
+        for (int k = 0; k < 9; k++) v[k] = reinterpret_cast<const u32x4*>(blk)[k];
+
+        const u32x4 h = v[0];
+        const float d = fp16_bits_to_f32(h.x), dmin = fp16_bits_to_f32(h.x >> 16);
+        float t = 0.0f;
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            // qs bytes 32jb .. 32jb+31 = pieces 1 + 2jb, 2 + 2jb
+            const u32x4 c0 = v[1 + 2 * jb], c1 = v[2 + 2 * jb];
+            const uint32_t qv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            u32x4 lo0, lo1, hi0, hi1;
+            if constexpr (ACT_LDS) {
+                // volatile reads: kept in the loop (hoisting them would cost 64 registers)
+                const uint32_t la = act_l + 64 * jb;
+                lds_b128<0>(lo0, la);
+                lds_b128<16>(lo1, la);
+                lds_b128<32>(hi0, la);
+                lds_b128<48>(hi1, la);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                lds_wait_v(lo0);
+                lds_wait_v(lo1);
+                lds_wait_v(hi0);
+                lds_wait_v(hi1);
+            } else {
+                lo0 = a[4 * jb]; lo1 = a[4 * jb + 1]; hi0 = a[4 * jb + 2]; hi1 = a[4 * jb + 3];
+            }
+            const uint32_t al[8] = {lo0.x, lo0.y, lo0.z, lo0.w, lo1.x, lo1.y, lo1.z, lo1.w};
+            const uint32_t ah[8] = {hi0.x, hi0.y, hi0.z, hi0.w, hi1.x, hi1.y, hi1.z, hi1.w};
+            int s0 = 0, s1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                s0 = dot4(qv[i] & 0x0f0f0f0fu, al[i], s0);
+                s1 = dot4((qv[i] >> 4) & 0x0f0f0f0fu, ah[i], s1);
+            }
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_k4(2 * jb, h.y, h.z, h.w, sc0, m0);
+            scale_min_k4(2 * jb + 1, h.y, h.z, h.w, sc1, m1);
+            t = fmaf((d * (float)sc0) * xd[2 * jb], (float)s0, t);
+            t = fmaf((d * (float)sc1) * xd[2 * jb + 1], (float)s1, t);
+            t = fmaf(-(dmin * (float)m0), xs[2 * jb], t);
+            t = fmaf(-(dmin * (float)m1), xs[2 * jb + 1], t);
+        }
+        t = active ? t : 0.0f;
+        const float sum = group_sum(t, L);        // lands in lane L-1 of the group
+        if (sl == L - 1 && row < N) y[row] = sum;
+    }
+}
+
+// Lanes per row for the one-super-block-per-lane kernel (0: K not handled).
+static int sb_lanes(int K) {
+    if (K % 256 != 0) return 0;
+    const int nsb = K / 256;
+    if (nsb > 64) return 0;
+    int L = 2;
+    while (L < nsb) L <<= 1;
+    return L;
+}
+
+template <bool ACT_LDS = true>
+static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, float* y, int K, int N,
+                                hipStream_t st, int waves_per_cu = 0) {
+    const int L = sb_lanes(K);
+    const long groups = ((long)N + 64 / L - 1) / (64 / L);          // wave steps
+    long waves = groups;
+    if (waves_per_cu <= 0) waves_per_cu = ACT_LDS ? 20 : 12;
+    const long cap = (long)device_cu_count() * waves_per_cu;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    const size_t shm = ACT_LDS ? (size_t)(K / 256) * 272 : 0;
+#define LP_S(LL) case LL: hipLaunchKernelGGL((gemv_q4k_sb<LL, ACT_LDS>), dim3(grid), dim3(256), shm, st, w, A, y, K, N); break;
+    switch (L) {
+        LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_S
+    return hipGetLastError();
+}
+
 template <uint32_t T>
 static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y, int M, int K,
                                    int N, hipStream_t st) {
     switch (M) {
-        case 1: return launch_gemv_t<T, 1>(w, A, y, K, N, st);
+        case 1:
+            if constexpr (T == T_Q4_K) {
+                if (sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0)
+                    return launch_q4k_sb(w, A, y, K, N, st);
+            }
+            return launch_gemv_t<T, 1>(w, A, y, K, N, st);
         case 2: return launch_gemv_t<T, 2>(w, A, y, K, N, st);
         case 3: return launch_gemv_t<T, 3>(w, A, y, K, N, st);
         case 4: return launch_gemv_t<T, 4>(w, A, y, K, N, st);

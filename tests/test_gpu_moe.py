@@ -44,8 +44,10 @@ def test_moe_small(orc, t, multi):
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
-def test_moe_grouped_equals_gemv_bitwise(t):
-    """Each pair's row is bit-identical to the M=1 GEMV on its expert."""
+def test_moe_grouped_equals_gemv(t):
+    """Each pair's row equals the M=1 GEMV on its expert (same integer block
+    dots; the M=1 Q4_K GEMV sums the fp32 block terms in another order, so
+    the bar is fp32 rounding, 1e-6 normwise)."""
     E, T, topk, K, N = 8, 6, 3, 1024, 40
     w = synth_weights(t, K, N * E, seed=200 + t)
     idx = routing(T, topk, E, seed=11)
@@ -56,7 +58,7 @@ def test_moe_grouped_equals_gemv_bitwise(t):
         for j in range(topk):
             e = int(idx[tok, j])
             g = gemm_dev(t, x[tok], w[e * eb:(e + 1) * eb], N)[0]
-            assert np.array_equal(y[tok * topk + j], g), (tok, j, e)
+            assert normwise(y[tok * topk + j], g) <= 1e-6, (tok, j, e)
 
 
 def test_moe_skewed_and_duplicates(orc):

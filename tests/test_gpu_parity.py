@@ -266,3 +266,45 @@ def test_gemm_matches_gemv_rows(orc):
     yg = gemm_dev(Q4_K, x, w, N)
     yv = np.concatenate([gemm_dev(Q4_K, x[:8], w, N), gemm_dev(Q4_K, x[8:], w, N)])
     assert normwise(yg, yv) <= TOL
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_gemm_dev_equals_two_step(t, M):
+    """lp_gemm_dev (quantize + GEMV in one call) is bit-identical to
+    lp_quantize_act_dev + lp_gemm_q_dev on the stored blocks, including
+    blocks with zeros, exact ties, infinities and NaNs."""
+    import torch
+    from hip_util import L, stream, to_dev, workspace
+    from laplace_amd import _lib
+    K, N = 1024, 200
+    w = synth_weights(t, K, N, seed=300 + t)
+    x = synth_x(M, K, seed=301, outliers=0.01)
+    x[0, 32:64] = 0.0
+    x[0, 64:96] = np.array([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5] * 4, np.float32)
+    if M > 1:
+        x[1, 100] = np.inf
+        x[1, 300] = np.nan
+    y1 = gemm_dev(t, x, w, N)
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(M, K)
+    y2 = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    _lib.check(L().lp_quantize_act_dev(xd.data_ptr(), M, K, ws.data_ptr(), nb, stream()), "q")
+    _lib.check(L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), t, y2.data_ptr(), M, K, N, stream()), "g")
+    torch.cuda.synchronize()
+    y2 = y2.cpu().numpy().reshape(M, N)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("K", [2048, 2304, 5120, 14336, 18944, 21760])
+@pytest.mark.parametrize("N", [1, 5, 77, 1000])
+def test_q4k_stream_gemv_shapes(orc, K, N):
+    """The M=1 Q4_K GEMV streams whole rows per wave (R rows, I loads per
+    lane, both depending on K): every K it accepts, ragged N (partial last
+    wave, waves with no rows), against the oracle."""
+    t = Q4_K
+    w = synth_weights(t, K, N, seed=K + N)
+    x = synth_x(1, K, seed=7, outliers=0.01)
+    y = gemm_dev(t, x, w, N)
+    ref = orc.gemm_int(t, x, w, N)
+    assert normwise(y, ref) <= 1e-4
