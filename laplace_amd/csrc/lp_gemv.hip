@@ -278,52 +278,80 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // (src/matmul_simd.cpp:226-283), then a DPP sum over the L lanes of the row.
 // No LDS, no barriers; each wave strides over row groups.
 
-// ACT_LDS: the activation codes live in LDS (one padded copy per
-// workgroup, 272-byte super-block stride: the 16 super-blocks of a read hit
-// distinct banks) instead of 64 registers per lane, for occupancy.
-template <int L, bool ACT_LDS>
+// The activation codes live in LDS (one copy per workgroup, 272-byte
+// super-block stride: the 16 super-blocks of a read phase hit distinct
+// banks); the lane's 8 block scales and sums in registers.
+//
+// XPOSE: the wave loads its row group (RPW rows = RPW*nsb super-blocks,
+// contiguous bytes) with fully coalesced 16-byte loads (lane l: bytes 16l of
+// each KiB), writes them to a per-wave LDS buffer and reads its own
+// super-block back (144-byte lane stride: conflict-free in each 16-lane
+// phase). Otherwise each lane loads its super-block directly (cached loads at
+// a 144-byte lane stride).
+template <int L, bool XPOSE>
 __global__ void __launch_bounds__(256)
 gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int K, int N) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int RPW = 64 / L;                   // rows per wave per step
     const int lane = threadIdx.x & 63;
     const int nsb = K >> 8;
-    const size_t rb = (size_t)nsb * 144;
+    const long rb = (long)nsb * 144;
+    const long total = (long)N * rb;
     const int sl = lane & (L - 1);
     const int rsub = lane / L;
     const bool active = sl < nsb;
     const int sb = active ? sl : nsb - 1;
+    const int xbuf_off = (nsb * 272 + 15) & ~15;
+    uint8_t* wbuf = smem + xbuf_off + (size_t)((threadIdx.x >> 6) * 9216);
+    const uint32_t act_l = lds_addr_of(smem) + sb * 272;
 
-    // activation block 8*sb + k: codes (32 bytes), scale xd[k], sum xs[k]
-    u32x4 a[ACT_LDS ? 1 : 16];
-    float xd[8], xs[8];
-    if constexpr (ACT_LDS) {
-        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) {
-            const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
-            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
-        }
-    } else {
-        const u32x4* q = reinterpret_cast<const u32x4*>(A.qs + (size_t)sb * 256);
-#pragma unroll
-        for (int i = 0; i < 16; i++) a[i] = q[i];
+    // 1. activation codes -> LDS; the lane's block scales and sums -> registers
+    for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+        const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
+        *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
     }
+    float xd[8], xs[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         xd[k] = A.d[8 * sb + k];
         xs[k] = A.sum[8 * sb + k];
     }
-    if constexpr (ACT_LDS) __syncthreads();
-    const uint32_t act_l = lds_addr_of(smem) + sb * 272;
+    __syncthreads();
 
-    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
-    for (long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g * RPW < N; g += nwaves) {
-        const long row = g * RPW + rsub;
-        const long rr = row < N ? row : N - 1;
-        const uint8_t* blk = w + rr * rb + (size_t)sb * 144;
-        u32x4 v[9];
+    auto load_group = [&](long g, u32x4 (&v)[9]) {
+        if constexpr (XPOSE) {
+            const long gbeg = g * RPW * rb;
+            const long gend_full = gbeg + RPW * rb;
+            const long gend = gend_full < total ? gend_full : total;
 #pragma unroll
-        for (int k = 0; k < 9; k++) v[k] = reinterpret_cast<const u32x4*>(blk)[k];
+            for (int k = 0; k < 9; k++) {
+                long a = gbeg + 1024 * k + 16 * lane;
+                a = a + 16 <= gend ? a : gend - 16;
+                v[k] = ld_nt16(w + a);
+            }
+        } else {
+            long row = g * RPW + rsub;
+            row = row < N ? row : N - 1;
+            const u32x4* blk = reinterpret_cast<const u32x4*>(w + row * rb + (long)sb * 144);
+#pragma unroll
+            for (int k = 0; k < 9; k++) v[k] = blk[k];
+        }
+    };
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    u32x4 v[9];
+    if (g * RPW < N) load_group(g, v);
 
+    // 4. row groups
+    while (g * RPW < N) {
+        const long row = g * RPW + rsub;
+        if constexpr (XPOSE) {
+#pragma unroll
+            for (int k = 0; k < 9; k++) *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v[k];
+            const u32x4* mine = reinterpret_cast<const u32x4*>(wbuf + (size_t)(rsub * nsb + sb) * 144);
+#pragma unroll
+            for (int k = 0; k < 9; k++) v[k] = mine[k];
+        }
         const u32x4 h = v[0];
         const float d = fp16_bits_to_f32(h.x), dmin = fp16_bits_to_f32(h.x >> 16);
         float t = 0.0f;
@@ -332,22 +360,18 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int
             // qs bytes 32jb .. 32jb+31 = pieces 1 + 2jb, 2 + 2jb
             const u32x4 c0 = v[1 + 2 * jb], c1 = v[2 + 2 * jb];
             const uint32_t qv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            // volatile reads: kept in the loop (hoisting them would cost 64 registers)
             u32x4 lo0, lo1, hi0, hi1;
-            if constexpr (ACT_LDS) {
-                // volatile reads: kept in the loop (hoisting them would cost 64 registers)
-                const uint32_t la = act_l + 64 * jb;
-                lds_b128<0>(lo0, la);
-                lds_b128<16>(lo1, la);
-                lds_b128<32>(hi0, la);
-                lds_b128<48>(hi1, la);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                lds_wait_v(lo0);
-                lds_wait_v(lo1);
-                lds_wait_v(hi0);
-                lds_wait_v(hi1);
-            } else {
-                lo0 = a[4 * jb]; lo1 = a[4 * jb + 1]; hi0 = a[4 * jb + 2]; hi1 = a[4 * jb + 3];
-            }
+            const uint32_t la = act_l + 64 * jb;
+            lds_b128<0>(lo0, la);
+            lds_b128<16>(lo1, la);
+            lds_b128<32>(hi0, la);
+            lds_b128<48>(hi1, la);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_wait_v(lo0);
+            lds_wait_v(lo1);
+            lds_wait_v(hi0);
+            lds_wait_v(hi1);
             const uint32_t al[8] = {lo0.x, lo0.y, lo0.z, lo0.w, lo1.x, lo1.y, lo1.z, lo1.w};
             const uint32_t ah[8] = {hi0.x, hi0.y, hi0.z, hi0.w, hi1.x, hi1.y, hi1.z, hi1.w};
             int s0 = 0, s1 = 0;
@@ -367,6 +391,8 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int
         t = active ? t : 0.0f;
         const float sum = group_sum(t, L);        // lands in lane L-1 of the group
         if (sl == L - 1 && row < N) y[row] = sum;
+        g += nwaves;
+        if (g * RPW < N) load_group(g, v);
     }
 }
 
@@ -380,18 +406,17 @@ static int sb_lanes(int K) {
     return L;
 }
 
-template <bool ACT_LDS = true>
+template <bool XPOSE = true>
 static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, float* y, int K, int N,
-                                hipStream_t st, int waves_per_cu = 0) {
+                                hipStream_t st, int waves_per_cu = 12, int wg_waves = 4) {
     const int L = sb_lanes(K);
     const long groups = ((long)N + 64 / L - 1) / (64 / L);          // wave steps
     long waves = groups;
-    if (waves_per_cu <= 0) waves_per_cu = ACT_LDS ? 20 : 12;
     const long cap = (long)device_cu_count() * waves_per_cu;
     if (waves > cap) waves = cap;
-    const unsigned grid = (unsigned)((waves + 3) / 4);
-    const size_t shm = ACT_LDS ? (size_t)(K / 256) * 272 : 0;
-#define LP_S(LL) case LL: hipLaunchKernelGGL((gemv_q4k_sb<LL, ACT_LDS>), dim3(grid), dim3(256), shm, st, w, A, y, K, N); break;
+    const unsigned grid = (unsigned)((waves + wg_waves - 1) / wg_waves);
+    const size_t shm = (((size_t)(K / 256) * 272 + 15) & ~size_t(15)) + (XPOSE ? wg_waves * 9216 : 0);
+#define LP_S(LL) case LL: hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, y, K, N); break;
     switch (L) {
         LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
         default: return hipErrorInvalidValue;
