@@ -270,10 +270,14 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, yb)) != LP_OK) return rc;
     std::memcpy(c->x_pin, x, xb);
     LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
-    const ActView A = ws_view(c->ws, M, K);
-    LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
-    if ((rc = gemm_q(A, ws_planes(c->ws, M, K), wd, type, c->yd, M, K, N, c->stream)) != LP_OK)
-        return rc;
+    if (gemv_fused_supported(type, M, K, wd)) {
+        LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
+    } else {
+        const ActView A = ws_view(c->ws, M, K);
+        LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
+        if ((rc = gemm_q(A, ws_planes(c->ws, M, K), wd, type, c->yd, M, K, N, c->stream)) != LP_OK)
+            return rc;
+    }
     LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
     LP_HIP(hipStreamSynchronize(c->stream));
     std::memcpy(y, c->y_pin, yb);
@@ -510,6 +514,19 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
                 void* ws, size_t wsb, void* stream) {
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
+    if (gemv_fused_supported(type, M, K, w)) {
+        // one launch: the GEMV quantizes x itself (bit-identical blocks)
+        if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
+            set_err("workspace %zu < %zu bytes or null pointer", wsb, ws_bytes(M, K));
+            return LP_EINVAL;
+        }
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+            set_err("x must be 16-byte aligned");
+            return LP_EINVAL;
+        }
+        LP_HIP(launch_gemv_fused(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
+        return LP_OK;
+    }
     if ((rc = lp_quantize_act_dev(x, M, K, ws, wsb, stream)) != LP_OK) return rc;
     return lp_gemm_q_dev(ws, w, type, y, M, K, N, stream);
 }

@@ -27,6 +27,45 @@ namespace lp {
 // ---------------------------------------------------------------------------
 // Quantizer: 8 lanes per 32-element block, one float4 per lane.
 
+// One 32-element block quantized by 8 consecutive lanes (one float4 each,
+// lane g = elements 4g..4g+3): packed codes of the lane's 4 elements, and
+// the block's d, sum and (sum_lo | sum_hi << 16), valid in every lane.
+struct Q8Group {
+    uint32_t packed;
+    float d, sum;
+    int32_t s16;
+};
+
+__device__ __forceinline__ Q8Group quant_group8(const float4 v) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+        nan |= __shfl_xor(nan, off, 8);
+    }
+    if (nan) amax = __builtin_nanf("");                // FMAX propagates NaN
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const int32_t q0 = cvt_rne_sat(v.x * id), q1 = cvt_rne_sat(v.y * id);
+    const int32_t q2 = cvt_rne_sat(v.z * id), q3 = cvt_rne_sat(v.w * id);
+    // int32 sums wrap modulo 2^32 as the NEON lane adds do.
+    uint32_t s = (uint32_t)q0 + (uint32_t)q1 + (uint32_t)q2 + (uint32_t)q3;
+    s += __shfl_xor(s, 1, 8);
+    s += __shfl_xor(s, 2, 8);                          // lanes 0-3: elems 0-15, 4-7: 16-31
+    const uint32_t s_other = __shfl_xor(s, 4, 8);
+    const bool first_half = (threadIdx.x & 4) == 0;
+    const uint32_t s_lo = first_half ? s : s_other, s_hi = first_half ? s_other : s;
+    Q8Group r;
+    r.packed = sat8_byte(q0) | (sat8_byte(q1) << 8) | (sat8_byte(q2) << 16) | (sat8_byte(q3) << 24);
+    const int16_t lo = (int16_t)(uint16_t)s_lo;
+    const int16_t hi = (int16_t)(uint16_t)s_hi;
+    r.d = d;
+    r.sum = d * (float)((int32_t)lo + (int32_t)hi);
+    r.s16 = (int32_t)(((uint32_t)(uint16_t)lo) | ((uint32_t)(uint16_t)hi << 16));
+    return r;
+}
+
 __global__ void __launch_bounds__(256)
 quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
     const int nb = K >> 5;
@@ -37,35 +76,12 @@ quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
          blk += stride) {
         const long m = blk / nb, b = blk - m * nb;
         const float4 v = *reinterpret_cast<const float4*>(x + m * K + 32 * b + 4 * g);
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-            nan |= __shfl_xor(nan, off, 8);
-        }
-        if (nan) amax = __builtin_nanf("");                // FMAX propagates NaN
-        const float d = amax / 127.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        const int32_t q0 = cvt_rne_sat(v.x * id), q1 = cvt_rne_sat(v.y * id);
-        const int32_t q2 = cvt_rne_sat(v.z * id), q3 = cvt_rne_sat(v.w * id);
-        // int32 sums wrap modulo 2^32 as the NEON lane adds do.
-        uint32_t s = (uint32_t)q0 + (uint32_t)q1 + (uint32_t)q2 + (uint32_t)q3;
-        s += __shfl_xor(s, 1, 8);
-        s += __shfl_xor(s, 2, 8);                          // lanes 0-3: elems 0-15, 4-7: 16-31
-        const uint32_t s_hi = __shfl_xor(s, 4, 8);
-        auto sat8 = [](int32_t q) -> uint32_t {
-            q = q > 127 ? 127 : (q < -128 ? -128 : q);
-            return (uint32_t)(q & 0xff);
-        };
-        const uint32_t packed = sat8(q0) | (sat8(q1) << 8) | (sat8(q2) << 16) | (sat8(q3) << 24);
-        *reinterpret_cast<uint32_t*>(A.qs + m * K + 32 * b + 4 * g) = packed;
+        const Q8Group q = quant_group8(v);
+        *reinterpret_cast<uint32_t*>(A.qs + m * K + 32 * b + 4 * g) = q.packed;
         if (g == 0) {
-            const int16_t lo = (int16_t)(uint16_t)s;
-            const int16_t hi = (int16_t)(uint16_t)s_hi;
-            A.d[blk] = d;
-            A.sum[blk] = d * (float)((int32_t)lo + (int32_t)hi);
-            A.s16[blk] = (int32_t)(((uint32_t)(uint16_t)lo) | ((uint32_t)(uint16_t)hi << 16));
+            A.d[blk] = q.d;
+            A.sum[blk] = q.sum;
+            A.s16[blk] = q.s16;
         }
     }
 }
@@ -288,9 +304,13 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // super-block back (144-byte lane stride: conflict-free in each 16-lane
 // phase). Otherwise each lane loads its super-block directly (cached loads at
 // a 144-byte lane stride).
-template <int L, bool XPOSE>
+// FUSEQ: the workgroup quantizes the fp32 activation row x itself (same
+// arithmetic as quantize_act_kernel) into its LDS copy, so a GEMV step is
+// one launch; otherwise it copies the quantizer's codes from A.
+template <int L, bool XPOSE, bool FUSEQ>
 __global__ void __launch_bounds__(256)
-gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int K, int N) {
+gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
+            int K, int N) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int RPW = 64 / L;                   // rows per wave per step
     const int lane = threadIdx.x & 63;
@@ -301,22 +321,13 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int
     const int rsub = lane / L;
     const bool active = sl < nsb;
     const int sb = active ? sl : nsb - 1;
-    const int xbuf_off = (nsb * 272 + 15) & ~15;
+    const int nb = K >> 5;
+    // LDS: [codes: nsb x 272][d: nb floats][sum: nb floats][per-wave transpose buffers]
+    float* dl = reinterpret_cast<float*>(smem + nsb * 272);
+    float* sl_ = dl + nb;
+    const int xbuf_off = (nsb * 272 + 8 * nb + 15) & ~15;
     uint8_t* wbuf = smem + xbuf_off + (size_t)((threadIdx.x >> 6) * 9216);
     const uint32_t act_l = lds_addr_of(smem) + sb * 272;
-
-    // 1. activation codes -> LDS; the lane's block scales and sums -> registers
-    for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
-        const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
-        *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
-    }
-    float xd[8], xs[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        xd[k] = A.d[8 * sb + k];
-        xs[k] = A.sum[8 * sb + k];
-    }
-    __syncthreads();
 
     auto load_group = [&](long g, u32x4 (&v)[9]) {
         if constexpr (XPOSE) {
@@ -340,7 +351,40 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int
     const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
     long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     u32x4 v[9];
-    if (g * RPW < N) load_group(g, v);
+
+    // 1. activation codes -> LDS; the lane's block scales and sums -> registers
+    float xd[8], xs[8];
+    if constexpr (FUSEQ) {
+        // 8 consecutive threads per 32-element block (K/4 float4s, K/4 % 8 == 0)
+        for (int i = threadIdx.x; i < (K >> 2); i += blockDim.x) {
+            const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
+            const int b = i >> 3, gq = i & 7;
+            *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+            if (gq == 0) {
+                dl[b] = q.d;
+                sl_[b] = q.sum;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            xd[k] = dl[8 * sb + k];
+            xs[k] = sl_[8 * sb + k];
+        }
+        if (g * RPW < N) load_group(g, v);
+    } else {
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            xd[k] = A.d[8 * sb + k];
+            xs[k] = A.sum[8 * sb + k];
+        }
+        __syncthreads();
+        if (g * RPW < N) load_group(g, v);
+    }
 
     // 4. row groups
     while (g * RPW < N) {
@@ -406,23 +450,42 @@ static int sb_lanes(int K) {
     return L;
 }
 
+// x != nullptr: quantize fp32 x in the kernel (A unused).
 template <bool XPOSE = true>
-static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, float* y, int K, int N,
-                                hipStream_t st, int waves_per_cu = 12, int wg_waves = 4) {
+static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, const float* x, float* y, int K,
+                                int N, hipStream_t st, int waves_per_cu = 12, int wg_waves = 4) {
     const int L = sb_lanes(K);
     const long groups = ((long)N + 64 / L - 1) / (64 / L);          // wave steps
     long waves = groups;
     const long cap = (long)device_cu_count() * waves_per_cu;
     if (waves > cap) waves = cap;
     const unsigned grid = (unsigned)((waves + wg_waves - 1) / wg_waves);
-    const size_t shm = (((size_t)(K / 256) * 272 + 15) & ~size_t(15)) + (XPOSE ? wg_waves * 9216 : 0);
-#define LP_S(LL) case LL: hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, y, K, N); break;
+    const size_t shm = (((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15)) +
+                       (XPOSE ? wg_waves * 9216 : 0);
+#define LP_S(LL)                                                                                       \
+    case LL:                                                                                           \
+        if (x) hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, true>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N); \
+        else hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, false>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N); \
+        break;
     switch (L) {
         LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
         default: return hipErrorInvalidValue;
     }
 #undef LP_S
     return hipGetLastError();
+}
+
+// Fused quantize + GEMV for one fp32 activation row, when the type and shape
+// have a single-launch kernel (Q4_K); false otherwise.
+bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w) {
+    return type == T_Q4_K && M == 1 && sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+}
+
+hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K,
+                             int N, hipStream_t st) {
+    if (!gemv_fused_supported(type, M, K, w)) return hipErrorInvalidValue;
+    if (N <= 0) return hipSuccess;
+    return launch_q4k_sb(w, ActView{}, x, y, K, N, st);
 }
 
 template <uint32_t T>
@@ -432,7 +495,7 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
         case 1:
             if constexpr (T == T_Q4_K) {
                 if (sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0)
-                    return launch_q4k_sb(w, A, y, K, N, st);
+                    return launch_q4k_sb(w, A, nullptr, y, K, N, st);
             }
             return launch_gemv_t<T, 1>(w, A, y, K, N, st);
         case 2: return launch_gemv_t<T, 2>(w, A, y, K, N, st);

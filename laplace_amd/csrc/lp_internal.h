@@ -29,6 +29,11 @@ int device_cu_count();
 hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st);
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
                        int N, hipStream_t st);
+// Single-launch quantize + GEMV from fp32 x (M == 1, Q4_K): the workgroups
+// quantize x themselves, bit-identically to launch_quantize.
+bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w);
+hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K,
+                             int N, hipStream_t st);
 // Prefill GEMM (lp_gemm.hip): Q4_K weights, M > 8. `planes` is scratch of
 // gemm_planes_bytes(M, K) bytes (fp16 activation planes).
 bool gemm_supported(uint32_t type, int M, int K);
