@@ -308,7 +308,7 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // arithmetic as quantize_act_kernel) into its LDS copy, so a GEMV step is
 // one launch; otherwise it copies the quantizer's codes from A.
 template <int L, bool XPOSE, bool FUSEQ>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
             int K, int N) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -451,17 +451,26 @@ static int sb_lanes(int K) {
 }
 
 // x != nullptr: quantize fp32 x in the kernel (A unused).
+// Defaults from measurement on MI355X (Q4_K 14336 x 4096): 16 waves per CU;
+// one 16-wave workgroup per CU when it quantizes x itself (the quantization
+// is repeated per workgroup), 8-wave workgroups otherwise.
 template <bool XPOSE = true>
 static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, const float* x, float* y, int K,
-                                int N, hipStream_t st, int waves_per_cu = 12, int wg_waves = 4) {
+                                int N, hipStream_t st, int waves_per_cu = 16, int wg_waves = 0) {
+    if (wg_waves <= 0) wg_waves = x ? 16 : 8;
+    const size_t act_lds = ((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
+    if (XPOSE) {
+        const int fit = (int)((160 * 1024 - act_lds) / 9216);       // transpose buffers that fit
+        if (wg_waves > fit) wg_waves = fit;
+        if (wg_waves < 1) return hipErrorInvalidValue;
+    }
     const int L = sb_lanes(K);
     const long groups = ((long)N + 64 / L - 1) / (64 / L);          // wave steps
     long waves = groups;
     const long cap = (long)device_cu_count() * waves_per_cu;
     if (waves > cap) waves = cap;
     const unsigned grid = (unsigned)((waves + wg_waves - 1) / wg_waves);
-    const size_t shm = (((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15)) +
-                       (XPOSE ? wg_waves * 9216 : 0);
+    const size_t shm = act_lds + (XPOSE ? wg_waves * 9216 : 0);
 #define LP_S(LL)                                                                                       \
     case LL:                                                                                           \
         if (x) hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, true>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N); \
