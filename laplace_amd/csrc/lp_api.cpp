@@ -83,9 +83,9 @@ static size_t act_bytes(int M, int K) {
     return up256((size_t)M * K) + 3 * up256(nbk * 4);
 }
 
-// Activation blocks, plus the prefill GEMM's fp16 planes when M > 8.
+// Activation blocks, plus the fp16 planes of the MFMA products when M >= 5.
 static size_t ws_bytes(int M, int K) {
-    return act_bytes(M, K) + (M > 8 ? gemm_planes_bytes(M, K) : 0);
+    return act_bytes(M, K) + (M >= 5 ? gemm_planes_bytes(M, K) : 0);
 }
 
 static void* ws_planes(void* ws, int M, int K) {
@@ -272,6 +272,10 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
     if (gemv_fused_supported(type, M, K, wd)) {
         LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
+    } else if (gemm_supported(type, M, K)) {
+        void* planes = ws_planes(c->ws, M, K);
+        LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));
+        LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
     } else {
         const ActView A = ws_view(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
@@ -286,9 +290,11 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
 
 // Workspace of the grouped MoE call: activation rows (T, or T*topk in the
 // multi form), then the route table.
+// Workspace of the grouped MoE call: activation blocks and fp16 planes of the
+// activation rows (T, or T*topk in the multi form), then the route table.
 static size_t moe_ws_bytes(int T, int topk, int E, int K, int multi) {
-    const int P = T * topk;
-    return act_bytes(multi ? P : T, K) + up256(moe_route_bytes(P, E));
+    const int P = T * topk, rows = multi ? P : T;
+    return act_bytes(rows, K) + gemm_planes_bytes(rows, K) + up256(moe_route_bytes(P, E));
 }
 
 static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K, int N) {
@@ -310,9 +316,16 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
                  float* y, int T, int topk, int E, int K, int N, void* ws, hipStream_t st) {
     const int P = T * topk, rows = multi ? P : T;
     const ActView A = ws_view(ws, rows, K);
-    LP_HIP(launch_quantize(x, rows, K, A, st));
-    void* route = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
-    LP_HIP(launch_moe_grouped(type, w, A, idx, P, E, multi, topk, route, y, K, N, st));
+    void* planes = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
+    void* route = static_cast<uint8_t*>(planes) + gemm_planes_bytes(rows, K);
+    // groups of <= 16 pairs on the MFMA kernel pay off when experts are
+    // chosen by many pairs on average (prefill); decode-sized batches
+    // (a few pairs per expert) stay on the GEMV tile kernel
+    const bool mf = moe_mf_supported(type, K) && P >= 8 * E;
+    if (mf) LP_HIP(launch_planes_from_x(x, planes, rows, K, st));
+    else LP_HIP(launch_quantize(x, rows, K, A, st));
+    LP_HIP(launch_moe_grouped(type, w, A, mf ? planes : nullptr, rows, idx, P, E, multi, topk, route, y, K,
+                              N, st));
     return LP_OK;
 }
 
@@ -525,6 +538,22 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
             return LP_EINVAL;
         }
         LP_HIP(launch_gemv_fused(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
+        return LP_OK;
+    }
+    if (gemm_supported(type, M, K)) {
+        // fp16 planes straight from x (one pass), then the MFMA product
+        if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
+            set_err("workspace %zu < %zu bytes or null pointer", wsb, ws_bytes(M, K));
+            return LP_EINVAL;
+        }
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+            set_err("x must be 16-byte aligned");
+            return LP_EINVAL;
+        }
+        void* planes = ws_planes(ws, M, K);
+        hipStream_t hs = static_cast<hipStream_t>(stream);
+        LP_HIP(launch_planes_from_x(x, planes, M, K, hs));
+        LP_HIP(launch_gemm_planes(type, w, planes, y, M, K, N, hs));
         return LP_OK;
     }
     if ((rc = lp_quantize_act_dev(x, M, K, ws, wsb, stream)) != LP_OK) return rc;

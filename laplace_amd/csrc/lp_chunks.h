@@ -387,4 +387,43 @@ __device__ __forceinline__ uint32_t sat8_byte(int32_t q) {
     return (uint32_t)(q & 0xff);
 }
 
+// One 32-element block quantized by 8 consecutive lanes (one float4 each,
+// lane g = elements 4g..4g+3): packed codes of the lane's 4 elements, and
+// the block's d, sum and (sum_lo | sum_hi << 16), valid in every lane.
+struct Q8Group {
+    uint32_t packed;
+    float d, sum;
+    int32_t s16;
+};
+
+__device__ __forceinline__ Q8Group quant_group8(const float4 v) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+        nan |= __shfl_xor(nan, off, 8);
+    }
+    if (nan) amax = __builtin_nanf("");                // FMAX propagates NaN
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const int32_t q0 = cvt_rne_sat(v.x * id), q1 = cvt_rne_sat(v.y * id);
+    const int32_t q2 = cvt_rne_sat(v.z * id), q3 = cvt_rne_sat(v.w * id);
+    // int32 sums wrap modulo 2^32 as the NEON lane adds do.
+    uint32_t s = (uint32_t)q0 + (uint32_t)q1 + (uint32_t)q2 + (uint32_t)q3;
+    s += __shfl_xor(s, 1, 8);
+    s += __shfl_xor(s, 2, 8);                          // lanes 0-3: elems 0-15, 4-7: 16-31
+    const uint32_t s_other = __shfl_xor(s, 4, 8);
+    const bool first_half = (threadIdx.x & 4) == 0;
+    const uint32_t s_lo = first_half ? s : s_other, s_hi = first_half ? s_other : s;
+    Q8Group r;
+    r.packed = sat8_byte(q0) | (sat8_byte(q1) << 8) | (sat8_byte(q2) << 16) | (sat8_byte(q3) << 24);
+    const int16_t lo = (int16_t)(uint16_t)s_lo;
+    const int16_t hi = (int16_t)(uint16_t)s_hi;
+    r.d = d;
+    r.sum = d * (float)((int32_t)lo + (int32_t)hi);
+    r.s16 = (int32_t)(((uint32_t)(uint16_t)lo) | ((uint32_t)(uint16_t)hi << 16));
+    return r;
+}
+
 }  // namespace lp

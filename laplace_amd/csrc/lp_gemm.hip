@@ -33,14 +33,17 @@
 // in registers (v_perm + magic-number packed-fp16 FMA).
 #include <hip/hip_runtime.h>
 
-#include "lp_device.h"
+#include "lp_chunks.h"
 #include "lp_internal.h"
 
 namespace lp {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int kPlaneChunk = 1024;   // elements per workgroup in the plane kernels
 
 // ---------------------------------------------------------------------------
 // Activation planes for the GEMM, built from the quantized activations.
@@ -49,11 +52,16 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 //   escale : f32 [M]            2^E_m (applied to the row's outputs)
 // E_m = exponent of max_b xd_mb, so |xd*q*2^-E| <= 127.
 
+// hi = fp16(v) and lo = fp16(v - hi) must both come from the same fp32 v =
+// fl(d*q): if the compiler fuses the product into the fp16 conversion of one
+// use (v_fma_mix) but not the other, hi + lo misses v by an fp16 ulp at
+// rounding ties. Contraction is off and v passes through an empty asm.
 __global__ void __launch_bounds__(256)
 gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restrict__ lo,
                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
                  float* __restrict__ escale) {
-    const int m = blockIdx.x;
+#pragma clang fp contract(off)
+    const int m = blockIdx.y;
     const int nb = K >> 5;
     const float* d = A.d + (size_t)m * nb;
     const float* s = A.sum + (size_t)m * nb;
@@ -70,19 +78,31 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
     int e = 0;
     if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
     const float inv = ldexpf(1.0f, -e);
-    if (threadIdx.x == 0) escale[m] = ldexpf(1.0f, e);
-    const int8_t* q = A.qs + (size_t)m * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        const float v = (d[k >> 5] * inv) * (float)q[k];
-        const _Float16 h = (_Float16)v;
-        hi[(size_t)m * K + k] = h;
-        lo[(size_t)m * K + k] = (_Float16)(v - (float)h);
-    }
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-        const float v = s[b] * inv;
-        const _Float16 h = (_Float16)v;
-        shi[(size_t)m * nb + b] = h;
-        slo[(size_t)m * nb + b] = (_Float16)(v - (float)h);
+    if (threadIdx.x == 0 && blockIdx.x == 0) escale[m] = ldexpf(1.0f, e);
+    // this workgroup's chunk: 4 codes per thread
+    const int k = 4 * (blockIdx.x * (int)blockDim.x + (int)threadIdx.x);
+    if (k < K) {
+        const uint32_t qq = *reinterpret_cast<const uint32_t*>(A.qs + (size_t)m * K + k);
+        const float ds = d[k >> 5] * inv;
+        h4 vh, vl;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float v = ds * (float)(int8_t)(qq >> (8 * c));
+            asm volatile("" : "+v"(v));   // hi and lo both from fl32(v): no fused fp16 product
+            const _Float16 h = (_Float16)v;
+            vh[c] = h;
+            vl[c] = (_Float16)(v - (float)h);
+        }
+        *reinterpret_cast<h4*>(hi + (size_t)m * K + k) = vh;
+        *reinterpret_cast<h4*>(lo + (size_t)m * K + k) = vl;
+        if ((k & 31) == 0) {
+            const int b = k >> 5;
+            float v = s[b] * inv;
+            asm volatile("" : "+v"(v));
+            const _Float16 h = (_Float16)v;
+            shi[(size_t)m * nb + b] = h;
+            slo[(size_t)m * nb + b] = (_Float16)(v - (float)h);
+        }
     }
 }
 
@@ -446,37 +466,318 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// Planes of M activation rows carved from one buffer (256-byte aligned).
+
+struct Planes {
+    _Float16* hi;
+    _Float16* lo;
+    _Float16* shi;
+    _Float16* slo;
+    float* escale;
+};
+
+static Planes carve_planes(void* base, int M, int K) {
+    auto r = [](size_t v) { return (v + 255) / 256 * 256; };
+    uint8_t* p = static_cast<uint8_t*>(base);
+    Planes P;
+    P.hi = reinterpret_cast<_Float16*>(p);
+    p += r((size_t)M * K * 2);
+    P.lo = reinterpret_cast<_Float16*>(p);
+    p += r((size_t)M * K * 2);
+    P.shi = reinterpret_cast<_Float16*>(p);
+    p += r((size_t)M * (K / 32) * 2);
+    P.slo = reinterpret_cast<_Float16*>(p);
+    p += r((size_t)M * (K / 32) * 2);
+    P.escale = reinterpret_cast<float*>(p);
+    return P;
+}
+
+// Quantize fp32 activation rows and write their planes in one pass per
+// row (one workgroup per row), without storing the ActQ8 blocks: the same
+// values as quantize_act_kernel followed by gemm_prep_kernel. Pass 1: block
+// scales and their row maximum (the exponent E); pass 2: the codes again
+// (x is re-read from cache), hi/lo and shi/slo.
+__global__ void __launch_bounds__(256)
+quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
+#pragma clang fp contract(off)
+    const int m = blockIdx.y;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * K);
+    const int n4 = K >> 2, nb = K >> 5;
+    // pass 1 (whole row, every workgroup): the largest block scale. Block
+    // scales are fl(amax_b / 127), monotone in amax_b, so their maximum is
+    // fl(max amax_b / 127), over the blocks without a NaN (a NaN block's
+    // scale is NaN, which the maximum skips).
+    __shared__ float red[256];
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        const float4 v = xr[i];
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+            nan |= __shfl_xor(nan, off, 8);
+        }
+        if (!nan) mx = fmaxf(mx, amax);
+    }
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+        __syncthreads();
+    }
+    mx = red[0] / 127.0f;
+    int e = 0;
+    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+    const float inv = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0 && blockIdx.x == 0) P.escale[m] = ldexpf(1.0f, e);
+    // pass 2: this workgroup's chunk
+    _Float16* hi = P.hi + (size_t)m * K;
+    _Float16* lo = P.lo + (size_t)m * K;
+    const int i = blockIdx.x * (kPlaneChunk / 4) + threadIdx.x;
+    if (i < n4) {
+        const Q8Group q = quant_group8(xr[i]);
+        const float ds = q.d * inv;
+        h4 vh, vl;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float v = ds * (float)(int8_t)(q.packed >> (8 * c));
+            asm volatile("" : "+v"(v));   // hi and lo both from fl32(v): no fused fp16 product
+            const _Float16 h = (_Float16)v;
+            vh[c] = h;
+            vl[c] = (_Float16)(v - (float)h);
+        }
+        *reinterpret_cast<h4*>(hi + 4 * i) = vh;
+        *reinterpret_cast<h4*>(lo + 4 * i) = vl;
+        if ((i & 7) == 0) {
+            const int b = i >> 3;
+            float v = q.sum * inv;
+            asm volatile("" : "+v"(v));
+            const _Float16 h = (_Float16)v;
+            P.shi[(size_t)m * nb + b] = h;
+            P.slo[(size_t)m * nb + b] = (_Float16)(v - (float)h);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small-M Q4_K product on MFMA: M <= 16 activation rows (tokens) against
+// every weight row, with the prefill GEMM's exact operand folding (A = the
+// tokens' hi/lo planes, B = V = sc * nibble in fp16) on
+// v_mfma_f32_16x16x32_f16: one MFMA pair per 32-element sub-block, so the
+// per-element VALU work is the nibble decode alone, independent of M.
+//
+// Workgroup = kMfTiles x 16 weight rows x kMfWaves waves; wave w takes the
+// super-blocks [w*nsb/8, (w+1)*nsb/8) of all the rows (one activation load
+// feeds kMfTiles MFMA pairs), and the waves' partial sums are added in a
+// fixed order through LDS. Lane l: A row (token) l%16, B column
+// (weight row) l%16, k = 8*(l/16) .. +8 of the sub-block; D: weight row
+// l%16, tokens 4*(l/16) .. +4. Lanes load their row's super-block header
+// and their 8-byte slice of each 32-byte code quarter directly (cached).
+// MOE: blockIdx.y is a routed group (expert, first pair, n <= 16 pairs).
+
+constexpr int kMfWaves = 8;
+constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
+constexpr int kMfMaxM = 16;
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+struct MfArgs {
+    const uint8_t* w;
+    long rb;              // bytes per weight row
+    long ebytes;          // bytes per expert (MOE)
+    int N, K, M;
+    Planes P;
+    float* y;
+    const uint8_t* route; // MOE route table (see moe_route_kernel)
+    int max_groups, multi, topk;
+};
+
+template <bool MOE>
+__global__ void __launch_bounds__(64 * kMfWaves)
+gemv_q4k_mf(MfArgs a) {
+    __shared__ f4v red[kMfWaves][kMfTiles][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int tok = lane & 15, g = lane >> 4;
+    int M = a.M;
+    const uint8_t* w = a.w;
+    const int* pairs = nullptr;
+    int first = 0;
+    if constexpr (MOE) {
+        if ((int)blockIdx.y >= *reinterpret_cast<const int*>(a.route)) return;
+        const int4 gd = reinterpret_cast<const int4*>(a.route + 16)[blockIdx.y];
+        pairs = reinterpret_cast<const int*>(a.route + 16 + (size_t)a.max_groups * 16);
+        first = gd.y;
+        M = gd.z;
+        w += (size_t)gd.x * a.ebytes;
+    }
+    // activation row of token t (its planes)
+    auto act_row = [&](int t) -> int {
+        if constexpr (MOE) {
+            const int p = pairs[first + t];
+            return a.multi ? p : p / a.topk;
+        } else {
+            return t;
+        }
+    };
+    const bool tv = tok < M;
+    const int arow = act_row(tv ? tok : 0);
+    const int row0 = blockIdx.x * (16 * kMfTiles) + (lane & 15);
+    const int nsb = a.K >> 8, nb = a.K >> 5;
+    const int sb0 = wv * nsb / kMfWaves, sb1 = (wv + 1) * nsb / kMfWaves;
+    const uint8_t* wr[kMfTiles];
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) {
+        int row = row0 + 16 * t;
+        row = row < a.N ? row : a.N - 1;
+        wr[t] = w + (size_t)row * a.rb;
+    }
+    const _Float16* ahi = a.P.hi + (size_t)arow * a.K + 8 * g;
+    const _Float16* alo = a.P.lo + (size_t)arow * a.K + 8 * g;
+    const _Float16* xsh = a.P.shi + (size_t)arow * nb;
+    const _Float16* xsl = a.P.slo + (size_t)arow * nb;
+    const h8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    f4v acc[kMfTiles];
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) acc[t] = z4;
+    for (int s = sb0; s < sb1; s++) {
+        u32x4 h[kMfTiles];
+        uint2 q[kMfTiles][4];
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) {
+            const uint8_t* blk = wr[t] + 144 * s;
+            h[t] = *reinterpret_cast<const u32x4*>(blk);
+#pragma unroll
+            for (int jb = 0; jb < 4; jb++) q[t][jb] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * jb + 8 * g);
+        }
+        f4v mainv[kMfTiles];
+        h8 mm[kMfTiles];
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) mainv[t] = z4;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int k0 = 32 * (8 * s + b);
+            const h8 vh = tv ? *reinterpret_cast<const h8*>(ahi + k0) : z8;
+            const h8 vl = tv ? *reinterpret_cast<const h8*>(alo + k0) : z8;
+#pragma unroll
+            for (int t = 0; t < kMfTiles; t++) {
+                uint32_t sc, mn;
+                scale_min_k4(b, h[t].y, h[t].z, h[t].w, sc, mn);
+                mm[t][b] = (_Float16)(float)mn;
+                // even blocks use low nibbles (1024 + n), odd high (1024 + 16n)
+                const float sf = (b & 1) ? (float)sc * 0.0625f : (float)sc;
+                const _Float16 hs = (_Float16)sf, ha = (_Float16)(-1024.0f * sf);
+                const h8 v = decode_v(q[t][b >> 1].x, q[t][b >> 1].y, (b & 1) != 0, h2{hs, hs}, h2{ha, ha});
+                mainv[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, v, mainv[t], 0, 0, 0);
+                mainv[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, v, mainv[t], 0, 0, 0);
+            }
+        }
+        // min term: sum_b m_b * xs_b as a K = 8 product (k = 8g + e; only g = 0 non-zero)
+        const h8 sh = (tv && g == 0) ? *reinterpret_cast<const h8*>(xsh + 8 * s) : z8;
+        const h8 sl = (tv && g == 0) ? *reinterpret_cast<const h8*>(xsl + 8 * s) : z8;
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) {
+            const h8 mb = g == 0 ? mm[t] : z8;
+            f4v mnv = __builtin_amdgcn_mfma_f32_16x16x32_f16(sh, mb, z4, 0, 0, 0);
+            mnv = __builtin_amdgcn_mfma_f32_16x16x32_f16(sl, mb, mnv, 0, 0, 0);
+            const float d = fp16_bits_to_f32(h[t].x), dmin = fp16_bits_to_f32(h[t].x >> 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                acc[t][r] = fmaf(d, mainv[t][r], acc[t][r]);
+                acc[t][r] = fmaf(-dmin, mnv[r], acc[t][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) red[wv][t][lane] = acc[t];
+    __syncthreads();
+    // wave t sums tile t over the K-slices in a fixed order
+    if (wv < kMfTiles) {
+        const int t = wv;
+        f4v sum = red[0][t][lane];
+#pragma unroll
+        for (int i = 1; i < kMfWaves; i++) sum += red[i][t][lane];
+        const int row = row0 + 16 * t;
+        if (row < a.N) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tt = 4 * g + r;
+                if (tt < M) {
+                    int yr;
+                    if constexpr (MOE) yr = pairs[first + tt];
+                    else yr = tt;
+                    a.y[(size_t)yr * a.N + row] = sum[r] * a.P.escale[act_row(tt)];
+                }
+            }
+        }
+    }
+}
+
 size_t gemm_planes_bytes(int M, int K) {
     const size_t up = 256;
     auto r = [&](size_t v) { return (v + up - 1) / up * up; };
     return 2 * r((size_t)M * K * 2) + 2 * r((size_t)M * (K / 32) * 2) + r((size_t)M * 4);
 }
 
+// Measured on MI355X (Q4_K 18944 x 3584): the GEMV tile kernel is faster
+// up to M = 4, the small-M MFMA kernel from M = 5 to 16.
+constexpr int kMfMinM = 5;
+
 bool gemm_supported(uint32_t type, int M, int K) {
-    return type == T_Q4_K && M > 8 && K % 256 == 0;
+    return type == T_Q4_K && M >= kMfMinM && K % 256 == 0;
+}
+
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quant_planes_kernel, dim3((K + kPlaneChunk - 1) / kPlaneChunk, M), dim3(kPlaneChunk / 4), 0, st,
+                       x, K, carve_planes(planes, M, K));
+    return hipGetLastError();
+}
+
+static hipError_t launch_planes_from_act(const ActView& A, void* planes, int M, int K, hipStream_t st) {
+    const Planes P = carve_planes(planes, M, K);
+    hipLaunchKernelGGL(gemm_prep_kernel, dim3((K + kPlaneChunk - 1) / kPlaneChunk, M), dim3(kPlaneChunk / 4), 0, st,
+                       A, K, P.hi, P.lo, P.shi, P.slo, P.escale);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,
+                              hipStream_t st) {
+    if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
+    if (M <= 0 || N <= 0) return hipSuccess;
+    const Planes P = carve_planes(planes, M, K);
+    if (M <= kMfMaxM) {
+        MfArgs a{w, (long)row_bytes(type, K), 0, N, K, M, P, y, nullptr, 0, 0, 1};
+        hipLaunchKernelGGL(gemv_q4k_mf<false>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles)), dim3(64 * kMfWaves),
+                           0, st, a);
+        return hipGetLastError();
+    }
+    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K};
+    const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
+    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(ntn * ntm), dim3(kGemmThreads), GEMM_LDS, st, g, ntn);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
                        int M, int K, int N, hipStream_t st) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
-    auto r = [](size_t v) { return (v + 255) / 256 * 256; };
-    uint8_t* p = static_cast<uint8_t*>(planes);
-    _Float16* hi = reinterpret_cast<_Float16*>(p);
-    p += r((size_t)M * K * 2);
-    _Float16* lo = reinterpret_cast<_Float16*>(p);
-    p += r((size_t)M * K * 2);
-    _Float16* shi = reinterpret_cast<_Float16*>(p);
-    p += r((size_t)M * (K / 32) * 2);
-    _Float16* slo = reinterpret_cast<_Float16*>(p);
-    p += r((size_t)M * (K / 32) * 2);
-    float* escale = reinterpret_cast<float*>(p);
-    hipLaunchKernelGGL(gemm_prep_kernel, dim3(M), dim3(256), 0, st, A, K, hi, lo, shi, slo, escale);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_planes_from_act(A, planes, M, K, st);
     if (e != hipSuccess) return e;
-    GemmArgs g{hi, lo, shi, slo, escale, w, row_bytes(type, K), y, M, N, K};
-    const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(ntn * ntm), dim3(kGemmThreads), GEMM_LDS, st, g, ntn);
+    return launch_gemm_planes(type, w, planes, y, M, K, N, st);
+}
+
+bool moe_mf_supported(uint32_t type, int K) { return type == T_Q4_K && K % 256 == 0; }
+
+hipError_t launch_moe_mf(const uint8_t* w, const void* planes, int rows, const void* route, int max_groups,
+                         int multi, int topk, float* y, int K, int N, hipStream_t st) {
+    const Planes P = carve_planes(const_cast<void*>(planes), rows, K);
+    const long rb = (long)row_bytes(T_Q4_K, K);
+    MfArgs a{w, rb, rb * N, N, K, 0, P, y, static_cast<const uint8_t*>(route), max_groups, multi, topk};
+    hipLaunchKernelGGL(gemv_q4k_mf<true>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles), max_groups),
+                       dim3(64 * kMfWaves), 0, st, a);
     return hipGetLastError();
 }
 

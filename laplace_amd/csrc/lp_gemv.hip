@@ -27,45 +27,6 @@ namespace lp {
 // ---------------------------------------------------------------------------
 // Quantizer: 8 lanes per 32-element block, one float4 per lane.
 
-// One 32-element block quantized by 8 consecutive lanes (one float4 each,
-// lane g = elements 4g..4g+3): packed codes of the lane's 4 elements, and
-// the block's d, sum and (sum_lo | sum_hi << 16), valid in every lane.
-struct Q8Group {
-    uint32_t packed;
-    float d, sum;
-    int32_t s16;
-};
-
-__device__ __forceinline__ Q8Group quant_group8(const float4 v) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-        nan |= __shfl_xor(nan, off, 8);
-    }
-    if (nan) amax = __builtin_nanf("");                // FMAX propagates NaN
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    const int32_t q0 = cvt_rne_sat(v.x * id), q1 = cvt_rne_sat(v.y * id);
-    const int32_t q2 = cvt_rne_sat(v.z * id), q3 = cvt_rne_sat(v.w * id);
-    // int32 sums wrap modulo 2^32 as the NEON lane adds do.
-    uint32_t s = (uint32_t)q0 + (uint32_t)q1 + (uint32_t)q2 + (uint32_t)q3;
-    s += __shfl_xor(s, 1, 8);
-    s += __shfl_xor(s, 2, 8);                          // lanes 0-3: elems 0-15, 4-7: 16-31
-    const uint32_t s_other = __shfl_xor(s, 4, 8);
-    const bool first_half = (threadIdx.x & 4) == 0;
-    const uint32_t s_lo = first_half ? s : s_other, s_hi = first_half ? s_other : s;
-    Q8Group r;
-    r.packed = sat8_byte(q0) | (sat8_byte(q1) << 8) | (sat8_byte(q2) << 16) | (sat8_byte(q3) << 24);
-    const int16_t lo = (int16_t)(uint16_t)s_lo;
-    const int16_t hi = (int16_t)(uint16_t)s_hi;
-    r.d = d;
-    r.sum = d * (float)((int32_t)lo + (int32_t)hi);
-    r.s16 = (int32_t)(((uint32_t)(uint16_t)lo) | ((uint32_t)(uint16_t)hi << 16));
-    return r;
-}
-
 __global__ void __launch_bounds__(256)
 quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
     const int nb = K >> 5;
@@ -547,6 +508,7 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float*
 // writes output row p.
 
 constexpr int kMoeGroup = 4;        // pairs per group (GEMV M)
+constexpr int kMoeGroupMf = 16;     // pairs per group on the small-M MFMA kernel (Q4_K)
 constexpr int kRouteThreads = 1024;
 
 // Route table in the workspace: [count: 1 int][pad to 16 B][groups:
@@ -568,7 +530,7 @@ int moe_max_groups(int P, int E) {
 // expert index is outside [0, E) are dropped (their outputs are not written).
 __global__ void __launch_bounds__(kRouteThreads)
 moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict__ route,
-                 int max_groups) {
+                 int max_groups, int gsize) {
     extern __shared__ int rs[];
     int* cnt = rs;                 // E
     int* off = rs + E;             // E: first pair slot of expert e
@@ -591,7 +553,7 @@ moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict_
     int sc = 0, sg = 0;
     for (int e = e0; e < e1; e++) {
         sc += cnt[e];
-        sg += (cnt[e] + kMoeGroup - 1) / kMoeGroup;
+        sg += (cnt[e] + gsize - 1) / gsize;
     }
     part[2 * tid] = sc;
     part[2 * tid + 1] = sg;
@@ -610,12 +572,12 @@ moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict_
         off[e] = sc;
         goff[e] = sg;
         const int c = cnt[e];
-        for (int g = 0; g * kMoeGroup < c; g++) {
-            const int n = c - g * kMoeGroup < kMoeGroup ? c - g * kMoeGroup : kMoeGroup;
-            groups[sg + g] = make_int4(e, sc + g * kMoeGroup, n, 0);
+        for (int g = 0; g * gsize < c; g++) {
+            const int n = c - g * gsize < gsize ? c - g * gsize : gsize;
+            groups[sg + g] = make_int4(e, sc + g * gsize, n, 0);
         }
         sc += c;
-        sg += (c + kMoeGroup - 1) / kMoeGroup;
+        sg += (c + gsize - 1) / gsize;
     }
     if (tid == nt - 1) ngroups[0] = part[2 * tid + 1];
     __syncthreads();
@@ -665,17 +627,19 @@ moe_gemv_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, const uint8
     }
 }
 
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const int* idx,
-                              int P, int E, int multi, int topk, void* route, float* y, int K, int N,
-                              hipStream_t st) {
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+                              int rows, const int* idx, int P, int E, int multi, int topk, void* route,
+                              float* y, int K, int N, hipStream_t st) {
     if (P <= 0 || N <= 0) return hipSuccess;
     if (E <= 0 || E > kMoeMaxExperts || topk <= 0) return hipErrorInvalidValue;
+    const bool mf = planes != nullptr && moe_mf_supported(type, K);
     const int mg = moe_max_groups(P, E);
     const size_t rshm = sizeof(int) * (3 * (size_t)E + 2 * kRouteThreads);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), rshm, st, idx, P, E,
-                       static_cast<uint8_t*>(route), mg);
+                       static_cast<uint8_t*>(route), mg, mf ? kMoeGroupMf : kMoeGroup);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (mf) return launch_moe_mf(w, planes, rows, route, mg, multi, topk, y, K, N, st);
     GemvGeom g;
     if (!gemv_geom(type, kMoeGroup, K, N, 0, g)) return hipErrorInvalidValue;
     const size_t rb = row_bytes(type, K);

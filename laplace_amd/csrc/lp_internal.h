@@ -34,20 +34,34 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float*
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w);
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K,
                              int N, hipStream_t st);
-// Prefill GEMM (lp_gemm.hip): Q4_K weights, M > 8. `planes` is scratch of
-// gemm_planes_bytes(M, K) bytes (fp16 activation planes).
+// Q4_K products for M >= 2 activation rows (lp_gemm.hip), on the fp16
+// "planes" of the activations (gemm_planes_bytes(M, K) bytes of scratch):
+// M <= 16 on the small-M MFMA kernel, larger M on the tiled GEMM.
 bool gemm_supported(uint32_t type, int M, int K);
 size_t gemm_planes_bytes(int M, int K);
+// planes from fp32 x (quantize + planes in one pass)
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st);
+hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,
+                              hipStream_t st);
+// planes from quantized activations A, then the product
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
                        int M, int K, int N, hipStream_t st);
+// grouped MoE on the small-M MFMA kernel (groups of <= 16 pairs), planes of
+// `rows` activation rows; route from launch_moe_route with group size 16.
+bool moe_mf_supported(uint32_t type, int K);
+hipError_t launch_moe_mf(const uint8_t* w, const void* planes, int rows, const void* route, int max_groups,
+                         int multi, int topk, float* y, int K, int N, hipStream_t st);
 // Grouped MoE dispatch (lp_gemv.hip). P = T * topk pairs, E experts stacked
 // in w (E x N rows). `route` is scratch of moe_route_bytes(P, E) bytes.
+// planes != nullptr (planes of `rows` activation rows): Q4_K runs on the
+// small-M MFMA kernel in groups of <= 16 pairs; otherwise the GEMV tile
+// kernel reads A in groups of <= 4.
 constexpr int kMoeMaxExperts = 8192;
 int moe_max_groups(int P, int E);
 size_t moe_route_bytes(int P, int E);
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const int* idx,
-                              int P, int E, int multi, int topk, void* route, float* y, int K, int N,
-                              hipStream_t st);
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+                              int rows, const int* idx, int P, int E, int multi, int topk, void* route,
+                              float* y, int K, int N, hipStream_t st);
 // dequantize (lp_dequant.hip): elements per block (0 = type not handled)
 // and source bytes of n elements.
 int dequant_block_elems(uint32_t type);

@@ -269,7 +269,7 @@ def test_gemm_matches_gemv_rows(orc):
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
-@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 16])
 def test_gemm_dev_equals_two_step(t, M):
     """lp_gemm_dev (quantize + GEMV in one call) is bit-identical to
     lp_quantize_act_dev + lp_gemm_q_dev on the stored blocks, including
@@ -307,4 +307,21 @@ def test_q4k_stream_gemv_shapes(orc, K, N):
     x = synth_x(1, K, seed=7, outliers=0.01)
     y = gemm_dev(t, x, w, N)
     ref = orc.gemm_int(t, x, w, N)
+    assert normwise(y, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("K,N", [(256, 17), (512, 40), (2048, 1000), (3584, 333), (4096, 64), (18944, 48)])
+@pytest.mark.parametrize("M", [5, 9, 16])
+def test_q4k_small_m_mfma(orc, K, N, M):
+    """5 <= M <= 16 Q4_K products run on the small-M MFMA kernel (planes from
+    x in one pass, 32 weight rows x 8 K-slices per workgroup): K with fewer
+    super-blocks than K-slices, ragged N, M up to the tile height. The
+    K=3584 cases hold an fp16 rounding tie of d*q (hi and lo must come from
+    the same fp32 product)."""
+    t = Q4_K
+    w = synth_weights(t, K, N, seed=K * 7 + N + M)
+    x = synth_x(M, K, seed=M + 11, outliers=0.01)
+    y = gemm_dev(t, x, w, N)
+    ref = orc.gemm_int(t, x, w, N)
+    assert np.isfinite(y).all()
     assert normwise(y, ref) <= 1e-4
