@@ -325,3 +325,27 @@ def test_q4k_small_m_mfma(orc, K, N, M):
     ref = orc.gemm_int(t, x, w, N)
     assert np.isfinite(y).all()
     assert normwise(y, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q6_K], ids=["Q8_0", "Q4_0", "Q6_K"])
+@pytest.mark.parametrize("K,N", [(256, 7), (768, 100), (3584, 257), (14336, 33), (18944, 40), (32768, 9)])
+def test_m1_gemv_shapes(orc, t, K, N):
+    """M=1 GEMV for Q8_0 / Q4_0 / Q6_K over a range of K (rows that are not
+    16-byte multiples for Q6_K, K up to the 32768 limit), ragged N: the
+    single-call path (lp_gemm_dev) against the oracle and bit-identical to
+    the quantizer-fed path (lp_gemm_q_dev)."""
+    import torch
+    from hip_util import L, stream, to_dev, workspace
+    from laplace_amd import _lib
+    w = synth_weights(t, K, N, seed=K + 3 * N + t)
+    x = synth_x(1, K, seed=K + t, outliers=0.01)
+    ref = orc.gemm_int(t, x, w, N)
+    y = gemm_dev(t, x, w, N)
+    assert normwise(y, ref) <= 1e-4
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(1, K)
+    y2 = torch.empty(N, dtype=torch.float32, device="cuda")
+    _lib.check(L().lp_quantize_act_dev(xd.data_ptr(), 1, K, ws.data_ptr(), nb, stream()), "q")
+    _lib.check(L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), t, y2.data_ptr(), 1, K, N, stream()), "g")
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(1, N).view(np.uint32), y.view(np.uint32))
