@@ -401,6 +401,162 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K GEMV for 2..4 activation rows (and grouped MoE, groups of <= 4 pairs)
+// with the one-super-block-per-lane layout of gemv_q4k_sb: the weight bytes
+// of a row group are loaded once (coalesced, transposed through LDS) and
+// dotted with every activation row; the rows' codes, block scales and sums
+// live in LDS (per row: codes at a 272-byte super-block stride, then d, sum).
+// MOE: blockIdx.y is a routed group (expert, first pair, n <= 4 pairs); the
+// workgroup copies the group's activation rows and scatters its outputs.
+
+constexpr int kSbmMaxM = 4;
+constexpr int kSbmWaves = 4;
+
+struct SbmArgs {
+    const uint8_t* w;
+    long ebytes;          // bytes per expert (MOE)
+    ActView A;
+    float* y;
+    int K, N, M;
+    const uint8_t* route;
+    int max_groups, multi, topk;
+};
+
+template <int L, bool MOE>
+__global__ void __launch_bounds__(64 * kSbmWaves)
+gemv_q4k_sbm(SbmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int RPW = 64 / L;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.K, N = a.N;
+    const int nsb = K >> 8, nb = K >> 5;
+    const long rb = (long)nsb * 144;
+    const long total = (long)N * rb;
+    const int sl = lane & (L - 1);
+    const int rsub = lane / L;
+    const bool active = sl < nsb;
+    const int sb = active ? sl : nsb - 1;
+
+    int mg = a.M;
+    const uint8_t* w = a.w;
+    int arow[kSbmMaxM], yrow[kSbmMaxM];
+    if constexpr (MOE) {
+        if ((int)blockIdx.y >= *reinterpret_cast<const int*>(a.route)) return;
+        const int4 gd = reinterpret_cast<const int4*>(a.route + 16)[blockIdx.y];
+        const int* pairs = reinterpret_cast<const int*>(a.route + 16 + (size_t)a.max_groups * 16);
+        mg = gd.z;
+        w += (size_t)gd.x * a.ebytes;
+#pragma unroll
+        for (int m = 0; m < kSbmMaxM; m++) {
+            const int p = pairs[gd.y + (m < mg ? m : 0)];
+            arow[m] = a.multi ? p : p / a.topk;
+            yrow[m] = p;
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < kSbmMaxM; m++) arow[m] = yrow[m] = m < mg ? m : 0;
+    }
+
+    // LDS: per activation row m: [codes: nsb x 272][d: nb][sum: nb]; then per-wave buffers
+    const int act_row_bytes = (nsb * 272 + 8 * nb + 15) & ~15;
+    uint8_t* wbuf = smem + kSbmMaxM * act_row_bytes + (size_t)wave * 9216;
+    const uint32_t l0 = lds_addr_of(smem);
+    for (int m = 0; m < mg; m++) {
+        uint8_t* ar = smem + m * act_row_bytes;
+        const int8_t* q = a.A.qs + (size_t)arow[m] * K;
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x)
+            *reinterpret_cast<u32x4*>(ar + (i >> 4) * 272 + (i & 15) * 16) = reinterpret_cast<const u32x4*>(q)[i];
+        float* dlm = reinterpret_cast<float*>(ar + nsb * 272);
+        for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+            dlm[b] = a.A.d[(size_t)arow[m] * nb + b];
+            dlm[nb + b] = a.A.sum[(size_t)arow[m] * nb + b];
+        }
+    }
+    __syncthreads();
+
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    for (long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g * RPW < N; g += nwaves) {
+        const long gbeg = g * RPW * rb;
+        const long gend_full = gbeg + RPW * rb;
+        const long gend = gend_full < total ? gend_full : total;
+        u32x4 v[9];
+#pragma unroll
+        for (int k = 0; k < 9; k++) {
+            long o = gbeg + 1024 * k + 16 * lane;
+            o = o + 16 <= gend ? o : gend - 16;
+            v[k] = ld_nt16(w + o);
+        }
+#pragma unroll
+        for (int k = 0; k < 9; k++) *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v[k];
+        const u32x4* mine = reinterpret_cast<const u32x4*>(wbuf + (size_t)(rsub * nsb + sb) * 144);
+#pragma unroll
+        for (int k = 0; k < 9; k++) v[k] = mine[k];
+
+        const long row = g * RPW + rsub;
+        const u32x4 h = v[0];
+        const float d = fp16_bits_to_f32(h.x), dmin = fp16_bits_to_f32(h.x >> 16);
+        float t[kSbmMaxM] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            const u32x4 c0 = v[1 + 2 * jb], c1 = v[2 + 2 * jb];
+            const uint32_t qv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_k4(2 * jb, h.y, h.z, h.w, sc0, m0);
+            scale_min_k4(2 * jb + 1, h.y, h.z, h.w, sc1, m1);
+            const float ds0 = d * (float)sc0, ds1 = d * (float)sc1;
+            const float dm0 = -(dmin * (float)m0), dm1 = -(dmin * (float)m1);
+#pragma unroll
+            for (int m = 0; m < kSbmMaxM; m++) {
+                if (m < mg) {
+                    // volatile reads: kept here (hoisting them would cost registers per row)
+                    const uint32_t la = l0 + m * act_row_bytes + sb * 272 + 64 * jb;
+                    const uint32_t ld = l0 + m * act_row_bytes + nsb * 272 + 4 * (8 * sb + 2 * jb);
+                    u32x4 lo0, lo1, hi0, hi1;
+                    uint32_t dd[2], ss[2];
+                    lds_b128<0>(lo0, la);
+                    lds_b128<16>(lo1, la);
+                    lds_b128<32>(hi0, la);
+                    lds_b128<48>(hi1, la);
+                    lds_dwords<2>(ld, dd);
+                    lds_dwords<2>(ld + 4 * nb, ss);
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    lds_wait_v(lo0);
+                    lds_wait_v(lo1);
+                    lds_wait_v(hi0);
+                    lds_wait_v(hi1);
+                    lds_wait(dd);
+                    lds_wait(ss);
+                    const uint32_t al[8] = {lo0.x, lo0.y, lo0.z, lo0.w, lo1.x, lo1.y, lo1.z, lo1.w};
+                    const uint32_t ah[8] = {hi0.x, hi0.y, hi0.z, hi0.w, hi1.x, hi1.y, hi1.z, hi1.w};
+                    int s0 = 0, s1 = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        s0 = dot4(qv[i] & 0x0f0f0f0fu, al[i], s0);
+                        s1 = dot4((qv[i] >> 4) & 0x0f0f0f0fu, ah[i], s1);
+                    }
+                    float u = t[m];
+                    u = fmaf(ds0 * __uint_as_float(dd[0]), (float)s0, u);
+                    u = fmaf(ds1 * __uint_as_float(dd[1]), (float)s1, u);
+                    u = fmaf(dm0, __uint_as_float(ss[0]), u);
+                    u = fmaf(dm1, __uint_as_float(ss[1]), u);
+                    t[m] = u;
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < kSbmMaxM; m++) {
+            if (m < mg) {
+                const float sum = group_sum(active ? t[m] : 0.0f, L);   // lane L-1 of the group
+                if (sl == L - 1 && row < N) a.y[(size_t)yrow[m] * N + row] = sum;
+            }
+        }
+    }
+}
+
+// Launch of gemv_q4k_sbm: grid.x workgroups per weight matrix, grid.y groups.
+static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t st);
+
 // Lanes per row for the one-super-block-per-lane kernel (0: K not handled).
 static int sb_lanes(int K) {
     if (K % 256 != 0) return 0;
@@ -447,6 +603,39 @@ static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, const float*
 
 // Fused quantize + GEMV for one fp32 activation row, when the type and shape
 // have a single-launch kernel (Q4_K); false otherwise.
+static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t st) {
+    const int L = sb_lanes(args.K);
+    if (L == 0) return hipErrorInvalidValue;
+    const int rpw = 64 / L;
+    const long groups = ((long)args.N + rpw - 1) / rpw;     // row groups per matrix
+    long waves = groups;
+    if (ngroups == 1) {
+        const long cap = (long)device_cu_count() * 16;
+        if (waves > cap) waves = cap;
+    }
+    const unsigned gx = (unsigned)((waves + kSbmWaves - 1) / kSbmWaves);
+    const int nsb = args.K / 256, nb = args.K / 32;
+    const size_t shm = (size_t)kSbmMaxM * ((nsb * 272 + 8 * nb + 15) & ~15) + (size_t)kSbmWaves * 9216;
+    if (shm > 160 * 1024) return hipErrorInvalidValue;
+#define LP_S(LL)                                                                                           \
+    case LL:                                                                                               \
+        if (args.route) hipLaunchKernelGGL((gemv_q4k_sbm<LL, true>), dim3(gx, ngroups), dim3(64 * kSbmWaves), shm, st, args); \
+        else hipLaunchKernelGGL((gemv_q4k_sbm<LL, false>), dim3(gx, 1), dim3(64 * kSbmWaves), shm, st, args); \
+        break;
+    switch (L) {
+        LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_S
+    return hipGetLastError();
+}
+
+static bool sbm_supported(int K, const uint8_t* w) {
+    const int nsb = K / 256;
+    return sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+           (size_t)kSbmMaxM * ((nsb * 272 + 8 * (K / 32) + 15) & ~15) + (size_t)kSbmWaves * 9216 <= 160 * 1024;
+}
+
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w) {
     return type == T_Q4_K && M == 1 && sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
 }
@@ -468,9 +657,16 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
                     return launch_q4k_sb(w, A, nullptr, y, K, N, st);
             }
             return launch_gemv_t<T, 1>(w, A, y, K, N, st);
-        case 2: return launch_gemv_t<T, 2>(w, A, y, K, N, st);
-        case 3: return launch_gemv_t<T, 3>(w, A, y, K, N, st);
-        case 4: return launch_gemv_t<T, 4>(w, A, y, K, N, st);
+        case 2: case 3: case 4:
+            if constexpr (T == T_Q4_K) {
+                if (sbm_supported(K, w)) {
+                    SbmArgs args{w, 0, A, y, K, N, M, nullptr, 0, 0, 1};
+                    return launch_q4k_sbm(args, 1, st);
+                }
+            }
+            if (M == 2) return launch_gemv_t<T, 2>(w, A, y, K, N, st);
+            if (M == 3) return launch_gemv_t<T, 3>(w, A, y, K, N, st);
+            return launch_gemv_t<T, 4>(w, A, y, K, N, st);
         case 5: return launch_gemv_t<T, 5>(w, A, y, K, N, st);
         case 6: return launch_gemv_t<T, 6>(w, A, y, K, N, st);
         case 7: return launch_gemv_t<T, 7>(w, A, y, K, N, st);
@@ -640,6 +836,11 @@ hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A,
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (mf) return launch_moe_mf(w, planes, rows, route, mg, multi, topk, y, K, N, st);
+    if (type == T_Q4_K && sbm_supported(K, w)) {
+        SbmArgs args{w, (long)row_bytes(type, K) * N, A, y, K, N, 0, static_cast<const uint8_t*>(route), mg, multi,
+                     topk};
+        return launch_q4k_sbm(args, mg, st);
+    }
     GemvGeom g;
     if (!gemv_geom(type, kMoeGroup, K, N, 0, g)) return hipErrorInvalidValue;
     const size_t rb = row_bytes(type, K);
