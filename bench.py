@@ -124,7 +124,7 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
     nbws = int(g.L.lp_act_workspace_bytes(M, K))
     ws = torch.empty(nbws, dtype=torch.uint8, device=g.dev)
     alg_bytes = w.nbytes + 4 * M * K + 4 * M * N
-    fused = (t == Q4_K and M == 1 and K % 256 == 0 and K // 256 <= 64)
+    fused = (t in (Q4_K, Q4_0, Q8_0) and M == 1 and K % 256 == 0 and K // 256 <= 64)
 
     def step(i):
         g.check(g.L.lp_gemm_dev(xd.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),

@@ -557,6 +557,154 @@ gemv_q4k_sbm(SbmArgs a) {
 // Launch of gemv_q4k_sbm: grid.x workgroups per weight matrix, grid.y groups.
 static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t st);
 
+// ---------------------------------------------------------------------------
+// Q4_0 / Q8_0 GEMV for one activation row with the layout of gemv_q4k_sb:
+// a lane owns 8 consecutive 32-element blocks (256 elements, SBB bytes) of
+// every row its group visits, loaded coalesced and transposed through a
+// per-wave LDS buffer. Block j of the lane's span starts at byte j*bpb
+// (2-byte aligned): its fields are cut out of the loaded dwords with
+// v_alignbyte at compile-time offsets. Per block the reference's int dot
+// and fp32 terms (dot_row_q4_0_int_neon / dot_row_q8_0_int_neon,
+// src/matmul_simd.cpp:143-182).
+
+template <uint32_t T> struct B32Geom;
+template <> struct B32Geom<T_Q4_0> { static constexpr int BPB = 18; };
+template <> struct B32Geom<T_Q8_0> { static constexpr int BPB = 34; };
+
+// byte-offset extraction from the lane's span held as dwords
+template <int OFF>
+__device__ __forceinline__ uint32_t span_dword(const uint32_t* wd) {
+    if constexpr ((OFF & 3) == 0) return wd[OFF >> 2];
+    else return alignb(wd[(OFF >> 2) + 1], wd[OFF >> 2], OFF & 3);
+}
+
+template <uint32_t T, int J>
+__device__ __forceinline__ float b32_block(const uint32_t* wd, const u32x4 (&aq)[2], float xd, float xs,
+                                           float t) {
+    constexpr int BPB = B32Geom<T>::BPB;
+    constexpr int O = J * BPB;
+    const uint32_t dw = wd[O >> 2] >> (8 * (O & 3));          // O % 4 is 0 or 2: d never straddles
+    const float d = fp16_bits_to_f32(dw);
+    const uint32_t al[8] = {aq[0].x, aq[0].y, aq[0].z, aq[0].w, aq[1].x, aq[1].y, aq[1].z, aq[1].w};
+    int is = 0;
+    if constexpr (T == T_Q4_0) {
+        // nibble l (low) pairs with element l, high nibble with element l + 16
+        const uint32_t q[4] = {span_dword<O + 2>(wd), span_dword<O + 6>(wd), span_dword<O + 10>(wd),
+                               span_dword<O + 14>(wd)};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            is = dot4(q[i] & 0x0f0f0f0fu, al[i], is);
+            is = dot4((q[i] >> 4) & 0x0f0f0f0fu, al[4 + i], is);
+        }
+        t = fmaf(d * xd, (float)is, t);
+        return fmaf(-(d * 8.0f), xs, t);
+    } else {
+        const uint32_t q[8] = {span_dword<O + 2>(wd), span_dword<O + 6>(wd), span_dword<O + 10>(wd),
+                               span_dword<O + 14>(wd), span_dword<O + 18>(wd), span_dword<O + 22>(wd),
+                               span_dword<O + 26>(wd), span_dword<O + 30>(wd)};
+#pragma unroll
+        for (int i = 0; i < 8; i++) is = dot4(q[i], al[i], is);
+        return fmaf(d * xd, (float)is, t);
+    }
+}
+
+template <uint32_t T, int J = 0>
+__device__ __forceinline__ float b32_span(const uint32_t* wd, uint32_t act_l, const float (&xd)[8],
+                                          const float (&xs)[8], float t) {
+    if constexpr (J < 8) {
+        u32x4 aq[2];
+        lds_b128<32 * J>(aq[0], act_l);
+        lds_b128<32 * J + 16>(aq[1], act_l);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_wait_v(aq[0]);
+        lds_wait_v(aq[1]);
+        t = b32_block<T, J>(wd, aq, xd[J], xs[J], t);
+        return b32_span<T, J + 1>(wd, act_l, xd, xs, t);
+    } else {
+        return t;
+    }
+}
+
+template <uint32_t T, int L, bool FUSEQ>
+__global__ void __launch_bounds__(1024)
+gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
+            int K, int N, int wbuf_bytes) {
+    constexpr int SBB = 8 * B32Geom<T>::BPB;      // 144 (Q4_0) or 272 (Q8_0)
+    constexpr int NV = SBB / 16;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int RPW = 64 / L;
+    const int lane = threadIdx.x & 63;
+    const int nsb = K >> 8, nb = K >> 5;
+    const long rb = (long)nsb * SBB;
+    const long total = (long)N * rb;
+    const int sl = lane & (L - 1);
+    const int rsub = lane / L;
+    const bool active = sl < nsb;
+    const int sb = active ? sl : nsb - 1;
+    float* dl = reinterpret_cast<float*>(smem + nsb * 272);
+    float* sl_ = dl + nb;
+    const int xbuf_off = (nsb * 272 + 8 * nb + 15) & ~15;
+    uint8_t* wbuf = smem + xbuf_off + (size_t)(threadIdx.x >> 6) * wbuf_bytes;
+    const uint32_t act_l = lds_addr_of(smem) + sb * 272;
+
+    float xd[8], xs[8];
+    if constexpr (FUSEQ) {
+        for (int i = threadIdx.x; i < (K >> 2); i += blockDim.x) {
+            const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
+            const int b = i >> 3, gq = i & 7;
+            *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+            if (gq == 0) {
+                dl[b] = q.d;
+                sl_[b] = q.sum;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            xd[k] = dl[8 * sb + k];
+            xs[k] = sl_[8 * sb + k];
+        }
+    } else {
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            xd[k] = A.d[8 * sb + k];
+            xs[k] = A.sum[8 * sb + k];
+        }
+        __syncthreads();
+    }
+
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    for (long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g * RPW < N; g += nwaves) {
+        const long gbeg = g * RPW * rb;
+        const long gend_full = gbeg + RPW * rb;
+        const long gend = gend_full < total ? gend_full : total;
+        const int nld = (int)((gend - gbeg + 1023) / 1024);
+        for (int k = 0; k < nld; k++) {
+            long a = gbeg + 1024 * k + 16 * lane;
+            a = a + 16 <= gend ? a : gend - 16;
+            const u32x4 v = ld_nt16(w + a);
+            *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v;
+        }
+        const u32x4* mine = reinterpret_cast<const u32x4*>(wbuf + (size_t)(rsub * nsb + sb) * SBB);
+        uint32_t wd[4 * NV + 1];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const u32x4 v = mine[k];
+            wd[4 * k] = v.x; wd[4 * k + 1] = v.y; wd[4 * k + 2] = v.z; wd[4 * k + 3] = v.w;
+        }
+        wd[4 * NV] = 0;                           // alignbyte partner past the span end (unused bytes)
+        float t = b32_span<T>(wd, act_l, xd, xs, 0.0f);
+        t = active ? t : 0.0f;
+        const long row = g * RPW + rsub;
+        const float sum = group_sum(t, L);
+        if (sl == L - 1 && row < N) y[row] = sum;
+    }
+}
+
 // Lanes per row for the one-super-block-per-lane kernel (0: K not handled).
 static int sb_lanes(int K) {
     if (K % 256 != 0) return 0;
@@ -630,6 +778,41 @@ static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t s
     return hipGetLastError();
 }
 
+template <uint32_t T>
+static hipError_t launch_b32_sb(const uint8_t* w, const ActView& A, const float* x, float* y, int K, int N,
+                                hipStream_t st) {
+    constexpr int SBB = 8 * B32Geom<T>::BPB;
+    const int L = sb_lanes(K);
+    if (L == 0) return hipErrorInvalidValue;
+    const int rpw = 64 / L;
+    const int nsb = K / 256;
+    const int wbuf = ((rpw * nsb * SBB + 1023) / 1024) * 1024;
+    const size_t act_lds = ((size_t)nsb * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
+    int wg = x ? 16 : 8;
+    while (wg > 1 && act_lds + (size_t)wg * wbuf > 160 * 1024) wg >>= 1;
+    const long groups = ((long)N + rpw - 1) / rpw;
+    long waves = groups;
+    const long cap = (long)device_cu_count() * 16;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + wg - 1) / wg);
+    const size_t shm = act_lds + (size_t)wg * wbuf;
+#define LP_S(LL)                                                                                             \
+    case LL:                                                                                                 \
+        if (x) hipLaunchKernelGGL((gemv_b32_sb<T, LL, true>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
+        else hipLaunchKernelGGL((gemv_b32_sb<T, LL, false>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
+        break;
+    switch (L) {
+        LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_S
+    return hipGetLastError();
+}
+
+static bool b32_sb_supported(uint32_t type, int K, const uint8_t* w) {
+    return (type == T_Q4_0 || type == T_Q8_0) && sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 4 == 0;
+}
+
 static bool sbm_supported(int K, const uint8_t* w) {
     const int nsb = K / 256;
     return sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
@@ -637,14 +820,18 @@ static bool sbm_supported(int K, const uint8_t* w) {
 }
 
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w) {
-    return type == T_Q4_K && M == 1 && sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    if (M != 1) return false;
+    if (type == T_Q4_K) return sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    return b32_sb_supported(type, K, w);
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K,
                              int N, hipStream_t st) {
     if (!gemv_fused_supported(type, M, K, w)) return hipErrorInvalidValue;
     if (N <= 0) return hipSuccess;
-    return launch_q4k_sb(w, ActView{}, x, y, K, N, st);
+    if (type == T_Q4_K) return launch_q4k_sb(w, ActView{}, x, y, K, N, st);
+    if (type == T_Q4_0) return launch_b32_sb<T_Q4_0>(w, ActView{}, x, y, K, N, st);
+    return launch_b32_sb<T_Q8_0>(w, ActView{}, x, y, K, N, st);
 }
 
 template <uint32_t T>
@@ -655,6 +842,8 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
             if constexpr (T == T_Q4_K) {
                 if (sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0)
                     return launch_q4k_sb(w, A, nullptr, y, K, N, st);
+            } else if constexpr (T == T_Q4_0 || T == T_Q8_0) {
+                if (b32_sb_supported(T, K, w)) return launch_b32_sb<T>(w, A, nullptr, y, K, N, st);
             }
             return launch_gemv_t<T, 1>(w, A, y, K, N, st);
         case 2: case 3: case 4:
