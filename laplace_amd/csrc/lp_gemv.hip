@@ -705,6 +705,261 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K GEMV for 1..4 activation rows, one 210-byte super-block per lane
+// (lanes cover super-blocks l, l + L, ... of a row; L <= 64, so K up to
+// 32768 takes at most two per lane). The lane loads its super-block with
+// cached 16-byte loads from the 4-byte aligned address below it (plus one
+// dword when it starts 2 bytes into a dword; d with a 16-bit load, so no
+// load passes the block's end), funnel-shifts it to dword alignment and
+// builds the 6-bit codes v = ql nibble | (qh bits << 4) once for all rows.
+// Per 16 elements the reference's integer sum sum(v*q) - 32*sum(q) and fp32
+// term (d*xd)*sc*is (dot_row_q6_k_int_neon, src/matmul_simd.cpp:285-342).
+// The activation rows sit in LDS: codes at a 272-byte super-block stride,
+// then per block d and the two 16-element code sums.
+
+constexpr int kQ6Waves = 8;
+
+// One Q6_K super-block (raw: its 210 bytes from the dword at or below its start,
+// shifted by sh bytes) against M activation rows in LDS; adds into t[m].
+template <int M>
+__device__ __forceinline__ void q6_sb_dot(const uint32_t (&raw)[53], uint32_t sh, float d, int sb, uint32_t l0,
+                                          int arb, int nsb, int nb, float (&t)[M]) {
+    uint32_t wd[52];
+#pragma unroll
+    for (int k = 0; k < 52; k++) wd[k] = alignb(raw[k + 1], raw[k], sh);
+    // ql: wd[0..31], qh: wd[32..47], scales: wd[48..51]. Per half n (128 elements)
+    // and row m all LDS reads issue together: 8 x 16 B codes, the 4 block scales
+    // and the 8 sixteen-element code sums, then one wait.
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const uint32_t la = l0 + m * arb + sb * 272 + 128 * n;
+            const uint32_t ld = l0 + m * arb + nsb * 272 + 32 * sb + 16 * n;
+            const uint32_t lq = l0 + m * arb + nsb * 272 + 4 * nb + 64 * sb + 32 * n;
+            u32x4 a[8], dv, q0, q1;
+            lds_b128<0>(dv, ld);
+            lds_b128<0>(q0, lq);     lds_b128<16>(q1, lq);
+            lds_b128<0>(a[0], la);   lds_b128<16>(a[1], la);
+            lds_b128<32>(a[2], la);  lds_b128<48>(a[3], la);
+            lds_b128<64>(a[4], la);  lds_b128<80>(a[5], la);
+            lds_b128<96>(a[6], la);  lds_b128<112>(a[7], la);
+            // LDS reads complete in order: group gg needs the first 5 + 2 gg of them
+            asm volatile("s_waitcnt lgkmcnt(6)" ::: "memory");
+            lds_wait_v(dv); lds_wait_v(q0); lds_wait_v(q1); lds_wait_v(a[0]); lds_wait_v(a[1]);
+            const float xd[4] = {__uint_as_float(dv.x), __uint_as_float(dv.y), __uint_as_float(dv.z),
+                                 __uint_as_float(dv.w)};
+            const uint32_t qs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            float u = t[m];
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) {
+                uint32_t v[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t ql = wd[16 * n + 8 * (gg & 1) + k];
+                    const uint32_t qh = wd[32 + 8 * n + k];
+                    v[k] = ((ql >> (4 * (gg >> 1))) & 0x0f0f0f0fu) | (((qh >> (2 * gg)) & 0x03030303u) << 4);
+                }
+                const int si = 8 * n + 2 * gg;         // scale of elements 0..15; si + 1 for 16..31
+                const float sc0 = (float)(int8_t)((wd[48 + (si >> 2)] >> (8 * (si & 3))) & 0xffu);
+                const float sc1 = (float)(int8_t)((wd[48 + ((si + 1) >> 2)] >> (8 * ((si + 1) & 3))) & 0xffu);
+                if (gg == 1) {
+                    asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+                    lds_wait_v(a[2]); lds_wait_v(a[3]);
+                } else if (gg == 2) {
+                    asm volatile("s_waitcnt lgkmcnt(2)" ::: "memory");
+                    lds_wait_v(a[4]); lds_wait_v(a[5]);
+                } else if (gg == 3) {
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    lds_wait_v(a[6]); lds_wait_v(a[7]);
+                }
+                const u32x4 a0 = a[2 * gg], a1 = a[2 * gg + 1];
+                int s0 = 0, s1 = 0;
+                s0 = dot4(v[0], a0.x, s0); s0 = dot4(v[1], a0.y, s0);
+                s0 = dot4(v[2], a0.z, s0); s0 = dot4(v[3], a0.w, s0);
+                s1 = dot4(v[4], a1.x, s1); s1 = dot4(v[5], a1.y, s1);
+                s1 = dot4(v[6], a1.z, s1); s1 = dot4(v[7], a1.w, s1);
+                s0 -= 32 * (int)qs[2 * gg];
+                s1 -= 32 * (int)qs[2 * gg + 1];
+                const float dx = d * xd[gg];
+                u = fmaf(dx * sc0, (float)s0, u);
+                u = fmaf(dx * sc1, (float)s1, u);
+            }
+            t[m] = u;
+        }
+    }
+}
+
+template <int L, int M>
+__global__ void __launch_bounds__(64 * kQ6Waves)
+gemv_q6k_sbm(const uint8_t* __restrict__ w, ActView A, int arow0, float* __restrict__ y, int K, int N) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int RPW = 64 / L;
+    const int lane = threadIdx.x & 63;
+    const int nsb = K >> 8, nb = K >> 5;
+    const long rb = (long)nsb * 210;
+    const int sl = lane & (L - 1);
+    const int rsub = lane / L;
+    // LDS per row m: [codes: nsb x 272][d: nb floats][qsum: 2 x nb ints]
+    const int arb = (nsb * 272 + 12 * nb + 15) & ~15;
+    // The first super-block's loads issue before the activation staging, so their
+    // latency overlaps it. raw always holds the lane's next super-block.
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    const int sl0 = sl < nsb ? sl : nsb - 1;
+    u32x4 rw[13];
+    uint32_t tail, dh, sh, l0 = 0;
+    long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    auto row_of = [&](long gg) { const long r = gg * RPW + rsub; return r < N ? r : (long)N - 1; };
+    // Untracked loads: the caller waits with s_waitcnt vmcnt(0) and fences the registers.
+    auto load = [&](long row, int sb) {
+        const uint8_t* blk = w + row * rb + (long)sb * 210;
+        const uintptr_t ab = reinterpret_cast<uintptr_t>(blk);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(ab & ~uintptr_t(3));
+        sh = (uint32_t)(ab & 3);                              // 0 or 2
+        asm volatile(
+            "global_load_dwordx4 %0, %13, off\n"
+            "global_load_dwordx4 %1, %13, off offset:16\n"
+            "global_load_dwordx4 %2, %13, off offset:32\n"
+            "global_load_dwordx4 %3, %13, off offset:48\n"
+            "global_load_dwordx4 %4, %13, off offset:64\n"
+            "global_load_dwordx4 %5, %13, off offset:80\n"
+            "global_load_dwordx4 %6, %13, off offset:96\n"
+            "global_load_dwordx4 %7, %13, off offset:112\n"
+            "global_load_dwordx4 %8, %13, off offset:128\n"
+            "global_load_dwordx4 %9, %13, off offset:144\n"
+            "global_load_dwordx4 %10, %13, off offset:160\n"
+            "global_load_dwordx4 %11, %13, off offset:176\n"
+            "global_load_dwordx4 %12, %13, off offset:192\n"
+            : "=&v"(rw[0]), "=&v"(rw[1]), "=&v"(rw[2]), "=&v"(rw[3]), "=&v"(rw[4]), "=&v"(rw[5]), "=&v"(rw[6]),
+              "=&v"(rw[7]), "=&v"(rw[8]), "=&v"(rw[9]), "=&v"(rw[10]), "=&v"(rw[11]), "=&v"(rw[12])
+            : "v"(base));
+        // dword 52 (block bytes 206..209) only when the block starts at byte 2 of a dword;
+        // else dword 51 again, so no load passes the block's end
+        asm volatile("global_load_dword %0, %1, off" : "=v"(tail) : "v"(base + (sh ? 208 : 204)));
+        asm volatile("global_load_ushort %0, %1, off" : "=v"(dh) : "v"(blk + 208));
+    };
+    auto wait_load = [&]() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 13; k++) asm volatile("" : "+v"(rw[k]));
+        asm volatile("" : "+v"(tail), "+v"(dh));
+    };
+    auto dot = [&](int sb, float (&t)[M]) {
+        uint32_t raw[53];
+#pragma unroll
+        for (int k = 0; k < 13; k++) {
+            raw[4 * k] = rw[k].x; raw[4 * k + 1] = rw[k].y; raw[4 * k + 2] = rw[k].z; raw[4 * k + 3] = rw[k].w;
+        }
+        raw[52] = tail;
+        q6_sb_dot<M>(raw, sh, fp16_bits_to_f32((uint16_t)dh), sb, l0, arb, nsb, nb, t);
+    };
+    load(row_of(g), sl0);           // unconditional: row_of clamps past-the-end groups
+    for (int m = 0; m < M; m++) {
+        uint8_t* ar = smem + m * arb;
+        const int8_t* q = A.qs + (size_t)(arow0 + m) * K;
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(q)[i];
+            *reinterpret_cast<u32x4*>(ar + (i >> 4) * 272 + (i & 15) * 16) = v;
+            const uint32_t qv[4] = {v.x, v.y, v.z, v.w};
+            int qs16 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs16 = dot4(qv[k], 0x01010101u, qs16);
+            reinterpret_cast<int*>(ar + nsb * 272 + 4 * nb)[i] = qs16;    // 16-element sum i
+        }
+        float* dl = reinterpret_cast<float*>(ar + nsb * 272);
+        for (int b = threadIdx.x; b < nb; b += blockDim.x) dl[b] = A.d[(size_t)(arow0 + m) * nb + b];
+    }
+    __syncthreads();
+    l0 = lds_addr_of(smem);
+    wait_load();
+    // Every load is waited in the block that issued it, so no value still in flight
+    // reaches a control-flow merge (where the compiler may copy registers).
+    bool first = true;
+    for (; g * RPW < N; g += nwaves) {
+        const long row = row_of(g);
+        const bool rv = g * RPW + rsub < N;
+        if (!first) {
+            load(row, sl0);
+            wait_load();
+        }
+        first = false;
+        float t[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) t[m] = 0.0f;
+        if (sl < nsb) dot(sl, t);
+        for (int sb = sl + L; sb < nsb; sb += L) {
+            load(row, sb);
+            wait_load();
+            dot(sb, t);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float sum = group_sum(t[m], L);          // lands in lane L-1 of the group
+            if (sl == L - 1 && rv) y[(size_t)m * N + row] = sum;
+        }
+    }
+}
+
+static int q6_lanes(int K) {
+    if (K % 256 != 0) return 0;
+    const int nsb = K / 256;
+    // At most 32 lanes per row: a long row (K = 18944: 74 super-blocks) then takes 3
+    // rounds per lane over 2 rows per wave, measured faster than 64 lanes x 2 rounds
+    // (58% of the second round idle) or 16 lanes x 5 rounds.
+    int L = 2;
+    while (L < nsb && L < 32) L <<= 1;
+    return L;
+}
+
+// rows arow0 .. arow0 + M - 1 of A -> y rows 0 .. M-1
+template <int M>
+static hipError_t launch_q6k_sbm_m(const uint8_t* w, const ActView& A, int arow0, float* y, int K, int N,
+                                   hipStream_t st) {
+    const int L = q6_lanes(K);
+    const int nsb = K / 256, nb = K / 32;
+    const size_t shm = (size_t)M * ((nsb * 272 + 12 * nb + 15) & ~15);
+    if (L == 0 || shm > 160 * 1024) return hipErrorInvalidValue;
+    const int rpw = 64 / L;
+    const long groups = ((long)N + rpw - 1) / rpw;
+    long waves = groups;
+    const long cap = (long)device_cu_count() * 16;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + kQ6Waves - 1) / kQ6Waves);
+#define LP_S(LL) case LL: hipLaunchKernelGGL((gemv_q6k_sbm<LL, M>), dim3(grid), dim3(64 * kQ6Waves), shm, st, w, A, arow0, y, K, N); break;
+    switch (L) {
+        LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32)
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_S
+    return hipGetLastError();
+}
+
+static bool q6k_sbm_supported(int K, int M, const uint8_t* w) {
+    const int nsb = K / 256, nb = K / 32;
+    const int mm = M < 4 ? M : 4;
+    return q6_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 2 == 0 &&
+           (size_t)mm * ((nsb * 272 + 12 * nb + 15) & ~15) <= 160 * 1024;
+}
+
+// M = 1..8 rows: in passes of up to 4 (each pass re-reads the weights)
+static hipError_t launch_q6k_sbm(const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
+                                 hipStream_t st) {
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int mt = M - m0 < 4 ? M - m0 : 4;
+        float* yp = y + (size_t)m0 * N;
+        hipError_t e;
+        switch (mt) {
+            case 1: e = launch_q6k_sbm_m<1>(w, A, m0, yp, K, N, st); break;
+            case 2: e = launch_q6k_sbm_m<2>(w, A, m0, yp, K, N, st); break;
+            case 3: e = launch_q6k_sbm_m<3>(w, A, m0, yp, K, N, st); break;
+            default: e = launch_q6k_sbm_m<4>(w, A, m0, yp, K, N, st); break;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 // Lanes per row for the one-super-block-per-lane kernel (0: K not handled).
 static int sb_lanes(int K) {
     if (K % 256 != 0) return 0;
@@ -837,6 +1092,9 @@ hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, fl
 template <uint32_t T>
 static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y, int M, int K,
                                    int N, hipStream_t st) {
+    if constexpr (T == T_Q6_K) {
+        if (q6k_sbm_supported(K, M, w)) return launch_q6k_sbm(w, A, y, M, K, N, st);
+    }
     switch (M) {
         case 1:
             if constexpr (T == T_Q4_K) {

@@ -358,3 +358,15 @@ def test_m1_gemv_shapes(orc, t, K, N):
     _lib.check(L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), t, y2.data_ptr(), 1, K, N, stream()), "g")
     torch.cuda.synchronize()
     assert np.array_equal(y2.cpu().numpy().reshape(1, N).view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
+@pytest.mark.parametrize("K,N", [(256, 7), (3584, 65), (18944, 40), (32768, 5)])
+def test_q6k_multi_row_gemv(orc, K, N, M):
+    """Q6_K GEMV for 2..8 activation rows (4 rows per weight pass; 5..8 take
+    two passes) over ragged N against the oracle, with activation outliers."""
+    _flush(f"q6k multi-row K={K} N={N} M={M}")
+    w = synth_weights(Q6_K, K, N, seed=K + 7 * N + M)
+    x = synth_x(M, K, seed=K + M, outliers=0.01)
+    y = gemm_dev(Q6_K, x, w, N)
+    assert normwise(y, orc.gemm_int(Q6_K, x, w, N)) <= 1e-4
