@@ -27,10 +27,12 @@
 // K step 64 (a quarter super-block). Each wave owns 64 x 64 = 2 x 2 MFMA
 // tiles of 32 x 32 (v_mfma_f32_32x32x16_f16). Per K step, the activation
 // hi/lo planes (32 KB) and the raw 4-bit codes of the weight rows (8 KB)
-// are copied into LDS with global_load_lds_dwordx4 (1 KiB per wave
-// instruction), double buffered; super-block headers and activation sums
-// are staged once per super-block. The 4-bit codes are turned into fp16 V
-// in registers (v_perm + magic-number packed-fp16 FMA).
+// are copied into LDS with buffer_load_dwordx4 ... lds (1 KiB per wave
+// instruction, scalar per-step offsets), three stages in flight; super-block
+// headers and activation sums are staged once per super-block. The 4-bit
+// codes become fp16 V in registers (v_bfi_b32 into the fp16 1024 + n pattern,
+// then one packed-fp16 FMA per pair), decoded between the MFMAs of the
+// previous K=16 sub-step.
 #include <hip/hip_runtime.h>
 
 #include "lp_chunks.h"
@@ -47,7 +49,8 @@ constexpr int kPlaneChunk = 1024;   // elements per workgroup in the plane kerne
 
 // ---------------------------------------------------------------------------
 // Activation planes for the GEMM, built from the quantized activations.
-//   hi, lo : fp16 [M][K]        xd*q*2^-E_m split into two fp16
+//   hi, lo : fp16 [M][K]        xd*q*2^-E_m split into two fp16; each group of
+//                               four elements stored in the order k0 k2 k1 k3
 //   shi, slo : fp16 [M][K/32]   xs*2^-E_m split likewise
 //   escale : f32 [M]            2^E_m (applied to the row's outputs)
 // E_m = exponent of max_b xd_mb, so |xd*q*2^-E| <= 127.
@@ -93,8 +96,9 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
             vh[c] = h;
             vl[c] = (_Float16)(v - (float)h);
         }
-        *reinterpret_cast<h4*>(hi + (size_t)m * K + k) = vh;
-        *reinterpret_cast<h4*>(lo + (size_t)m * K + k) = vl;
+        // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
+        *reinterpret_cast<h4*>(hi + (size_t)m * K + k) = h4{vh[0], vh[2], vh[1], vh[3]};
+        *reinterpret_cast<h4*>(lo + (size_t)m * K + k) = h4{vl[0], vl[2], vl[1], vl[3]};
         if ((k & 31) == 0) {
             const int b = k >> 5;
             float v = s[b] * inv;
@@ -109,7 +113,6 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
 // ---------------------------------------------------------------------------
 
 constexpr int BM = 128, BN = 256, BK = 64;
-constexpr int kGemmThreads = 512;
 constexpr int A_PLANE = BM * BK * 2;          // 16 KB per plane per stage
 constexpr int B_TILE = BN * 32;               // 8 KB of codes per stage
 constexpr int STAGE = 2 * A_PLANE + B_TILE;   // 40 KB
@@ -119,8 +122,17 @@ constexpr int SB_STAGE = HDR + 2 * XS;        // 8 KB
 constexpr int NSTAGE = 3;                     // K-step buffers in flight
 constexpr int GEMM_LDS = NSTAGE * STAGE + 2 * SB_STAGE;   // 136 KB
 
-__device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// Buffer-resource copies straight into LDS: the per-lane byte offset is fixed
+// for the whole tile and a K step only changes the scalar offset, so the copy
+// addresses cost no vector instructions. LDS destination: the wave-uniform
+// base plus 16 bytes per lane.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+    // 0x00020000: the raw-buffer configuration word of the gfx9 family
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void dma16(Rsrc r, uint32_t voff, uint32_t soff, uint8_t* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
 struct GemmArgs {
@@ -143,88 +155,128 @@ struct GemmArgs {
 __device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 7; }
 
 // Per-lane source offsets of this wave's copies, fixed for the whole tile;
-// a K step only adds a wave-uniform offset.
+// a K step only changes the scalar offset. Rows past M or N are clamped to
+// the last one (their results are not stored). A stage holds 32 activation
+// copies (16 per plane, 8 token rows x 128 B each), 8 weight-code copies (32
+// rows x 2 halves x 16 B) and, per super-block, 8 more (4 x 64 header rows,
+// 2 planes x 2 x 64 activation-sum rows); wave w takes an equal share of each.
+template <int NW>
 struct DmaPlan {
-    uint32_t a_off[4];      // element offset into the hi or lo plane
-    const _Float16* a_plane[4];
-    uint32_t a_lds[4];      // LDS byte offset inside a stage
-    const uint8_t* b_src;   // weight codes: row base + 16 + 16 * half
-    const uint8_t* sb_src;  // header row base (waves 0-3) or xs row base (waves 4-7)
-    uint32_t sb_lds;
+    static constexpr int NA = 32 / NW, NB = 8 / NW, NS = 8 / NW;
+    Rsrc a_rs[2];           // hi, lo planes from the tile's first token row
+    uint32_t a_off[NA];     // byte offsets of the wave's activation copies
+    uint32_t a_plane[NA];   // plane of each copy (wave-uniform)
+    uint32_t a_lds[NA];     // LDS byte offset inside a stage
+    Rsrc w_rs;              // weight rows from the tile's first row
+    uint32_t b_off[NB];     // weight codes: row + 16 + 16 * half
+    uint32_t b_lds[NB];
+    Rsrc s_rs[NS];          // headers (w_rs) or an activation-sum plane
+    uint32_t s_off[NS];
+    uint32_t s_lds[NS];
+    uint32_t s_hdr[NS];     // 1: header copy (stride 144 per super-block), 0: sums (16)
 };
 
-__device__ __forceinline__ DmaPlan make_plan(const GemmArgs& g, int m0, int n0, int wave, int lane) {
-    DmaPlan d;
+template <int NW>
+__device__ __forceinline__ DmaPlan<NW> make_plan(const GemmArgs& g, int m0, int n0, int wave, int lane) {
+    using P = DmaPlan<NW>;
+    P d;
+    const int mt = g.M - m0 < BM ? g.M - m0 : BM;     // token rows in this tile
+    const int nt = g.N - n0 < BN ? g.N - n0 : BN;     // weight rows in this tile
+    const uint32_t kb = (uint32_t)g.K * 2;            // plane row bytes
+    d.a_rs[0] = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * kb);
+    d.a_rs[1] = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * kb);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int p = wave * 4 + i;                   // 0..31: 16 per plane
+    for (int i = 0; i < P::NA; i++) {
+        const int p = wave * P::NA + i;               // 0..31: 16 per plane
         const int plane = p >> 4, pp = p & 15;
         const int row = pp * 8 + (lane >> 3);
         const int piece = (lane & 7) ^ a_swz(row);
-        int gm = m0 + row;
-        gm = gm < g.M ? gm : g.M - 1;
-        d.a_off[i] = (uint32_t)gm * (uint32_t)g.K + (uint32_t)piece * 8;
-        d.a_plane[i] = plane ? g.lo : g.hi;
+        const int r = row < mt ? row : mt - 1;
+        d.a_off[i] = (uint32_t)r * kb + (uint32_t)piece * 16;
+        d.a_plane[i] = plane;
         d.a_lds[i] = plane * A_PLANE + pp * 1024;
     }
-    {
-        int gn = n0 + wave * 32 + (lane & 31);
-        gn = gn < g.N ? gn : g.N - 1;
-        d.b_src = g.w + (size_t)gn * g.rb + 16 + 16 * (lane >> 5);
+    d.w_rs = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+#pragma unroll
+    for (int i = 0; i < P::NB; i++) {
+        const int c = wave * P::NB + i;               // 32-row group
+        int r = c * 32 + (lane & 31);
+        r = r < nt ? r : nt - 1;
+        d.b_off[i] = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
+        d.b_lds[i] = 2 * A_PLANE + c * 1024;
     }
-    if (wave < 4) {
-        int gn = n0 + wave * 64 + lane;
-        gn = gn < g.N ? gn : g.N - 1;
-        d.sb_src = g.w + (size_t)gn * g.rb;
-        d.sb_lds = wave * 1024;
-    } else {
-        const int plane = (wave - 4) >> 1, part = (wave - 4) & 1;
-        int gm = m0 + part * 64 + lane;
-        gm = gm < g.M ? gm : g.M - 1;
-        d.sb_src = reinterpret_cast<const uint8_t*>((plane ? g.slo : g.shi) + (size_t)gm * (g.K >> 5));
-        d.sb_lds = HDR + plane * XS + part * 1024;
+    const int nbk = g.K >> 5;
+#pragma unroll
+    for (int i = 0; i < P::NS; i++) {
+        const int c = wave * P::NS + i;
+        if (c < 4) {
+            int r = c * 64 + lane;
+            r = r < nt ? r : nt - 1;
+            d.s_rs[i] = d.w_rs;
+            d.s_off[i] = (uint32_t)((size_t)r * g.rb);
+            d.s_lds[i] = c * 1024;
+            d.s_hdr[i] = 1;
+        } else {
+            const int plane = (c - 4) >> 1, part = (c - 4) & 1;
+            int r = part * 64 + lane;
+            r = r < mt ? r : mt - 1;
+            d.s_rs[i] = make_rsrc((plane ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
+            d.s_off[i] = (uint32_t)(r * nbk * 2);
+            d.s_lds[i] = HDR + plane * XS + part * 1024;
+            d.s_hdr[i] = 0;
+        }
     }
     return d;
 }
 
 // Copies of K step kt into stage `st` (+ super-block data into `sbb` when
 // kt starts a super-block). Returns the number of DMA instructions issued.
-__device__ __forceinline__ int issue_kstep(const DmaPlan& d, int wave, int kt, uint8_t* st,
-                                           uint8_t* sbb) {
+template <int NW>
+__device__ __forceinline__ int issue_kstep(const DmaPlan<NW>& d, int kt, uint8_t* st, uint8_t* sbb) {
+    using P = DmaPlan<NW>;
     const int sb = kt >> 2, jb = kt & 3;
 #pragma unroll
-    for (int i = 0; i < 4; i++) dma16(d.a_plane[i] + d.a_off[i] + kt * BK, st + d.a_lds[i]);
-    dma16(d.b_src + sb * 144 + 32 * jb, st + 2 * A_PLANE + wave * 1024);
+    for (int i = 0; i < P::NA; i++)
+        dma16(d.a_plane[i] ? d.a_rs[1] : d.a_rs[0], d.a_off[i], (uint32_t)(kt * BK * 2), st + d.a_lds[i]);
+#pragma unroll
+    for (int i = 0; i < P::NB; i++) dma16(d.w_rs, d.b_off[i], (uint32_t)(sb * 144 + 32 * jb), st + d.b_lds[i]);
     if (jb == 0) {
-        dma16(d.sb_src + (wave < 4 ? sb * 144 : sb * 16), sbb + d.sb_lds);
-        return 6;
+#pragma unroll
+        for (int i = 0; i < P::NS; i++)
+            dma16(d.s_rs[i], d.s_off[i], (uint32_t)(d.s_hdr[i] ? sb * 144 : sb * 16), sbb + d.s_lds[i]);
+        return P::NA + P::NB + P::NS;
     }
-    return 5;
+    return P::NA + P::NB;
 }
 
 __device__ __forceinline__ void wait_dma(int outstanding) {
     // gfx9 s_waitcnt: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
     switch (outstanding) {
 #define LP_W(i) case i: __builtin_amdgcn_s_waitcnt(((i) & 15) | (7 << 4) | (15 << 8) | (((i) >> 4) << 14)); break;
-        LP_W(5) LP_W(6) LP_W(10) LP_W(11) LP_W(12)
+        LP_W(1) LP_W(2) LP_W(3) LP_W(4) LP_W(5) LP_W(6) LP_W(7) LP_W(8) LP_W(9) LP_W(10) LP_W(11) LP_W(12)
+        LP_W(13) LP_W(14) LP_W(15) LP_W(16) LP_W(17) LP_W(18) LP_W(19) LP_W(20) LP_W(21) LP_W(22) LP_W(23)
+        LP_W(24) LP_W(25) LP_W(26) LP_W(27) LP_W(28) LP_W(29) LP_W(30) LP_W(31) LP_W(32) LP_W(33) LP_W(34)
+        LP_W(35) LP_W(36) LP_W(37) LP_W(38) LP_W(39) LP_W(40)
 #undef LP_W
         default: __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); break;
     }
 }
 
-__device__ __forceinline__ uint32_t pick2(uint32_t u, int a) {
-    // bytes a and a+1 of u into bits 0-7 and 16-23 (others zero)
-    return __builtin_amdgcn_perm(0u, u, (uint32_t)a | (4u << 8) | ((uint32_t)(a + 1) << 16) | (4u << 24));
-}
-
-// 8 codes (bytes b0..b7 in u0,u1; nibble half `hi`) -> 8 fp16 V = sc * nibble.
+// 8 codes (bytes b0..b7 in u0,u1; nibble half `hi`) -> 8 fp16 V = sc * nibble,
+// in the order b0 b2 b1 b3 b4 b6 b5 b7: masking a dword's nibbles into fp16
+// 1024 + n (or 1024 + 16n) yields bytes 0 and 2 in one step and, after a
+// shift by 8, bytes 1 and 3. The activation planes store each group of four
+// elements in the same order (k0 k2 k1 k3), so every MFMA sums the same
+// products as the natural order.
 __device__ __forceinline__ h8 decode_v(uint32_t u0, uint32_t u1, bool hi_nib, h2 mul, h2 add) {
     const uint32_t mask = hi_nib ? 0x00f000f0u : 0x000f000fu;
     h8 out;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const uint32_t x = pick2(t < 2 ? u0 : u1, (2 * t) & 3);
-        const uint32_t mg = (x & mask) | 0x64006400u;          // fp16 1024 + n (or 1024 + 16n)
+        const uint32_t u = t < 2 ? u0 : u1;
+        // (x & mask) | (0x64006400 & ~mask) in one v_bfi_b32 (the two fields are disjoint)
+        uint32_t mg;
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(mg) : "v"(mask), "v"((t & 1) ? (u >> 8) : u), "s"(0x64006400u));
         const h2 hv = __builtin_bit_cast(h2, mg);
         const h2 v = __builtin_elementwise_fma(hv, mul, add);  // (h - 1024) * scale, exact
         out[2 * t] = v[0];
@@ -252,6 +304,28 @@ __device__ __forceinline__ void lds_rd128u(u32x4& out, uint32_t a) {
 template <int OFF>
 __device__ __forceinline__ void lds_rd64(uint2& out, uint32_t a) {
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(out) : "v"(a), "n"(OFF));
+}
+
+// Activation hi/lo fragments of the wave's two token tiles for one K=16 sub-step.
+struct AFrag {
+    h8 hi[2], lo[2];
+};
+
+template <int S>
+__device__ __forceinline__ void read_afrag(AFrag& o, uint32_t stage_off, const uint32_t a_base[2], const int a_x[2]) {
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        // piece (2S + lane/32) ^ swz: the lane/32 term is folded into a_x
+        const uint32_t a = a_base[tt] + stage_off + (uint32_t)(((2 * S) ^ a_x[tt]) * 16);
+        lds_rd128<0>(o.hi[tt], a);
+        lds_rd128<A_PLANE>(o.lo[tt], a);
+    }
+}
+
+// Wait until at most N LDS reads are outstanding (LDS reads complete in order).
+template <int N>
+__device__ __forceinline__ void wait_afrag(AFrag& o) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(o.hi[0]), "+v"(o.hi[1]), "+v"(o.lo[0]), "+v"(o.lo[1]) : "n"(N));
 }
 
 // Operands of one K=16 sub-step: activation hi/lo fragments of the wave's two
@@ -306,18 +380,24 @@ __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
     return mm;
 }
 
-__global__ void __launch_bounds__(kGemmThreads)
+// NW waves as 2 (tokens) x NW/2 (weight rows); each wave computes 64 tokens x
+// 32*CT weight rows (2 x CT MFMA tiles of 32 x 32), NW * CT = 16.
+template <int NW, int CT>
+__global__ void __launch_bounds__(64 * NW)
 gemm_q4k_kernel(GemmArgs g, int ntn) {
+    static_assert(NW * CT == 16, "the workgroup tile is 128 x 256");
+    constexpr int WN = NW / 2;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
     const int tile = blockIdx.x;
     const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * BN;
     // stage buffer i at smem + i * STAGE; super-block buffer i after them
     auto stage = [&](int i) { return smem + i * STAGE; };
     auto sbuf = [&](int i) { return smem + NSTAGE * STAGE + i * SB_STAGE; };
     const int nk = g.K / BK;
-    const DmaPlan plan = make_plan(g, m0, n0, wave, lane);
+    const DmaPlan<NW> plan = make_plan<NW>(g, m0, n0, wave, lane);
 
     const uint32_t lds0 = lds_addr(smem);
     uint32_t a_base[2];
@@ -328,27 +408,28 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
         a_base[tt] = lds0 + row * 128;
         a_x[tt] = (lane >> 5) ^ a_swz(row);
     }
-    const uint32_t b_base = lds0 + 2 * A_PLANE + (wn * 2) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
-    const uint32_t hdr_base = lds0 + NSTAGE * STAGE + (wn * 64 + (lane & 31)) * 16;
+    // weight tile ct of this wave: rows wn*32*CT + ct*32 + lane%32 (code group wn*CT + ct)
+    const uint32_t b_base = lds0 + 2 * A_PLANE + (wn * CT) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
+    const uint32_t hdr_base = lds0 + NSTAGE * STAGE + (wn * 32 * CT + (lane & 31)) * 16;
     const uint32_t xs_base = lds0 + NSTAGE * STAGE + HDR + (wm * 64 + (lane & 31)) * 16;
 
-    f16v acc[2][2], main_[2][2];
+    f16v acc[2][CT], main_[2][CT];
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int b = 0; b < CT; b++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
     const f16v zero = {};
 
-    // header words of the lane's two weight rows for the current super-block
-    uint32_t hy[2], hz[2], hw[2];
-    float dsc[2], dmn[2];
+    // header words of the lane's weight rows for the current super-block
+    uint32_t hy[CT], hz[CT], hw[CT];
+    float dsc[CT], dmn[CT];
 
     // steps kt+1 and kt+2 are in flight while step kt is computed
     int cnt_next = 0;                                 // DMA count of step kt+1
-    (void)issue_kstep(plan, wave, 0, stage(0), sbuf(0));
-    if (nk > 1) cnt_next = issue_kstep(plan, wave, 1, stage(1), sbuf(0));
+    (void)issue_kstep<NW>(plan, 0, stage(0), sbuf(0));
+    if (nk > 1) cnt_next = issue_kstep<NW>(plan, 1, stage(1), sbuf(0));
     const int nsb = nk >> 2;
     for (int sb = 0; sb < nsb; sb++) {
         const uint32_t sb_off = (uint32_t)((sb & 1) * SB_STAGE);
@@ -356,22 +437,23 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
         for (int jb = 0; jb < 4; jb++) {
             const int kt = 4 * sb + jb;
-            wait_dma(cnt_next);                         // step kt has landed
+            wait_dma(cnt_next);                       // step kt has landed
             // after this barrier every wave has finished step kt-1, whose
             // stage buffer is the one step kt+2 is copied into
             __builtin_amdgcn_s_barrier();
             cnt_next = 0;
             if (kt + 2 < nk)
-                cnt_next = issue_kstep(plan, wave, kt + 2, stage((kt + 2) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
+                cnt_next = issue_kstep<NW>(plan, kt + 2, stage((kt + 2) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
             const uint32_t st_off = (uint32_t)((kt % NSTAGE) * STAGE);
 
             if (jb == 0) {
-                u32x4 h[2];
-                lds_rd128u<0>(h[0], hdr_base + sb_off);
-                lds_rd128u<512>(h[1], hdr_base + sb_off);
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(h[0]), "+v"(h[1]));
+                u32x4 h[CT];
 #pragma unroll
-                for (int ct = 0; ct < 2; ct++) {
+                for (int ct = 0; ct < CT; ct++) lds_rd128u<0>(h[ct], hdr_base + sb_off + 512 * ct);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    lds_wait_v(h[ct]);
                     dsc[ct] = fp16_bits_to_f32(h[ct].x);
                     dmn[ct] = fp16_bits_to_f32(h[ct].x >> 16);
                     hy[ct] = h[ct].y;
@@ -379,39 +461,70 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
                     hw[ct] = h[ct].w;
                 }
             }
-            h2 vmul[2][2], vadd[2][2];
+            h2 vmul[CT][2], vadd[CT][2];
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++)
+            for (int ct = 0; ct < CT; ct++)
 #pragma unroll
                 for (int i = 0; i < 2; i++) scale_pair(hy[ct], hw[ct], 2 * jb + i, vmul[ct][i], vadd[ct][i]);
 
-            // four K=16 sub-steps; operands of sub-step s+1 are read while
-            // sub-step s computes. The hi and lo MFMAs of one tile are four
-            // instructions apart (no back-to-back accumulator dependency).
-            SubOps ops[2];
-            read_sub<0>(ops[0], st_off, a_base, a_x, b_base);
+            // Four K=16 sub-steps. The step's weight codes are two 8-byte pairs per
+            // tile: pair s&1 holds sub-step s (low nibbles) and s+2 (high nibbles),
+            // read once. Activation fragments are read one sub-step ahead, and the
+            // weights of sub-step s+1 are decoded between the MFMAs of sub-step s.
+            uint2 u[2][CT];                             // [s & 1][tile]
+            AFrag af[2];                                // [s & 1]
+            h8 v[2][CT];                                // [s & 1][tile]
+            {
+                const uint32_t bq = b_base + st_off;
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    lds_rd64<0>(u[0][ct], bq + 1024 * ct);
+                    lds_rd64<512>(u[1][ct], bq + 1024 * ct);
+                }
+            }
+            read_afrag<0>(af[0], st_off, a_base, a_x);
+            read_afrag<1>(af[1], st_off, a_base, a_x);
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++) {
+                asm volatile("" : "+v"(u[0][ct]), "+v"(u[1][ct]));
+                v[0][ct] = decode_v(u[0][ct].x, u[0][ct].y, false, vmul[ct][0], vadd[ct][0]);
+            }
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                SubOps& o = ops[s & 1];
-                wait_sub(o);
-                if (s == 0) read_sub<1>(ops[1], st_off, a_base, a_x, b_base);
-                if (s == 1) read_sub<2>(ops[0], st_off, a_base, a_x, b_base);
-                if (s == 2) read_sub<3>(ops[1], st_off, a_base, a_x, b_base);
-                const bool hi_nib = (s >> 1) != 0;
-                h8 v[2];
-#pragma unroll
-                for (int ct = 0; ct < 2; ct++) v[ct] = decode_v(o.u[ct].x, o.u[ct].y, hi_nib, vmul[ct][s >> 1], vadd[ct][s >> 1]);
+                AFrag& o = af[s & 1];
+                if (s < 3) wait_afrag<4>(o);
+                else wait_afrag<0>(o);
+                __builtin_amdgcn_sched_barrier(0);
+                const h8 (&vs)[CT] = v[s & 1];
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++)
+                    for (int ct = 0; ct < CT; ct++)
                         main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            o.ahi[tt], v[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
+                            o.hi[tt], vs[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++)
-                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.alo[tt], v[ct], main_[tt][ct], 0, 0, 0);
+                    for (int ct = 0; ct < CT; ct++)
+                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.lo[tt], vs[ct], main_[tt][ct], 0, 0, 0);
+                if (s < 3) {
+                    const int sn = s + 1;
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        v[sn & 1][ct] = decode_v(u[sn & 1][ct].x, u[sn & 1][ct].y, sn >= 2, vmul[ct][sn >> 1],
+                                                 vadd[ct][sn >> 1]);
+                }
+                // the MFMAs with the next sub-step's decode spread between them
+#pragma unroll
+                for (int i = 0; i < 4 * CT; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // the next-but-one activation fragments go into this sub-step's buffer
+                if (s == 0) read_afrag<2>(af[0], st_off, a_base, a_x);
+                if (s == 1) read_afrag<3>(af[1], st_off, a_base, a_x);
             }
 
             if (jb == 3) {
@@ -423,9 +536,9 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
                     lds_rd128<XS>(slv[tt], xs_base + sb_off + tt * 512);
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(shv[0]), "+v"(shv[1]), "+v"(slv[0]), "+v"(slv[1]));
-                h8 bmin[2];
+                h8 bmin[CT];
 #pragma unroll
-                for (int ct = 0; ct < 2; ct++) {
+                for (int ct = 0; ct < CT; ct++) {
                     // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
                     const h8 mm = min_codes(hy[ct], hz[ct], hw[ct]);
                     bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -433,15 +546,15 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++) {
                     if (lane >= 32) { shv[tt] = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv[tt] = shv[tt]; }
-                    f16v mn[2];
+                    f16v mn[CT];
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++)
+                    for (int ct = 0; ct < CT; ct++)
                         mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin[ct], zero, 0, 0, 0);
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++)
+                    for (int ct = 0; ct < CT; ct++)
                         mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin[ct], mn[ct], 0, 0, 0);
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++)
+                    for (int ct = 0; ct < CT; ct++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
                             acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
@@ -456,8 +569,8 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
     for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) {
-            const int n = n0 + wn * 64 + ct * 32 + (lane & 31);
+        for (int ct = 0; ct < CT; ct++) {
+            const int n = n0 + wn * 32 * CT + ct * 32 + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 64 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -548,8 +661,9 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
             vh[c] = h;
             vl[c] = (_Float16)(v - (float)h);
         }
-        *reinterpret_cast<h4*>(hi + 4 * i) = vh;
-        *reinterpret_cast<h4*>(lo + 4 * i) = vl;
+        // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
+        *reinterpret_cast<h4*>(hi + 4 * i) = h4{vh[0], vh[2], vh[1], vh[3]};
+        *reinterpret_cast<h4*>(lo + 4 * i) = h4{vl[0], vl[2], vl[1], vl[3]};
         if ((i & 7) == 0) {
             const int b = i >> 3;
             float v = q.sum * inv;
@@ -756,7 +870,9 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
     }
     GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K};
     const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(ntn * ntm), dim3(kGemmThreads), GEMM_LDS, st, g, ntn);
+    // 8 waves of 64 x 64 (2 x 2 MFMA tiles): measured faster than 4 waves of
+    // 64 x 128 (one wave per SIMD, 474 registers) on MI355X
+    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3(ntn * ntm), dim3(512), GEMM_LDS, st, g, ntn);
     return hipGetLastError();
 }
 
