@@ -145,6 +145,9 @@ struct GemmArgs {
     size_t rb;
     float* y;
     int M, N, K;
+    int ksplit;           // 2: two workgroups per tile, one per half of the super-blocks,
+                          // adding into a zeroed y (two fp32 adds onto 0 give the same
+                          // sum in either order)
 };
 
 // LDS layouts (per stage):
@@ -391,12 +394,14 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.x / g.ksplit, part = blockIdx.x % g.ksplit;
     const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * BN;
     // stage buffer i at smem + i * STAGE; super-block buffer i after them
     auto stage = [&](int i) { return smem + i * STAGE; };
     auto sbuf = [&](int i) { return smem + NSTAGE * STAGE + i * SB_STAGE; };
-    const int nk = g.K / BK;
+    const int nsb_all = g.K >> 8;
+    const int sb_beg = part * nsb_all / g.ksplit, sb_end = (part + 1) * nsb_all / g.ksplit;
+    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;     // this workgroup's K steps [kt0, nk)
     const DmaPlan<NW> plan = make_plan<NW>(g, m0, n0, wave, lane);
 
     const uint32_t lds0 = lds_addr(smem);
@@ -428,10 +433,9 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 
     // steps kt+1 and kt+2 are in flight while step kt is computed
     int cnt_next = 0;                                 // DMA count of step kt+1
-    (void)issue_kstep<NW>(plan, 0, stage(0), sbuf(0));
-    if (nk > 1) cnt_next = issue_kstep<NW>(plan, 1, stage(1), sbuf(0));
-    const int nsb = nk >> 2;
-    for (int sb = 0; sb < nsb; sb++) {
+    (void)issue_kstep<NW>(plan, kt0, stage(0), sbuf(sb_beg & 1));
+    cnt_next = issue_kstep<NW>(plan, kt0 + 1, stage(1), sbuf(sb_beg & 1));
+    for (int sb = sb_beg; sb < sb_end; sb++) {
         const uint32_t sb_off = (uint32_t)((sb & 1) * SB_STAGE);
         // jb unrolled so every register-array index below is a constant
 #pragma unroll
@@ -443,8 +447,8 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
             __builtin_amdgcn_s_barrier();
             cnt_next = 0;
             if (kt + 2 < nk)
-                cnt_next = issue_kstep<NW>(plan, kt + 2, stage((kt + 2) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
-            const uint32_t st_off = (uint32_t)((kt % NSTAGE) * STAGE);
+                cnt_next = issue_kstep<NW>(plan, kt + 2, stage((kt + 2 - kt0) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
+            const uint32_t st_off = (uint32_t)(((kt - kt0) % NSTAGE) * STAGE);
 
             if (jb == 0) {
                 u32x4 h[CT];
@@ -574,7 +578,11 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 64 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) g.y[(size_t)m * g.N + n] = acc[tt][ct][r] * g.escale[m];
+                if (m < g.M && n < g.N) {
+                    const float v = acc[tt][ct][r] * g.escale[m];
+                    if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = v;
+                    else atomicAdd(&g.y[(size_t)m * g.N + n], v);
+                }
             }
         }
 }
@@ -829,6 +837,14 @@ gemv_q4k_mf(MfArgs a) {
     }
 }
 
+// y = 0 (a kernel, not a memset, so the sequence can be captured in a graph)
+__global__ void __launch_bounds__(256) zero_f32_kernel(float* __restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 1024 + threadIdx.x;   // y may be only 4-byte aligned
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (i + 256 * k < n) y[i + 256 * k] = 0.0f;
+}
+
 size_t gemm_planes_bytes(int M, int K) {
     const size_t up = 256;
     auto r = [&](size_t v) { return (v + up - 1) / up * up; };
@@ -868,11 +884,20 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
                            0, st, a);
         return hipGetLastError();
     }
-    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K};
     const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
+    // at most half as many tiles as CUs: split K in two (twice the workgroups,
+    // still one wave of them; the halves add into y, zeroed first). Measured
+    // slower when the split makes more workgroups than CUs.
+    const long tiles = (long)ntn * ntm;
+    const int ksplit = (tiles * 2 <= device_cu_count() && (K >> 8) >= 2) ? 2 : 1;
+    if (ksplit == 2) {
+        const size_t n4 = (size_t)M * N;
+        hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
+    }
+    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K, ksplit};
     // 8 waves of 64 x 64 (2 x 2 MFMA tiles): measured faster than 4 waves of
     // 64 x 128 (one wave per SIMD, 474 registers) on MI355X
-    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3(ntn * ntm), dim3(512), GEMM_LDS, st, g, ntn);
+    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3((unsigned)(tiles * ksplit)), dim3(512), GEMM_LDS, st, g, ntn);
     return hipGetLastError();
 }
 
