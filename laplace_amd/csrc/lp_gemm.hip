@@ -614,27 +614,36 @@ static Planes carve_planes(void* base, int M, int K) {
     return P;
 }
 
-// Quantize fp32 activation rows and write their planes in one pass per
-// row (one workgroup per row), without storing the ActQ8 blocks: the same
-// values as quantize_act_kernel followed by gemm_prep_kernel. Pass 1: block
-// scales and their row maximum (the exponent E); pass 2: the codes again
-// (x is re-read from cache), hi/lo and shi/slo.
-__global__ void __launch_bounds__(256)
+// Quantize fp32 activation rows and write their planes, one workgroup per
+// row, without storing the ActQ8 blocks: the same values as
+// quantize_act_kernel followed by gemm_prep_kernel. The row is read once into
+// registers (NF float4 per thread, 8 consecutive threads per 32-element
+// block). Pass 1: block scales and their row maximum (the exponent E); pass
+// 2: codes, hi/lo and shi/slo from the registers.
+template <int NF>
+__global__ void __launch_bounds__(1024)
 quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
 #pragma clang fp contract(off)
-    const int m = blockIdx.y;
+    const int m = blockIdx.x;
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * K);
     const int n4 = K >> 2, nb = K >> 5;
-    // pass 1 (whole row, every workgroup): the largest block scale. Block
-    // scales are fl(amax_b / 127), monotone in amax_b, so their maximum is
-    // fl(max amax_b / 127), over the blocks without a NaN (a NaN block's
-    // scale is NaN, which the maximum skips).
-    __shared__ float red[256];
+    const int nt = blockDim.x;
+    float4 v[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const int i = threadIdx.x + j * nt;
+        v[j] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    // pass 1: the largest block scale. Block scales are fl(amax_b / 127),
+    // monotone in amax_b, so their maximum is fl(max amax_b / 127), over the
+    // blocks without a NaN (a NaN block's scale is NaN, which the maximum skips).
+    __shared__ float red[32];
     float mx = 0.0f;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-        const float4 v = xr[i];
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const float4 u = v[j];
+        float amax = fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w)));
+        int nan = (u.x != u.x) | (u.y != u.y) | (u.z != u.z) | (u.w != u.w);
 #pragma unroll
         for (int off = 1; off < 8; off <<= 1) {
             amax = fmaxf(amax, __shfl_xor(amax, off, 8));
@@ -642,43 +651,46 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
         }
         if (!nan) mx = fmaxf(mx, amax);
     }
-    red[threadIdx.x] = mx;
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-        __syncthreads();
-    }
-    mx = red[0] / 127.0f;
+    mx = 0.0f;
+    for (int wv = 0; wv < (nt + 63) / 64; wv++) mx = fmaxf(mx, red[wv]);
+    mx = mx / 127.0f;
     int e = 0;
     if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
     const float inv = ldexpf(1.0f, -e);
-    if (threadIdx.x == 0 && blockIdx.x == 0) P.escale[m] = ldexpf(1.0f, e);
-    // pass 2: this workgroup's chunk
+    if (threadIdx.x == 0) P.escale[m] = ldexpf(1.0f, e);
+    // pass 2
     _Float16* hi = P.hi + (size_t)m * K;
     _Float16* lo = P.lo + (size_t)m * K;
-    const int i = blockIdx.x * (kPlaneChunk / 4) + threadIdx.x;
-    if (i < n4) {
-        const Q8Group q = quant_group8(xr[i]);
-        const float ds = q.d * inv;
-        h4 vh, vl;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float v = ds * (float)(int8_t)(q.packed >> (8 * c));
-            asm volatile("" : "+v"(v));   // hi and lo both from fl32(v): no fused fp16 product
-            const _Float16 h = (_Float16)v;
-            vh[c] = h;
-            vl[c] = (_Float16)(v - (float)h);
-        }
-        // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
-        *reinterpret_cast<h4*>(hi + 4 * i) = h4{vh[0], vh[2], vh[1], vh[3]};
-        *reinterpret_cast<h4*>(lo + 4 * i) = h4{vl[0], vl[2], vl[1], vl[3]};
-        if ((i & 7) == 0) {
-            const int b = i >> 3;
-            float v = q.sum * inv;
-            asm volatile("" : "+v"(v));
-            const _Float16 h = (_Float16)v;
-            P.shi[(size_t)m * nb + b] = h;
-            P.slo[(size_t)m * nb + b] = (_Float16)(v - (float)h);
+    for (int j = 0; j < NF; j++) {
+        const int i = threadIdx.x + j * nt;
+        const Q8Group q = quant_group8(v[j]);
+        if (i < n4) {
+            const float ds = q.d * inv;
+            h4 vh, vl;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                float t = ds * (float)(int8_t)(q.packed >> (8 * c));
+                asm volatile("" : "+v"(t));   // hi and lo both from fl32(t): no fused fp16 product
+                const _Float16 h = (_Float16)t;
+                vh[c] = h;
+                vl[c] = (_Float16)(t - (float)h);
+            }
+            // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
+            *reinterpret_cast<h4*>(hi + 4 * i) = h4{vh[0], vh[2], vh[1], vh[3]};
+            *reinterpret_cast<h4*>(lo + 4 * i) = h4{vl[0], vl[2], vl[1], vl[3]};
+            if ((i & 7) == 0) {
+                const int b = i >> 3;
+                float t = q.sum * inv;
+                asm volatile("" : "+v"(t));
+                const _Float16 h = (_Float16)t;
+                P.shi[(size_t)m * nb + b] = h;
+                P.slo[(size_t)m * nb + b] = (_Float16)(t - (float)h);
+            }
         }
     }
 }
@@ -861,8 +873,18 @@ bool gemm_supported(uint32_t type, int M, int K) {
 
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quant_planes_kernel, dim3((K + kPlaneChunk - 1) / kPlaneChunk, M), dim3(kPlaneChunk / 4), 0, st,
-                       x, K, carve_planes(planes, M, K));
+    // NF float4 per thread, at most 1024 threads (K <= 32768); 8 | K/4/NF since 32 | K
+    const int n4 = K / 4;
+    const int nf = n4 <= 1024 ? 1 : n4 <= 2048 ? 2 : n4 <= 4096 ? 4 : 8;
+    const int threads = n4 / nf;
+    if (threads % 8 != 0) return hipErrorInvalidValue;     // 8-thread groups must not straddle blocks
+    const Planes P = carve_planes(planes, M, K);
+    switch (nf) {
+        case 1: hipLaunchKernelGGL(quant_planes_kernel<1>, dim3(M), dim3(threads), 0, st, x, K, P); break;
+        case 2: hipLaunchKernelGGL(quant_planes_kernel<2>, dim3(M), dim3(threads), 0, st, x, K, P); break;
+        case 4: hipLaunchKernelGGL(quant_planes_kernel<4>, dim3(M), dim3(threads), 0, st, x, K, P); break;
+        default: hipLaunchKernelGGL(quant_planes_kernel<8>, dim3(M), dim3(threads), 0, st, x, K, P); break;
+    }
     return hipGetLastError();
 }
 
