@@ -314,14 +314,14 @@ struct AFrag {
     h8 hi[2], lo[2];
 };
 
-template <int S>
+template <int S, int PLANE = A_PLANE>
 __device__ __forceinline__ void read_afrag(AFrag& o, uint32_t stage_off, const uint32_t a_base[2], const int a_x[2]) {
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
         // piece (2S + lane/32) ^ swz: the lane/32 term is folded into a_x
         const uint32_t a = a_base[tt] + stage_off + (uint32_t)(((2 * S) ^ a_x[tt]) * 16);
         lds_rd128<0>(o.hi[tt], a);
-        lds_rd128<A_PLANE>(o.lo[tt], a);
+        lds_rd128<PLANE>(o.lo[tt], a);
     }
 }
 
@@ -578,6 +578,286 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 64 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < g.M && n < g.N) {
+                    const float v = acc[tt][ct][r] * g.escale[m];
+                    if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = v;
+                    else atomicAdd(&g.y[(size_t)m * g.N + n], v);
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// 64-token tile variant: 4 waves (one 64 x 64 tile each, 64 tokens x 256
+// weight rows per workgroup) and 80 KB of LDS, so two workgroups share a CU
+// and their barriers do not keep the two waves of a SIMD in step.
+// LDS: 3 stages x (2 x 8 KB planes + 8 KB codes), one 4 KB header buffer (a
+// super-block's headers are read at its first K step; the next ones are
+// copied two K steps later, after a barrier every wave passed after reading
+// them), two 2 KB activation-sum buffers.
+constexpr int A_PLANE64 = 64 * BK * 2;              // 8 KB
+constexpr int STAGE64 = 2 * A_PLANE64 + B_TILE;     // 24 KB
+constexpr int HDR64_OFF = NSTAGE * STAGE64;         // 72 KB
+constexpr int XS64 = 64 * 16;                       // 1 KB per plane
+constexpr int XS64_BUF = 2 * XS64;
+constexpr int XS64_OFF = HDR64_OFF + HDR;           // 76 KB
+constexpr int GEMM64_LDS = XS64_OFF + 2 * XS64_BUF; // 80 KB
+
+struct DmaPlan64 {
+    Rsrc a_rs[2];
+    uint32_t a_off[4], a_plane[4], a_lds[4];
+    Rsrc w_rs;
+    uint32_t b_off[2], b_lds[2];
+    uint32_t h_off, h_lds;
+    Rsrc x_rs;                       // waves 0-1: one activation-sum plane
+    uint32_t x_off;
+};
+
+__device__ __forceinline__ DmaPlan64 make_plan64(const GemmArgs& g, int m0, int n0, int wave, int lane) {
+    DmaPlan64 d;
+    const int mt = g.M - m0 < 64 ? g.M - m0 : 64;
+    const int nt = g.N - n0 < BN ? g.N - n0 : BN;
+    const uint32_t kb = (uint32_t)g.K * 2;
+    d.a_rs[0] = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * kb);
+    d.a_rs[1] = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * kb);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int p = wave * 4 + i;                   // 0..15: 8 per plane
+        const int plane = p >> 3, pp = p & 7;
+        const int row = pp * 8 + (lane >> 3);
+        const int piece = (lane & 7) ^ a_swz(row);
+        const int r = row < mt ? row : mt - 1;
+        d.a_off[i] = (uint32_t)r * kb + (uint32_t)piece * 16;
+        d.a_plane[i] = plane;
+        d.a_lds[i] = plane * A_PLANE64 + pp * 1024;
+    }
+    d.w_rs = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int c = wave * 2 + i;
+        int r = c * 32 + (lane & 31);
+        r = r < nt ? r : nt - 1;
+        d.b_off[i] = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
+        d.b_lds[i] = 2 * A_PLANE64 + c * 1024;
+    }
+    {
+        int r = wave * 64 + lane;
+        r = r < nt ? r : nt - 1;
+        d.h_off = (uint32_t)((size_t)r * g.rb);
+        d.h_lds = HDR64_OFF + wave * 1024;
+    }
+    {
+        const int nbk = g.K >> 5;
+        const int r = lane < mt ? lane : mt - 1;
+        d.x_rs = make_rsrc(((wave & 1) ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
+        d.x_off = (uint32_t)(r * nbk * 2);
+    }
+    return d;
+}
+
+__device__ __forceinline__ int issue_kstep64(const DmaPlan64& d, int wave, int kt, int kt0, uint8_t* smem) {
+    const int sb = kt >> 2, jb = kt & 3;
+    uint8_t* st = smem + ((kt - kt0) % NSTAGE) * STAGE64;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        dma16(d.a_plane[i] ? d.a_rs[1] : d.a_rs[0], d.a_off[i], (uint32_t)(kt * BK * 2), st + d.a_lds[i]);
+#pragma unroll
+    for (int i = 0; i < 2; i++) dma16(d.w_rs, d.b_off[i], (uint32_t)(sb * 144 + 32 * jb), st + d.b_lds[i]);
+    if (jb != 0) return 6;
+    dma16(d.w_rs, d.h_off, (uint32_t)(sb * 144), smem + d.h_lds);
+    if (wave >= 2) return 7;
+    dma16(d.x_rs, d.x_off, (uint32_t)(sb * 16), smem + XS64_OFF + (sb & 1) * XS64_BUF + (wave & 1) * XS64);
+    return 8;
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_q4k_m64(GemmArgs g, int ntn) {
+    constexpr int CT = 2;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave;
+    const int tile = blockIdx.x / g.ksplit, part = blockIdx.x % g.ksplit;
+    const int m0 = (tile / ntn) * 64, n0 = (tile % ntn) * BN;
+    const int nsb_all = g.K >> 8;
+    const int sb_beg = part * nsb_all / g.ksplit, sb_end = (part + 1) * nsb_all / g.ksplit;
+    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;     // this workgroup's K steps [kt0, nk)
+    const DmaPlan64 plan = make_plan64(g, m0, n0, wave, lane);
+
+    const uint32_t lds0 = lds_addr(smem);
+    uint32_t a_base[2];
+    int a_x[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        const int row = tt * 32 + (lane & 31);
+        a_base[tt] = lds0 + row * 128;
+        a_x[tt] = (lane >> 5) ^ a_swz(row);
+    }
+    // weight tile ct of this wave: rows wn*32*CT + ct*32 + lane%32 (code group wn*CT + ct)
+    const uint32_t b_base = lds0 + 2 * A_PLANE64 + (wn * CT) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
+    const uint32_t hdr_base = lds0 + HDR64_OFF + (wn * 32 * CT + (lane & 31)) * 16;
+    const uint32_t xs_base = lds0 + XS64_OFF + (lane & 31) * 16;
+
+    f16v acc[2][CT], main_[2][CT];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < CT; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+    const f16v zero = {};
+
+    // header words of the lane's weight rows for the current super-block
+    uint32_t hy[CT], hz[CT], hw[CT];
+    float dsc[CT], dmn[CT];
+
+    // steps kt+1 and kt+2 are in flight while step kt is computed
+    int cnt_next = 0;                                 // DMA count of step kt+1
+    (void)issue_kstep64(plan, wave, kt0, kt0, smem);
+    cnt_next = issue_kstep64(plan, wave, kt0 + 1, kt0, smem);
+    for (int sb = sb_beg; sb < sb_end; sb++) {
+        const uint32_t xs_off = (uint32_t)((sb & 1) * XS64_BUF);
+        // jb unrolled so every register-array index below is a constant
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            const int kt = 4 * sb + jb;
+            wait_dma(cnt_next);                       // step kt has landed
+            // after this barrier every wave has finished step kt-1, whose
+            // stage buffer is the one step kt+2 is copied into
+            __builtin_amdgcn_s_barrier();
+            cnt_next = 0;
+            if (kt + 2 < nk)
+                cnt_next = issue_kstep64(plan, wave, kt + 2, kt0, smem);
+            const uint32_t st_off = (uint32_t)(((kt - kt0) % NSTAGE) * STAGE64);
+
+            if (jb == 0) {
+                u32x4 h[CT];
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) lds_rd128u<0>(h[ct], hdr_base + 512 * ct);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    lds_wait_v(h[ct]);
+                    dsc[ct] = fp16_bits_to_f32(h[ct].x);
+                    dmn[ct] = fp16_bits_to_f32(h[ct].x >> 16);
+                    hy[ct] = h[ct].y;
+                    hz[ct] = h[ct].z;
+                    hw[ct] = h[ct].w;
+                }
+            }
+            h2 vmul[CT][2], vadd[CT][2];
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) scale_pair(hy[ct], hw[ct], 2 * jb + i, vmul[ct][i], vadd[ct][i]);
+
+            // Four K=16 sub-steps. The step's weight codes are two 8-byte pairs per
+            // tile: pair s&1 holds sub-step s (low nibbles) and s+2 (high nibbles),
+            // read once. Activation fragments are read one sub-step ahead, and the
+            // weights of sub-step s+1 are decoded between the MFMAs of sub-step s.
+            uint2 u[2][CT];                             // [s & 1][tile]
+            AFrag af[2];                                // [s & 1]
+            h8 v[2][CT];                                // [s & 1][tile]
+            {
+                const uint32_t bq = b_base + st_off;
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    lds_rd64<0>(u[0][ct], bq + 1024 * ct);
+                    lds_rd64<512>(u[1][ct], bq + 1024 * ct);
+                }
+            }
+            read_afrag<0, A_PLANE64>(af[0], st_off, a_base, a_x);
+            read_afrag<1, A_PLANE64>(af[1], st_off, a_base, a_x);
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++) {
+                asm volatile("" : "+v"(u[0][ct]), "+v"(u[1][ct]));
+                v[0][ct] = decode_v(u[0][ct].x, u[0][ct].y, false, vmul[ct][0], vadd[ct][0]);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                AFrag& o = af[s & 1];
+                if (s < 3) wait_afrag<4>(o);
+                else wait_afrag<0>(o);
+                __builtin_amdgcn_sched_barrier(0);
+                const h8 (&vs)[CT] = v[s & 1];
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            o.hi[tt], vs[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.lo[tt], vs[ct], main_[tt][ct], 0, 0, 0);
+                if (s < 3) {
+                    const int sn = s + 1;
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        v[sn & 1][ct] = decode_v(u[sn & 1][ct].x, u[sn & 1][ct].y, sn >= 2, vmul[ct][sn >> 1],
+                                                 vadd[ct][sn >> 1]);
+                }
+                // the MFMAs with the next sub-step's decode spread between them
+#pragma unroll
+                for (int i = 0; i < 4 * CT; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // the next-but-one activation fragments go into this sub-step's buffer
+                if (s == 0) read_afrag<2, A_PLANE64>(af[0], st_off, a_base, a_x);
+                if (s == 1) read_afrag<3, A_PLANE64>(af[1], st_off, a_base, a_x);
+            }
+
+            if (jb == 3) {
+                // min term of this super-block and the per-super-block epilogue
+                h8 shv[2], slv[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    lds_rd128<0>(shv[tt], xs_base + xs_off + tt * 512);
+                    lds_rd128<XS64>(slv[tt], xs_base + xs_off + tt * 512);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(shv[0]), "+v"(shv[1]), "+v"(slv[0]), "+v"(slv[1]));
+                h8 bmin[CT];
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
+                    const h8 mm = min_codes(hy[ct], hz[ct], hw[ct]);
+                    bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    if (lane >= 32) { shv[tt] = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv[tt] = shv[tt]; }
+                    f16v mn[CT];
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin[ct], zero, 0, 0, 0);
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin[ct], mn[ct], 0, 0, 0);
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
+                            acc[tt][ct][r] = fmaf(-dmn[ct], mn[ct][r], acc[tt][ct][r]);
+                        }
+                }
+            }
+        }
+    }
+
+    // store: D[token][row] -> y[token * N + row] * 2^E_token
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) {
+            const int n = n0 + wn * 32 * CT + ct * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < g.M && n < g.N) {
                     const float v = acc[tt][ct][r] * g.escale[m];
                     if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = v;
@@ -907,19 +1187,23 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
         return hipGetLastError();
     }
     const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
-    // at most half as many tiles as CUs: split K in two (twice the workgroups,
-    // still one wave of them; the halves add into y, zeroed first). Measured
-    // slower when the split makes more workgroups than CUs.
-    const long tiles = (long)ntn * ntm;
-    const int ksplit = (tiles * 2 <= device_cu_count() && (K >> 8) >= 2) ? 2 : 1;
-    if (ksplit == 2) {
-        const size_t n4 = (size_t)M * N;
-        hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
+    const long cus = device_cu_count();
+    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K, 1};
+    if ((long)ntn * ntm < cus) {
+        // fewer 128-token tiles than CUs: 64-token tiles (two workgroups per CU),
+        // and when even those leave CUs idle, K split over two workgroups that
+        // add into a zeroed y (two fp32 additions onto 0 give the same sum in
+        // either order). Measured: Q4_K 4096 x 4096, M 512: 130 -> 80 us.
+        const long t64 = (long)ntn * ((M + 63) / 64);
+        g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
+        if (g.ksplit == 2) {
+            const size_t n4 = (size_t)M * N;
+            hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
+        }
+        hipLaunchKernelGGL(gemm_q4k_m64, dim3((unsigned)(t64 * g.ksplit)), dim3(256), GEMM64_LDS, st, g, ntn);
+        return hipGetLastError();
     }
-    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K, ksplit};
-    // 8 waves of 64 x 64 (2 x 2 MFMA tiles): measured faster than 4 waves of
-    // 64 x 128 (one wave per SIMD, 474 registers) on MI355X
-    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3((unsigned)(tiles * ksplit)), dim3(512), GEMM_LDS, st, g, ntn);
+    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3((unsigned)(ntn * ntm)), dim3(512), GEMM_LDS, st, g, ntn);
     return hipGetLastError();
 }
 
