@@ -447,7 +447,9 @@ def main():
     if not args.no_extra:
         cfgs = [(Q8_0, 4096, 4096, 1), (Q4_0, 14336, 4096, 1), (Q4_0, 4096, 14336, 1),
                 (Q4_K, 18944, 3584, 1), (Q4_K, 18944, 3584, 4), (Q4_K, 18944, 3584, 8),
-                (Q6_K, 3584, 18944, 1), (Q6_K, 3584, 18944, 4), (Q6_K, 3584, 18944, 8)]
+                (Q6_K, 3584, 18944, 1), (Q6_K, 3584, 18944, 4), (Q6_K, 3584, 18944, 8),
+                # LM head, the largest single weight stream (tests/bench_cpu_gpu.cpp:58)
+                (Q4_K, 262144, 2816, 1)]
         for (tt, n, k, m) in cfgs:
             e = measure_gemv(g, tt, n, k, m, max(64, args.steps // 4), 16)
             extra.append({"workload": f"{TNAME[tt]} GEMV {n}x{k} M={m}",

@@ -141,6 +141,8 @@ CONFIG_SHAPES = [
     (Q4_K, 4096, 14336, 1),
     (Q4_K, 3584, 18944, 1), (Q4_K, 3584, 18944, 4), (Q4_K, 3584, 18944, 8),
     (Q6_K, 18944, 3584, 1), (Q6_K, 18944, 3584, 4), (Q6_K, 18944, 3584, 8),
+    # LM head of the reference's GPU benchmark (tests/bench_cpu_gpu.cpp:58)
+    (Q4_K, 2816, 262144, 1),
 ]
 
 
