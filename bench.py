@@ -44,11 +44,16 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 ROTATE_MIN_BYTES = 512 << 20
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-TNAME = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+F32, F16, Q5_0, Q2_K, Q3_K, Q5_K, BF16 = 0, 1, 6, 10, 11, 13, 30
+FACT_TYPES = (F32, F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K)   # fp32-activation GEMV
+TNAME = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", F32: "F32", F16: "F16",
+         BF16: "BF16", Q5_0: "Q5_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q5_K: "Q5_K"}
 
 
 def row_bytes(t, K):
-    return {Q4_0: K // 32 * 18, Q8_0: K // 32 * 34, Q4_K: K // 256 * 144, Q6_K: K // 256 * 210}[t]
+    return {Q4_0: K // 32 * 18, Q8_0: K // 32 * 34, Q4_K: K // 256 * 144, Q6_K: K // 256 * 210,
+            F32: K * 4, F16: K * 2, BF16: K * 2, Q5_0: K // 32 * 22, Q2_K: K // 256 * 84,
+            Q3_K: K // 256 * 110, Q5_K: K // 256 * 176}[t]
 
 
 def synth_weights(t, K, N, seed):
@@ -56,7 +61,14 @@ def synth_weights(t, K, N, seed):
     6-bit fields, fp16 scales |N(0,1)| * 0.01, Q4_0 * 0.02, Q6_K int8
     scales uniform in [-32, 31])."""
     rng = np.random.default_rng(seed)
-    bpb = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[t]
+    if t in (F32, F16, BF16):
+        v = (rng.standard_normal(K * N) * 0.05).astype(np.float32)
+        if t == F32:
+            return v.view(np.uint8).copy()
+        if t == F16:
+            return v.astype(np.float16).view(np.uint8).copy()
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
+    bpb = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q5_0: 22, Q2_K: 84, Q3_K: 110, Q5_K: 176}[t]
     w = rng.integers(0, 256, row_bytes(t, K) * N, dtype=np.uint8)
     b = w.reshape(-1, bpb)
     nb = b.shape[0]
@@ -74,6 +86,10 @@ def synth_weights(t, K, N, seed):
     elif t == Q6_K:
         b[:, 192:208] = rng.integers(-32, 32, (nb, 16), dtype=np.int8).view(np.uint8)
         b[:, 208:210] = f16(0.01)
+    else:
+        # fp16 scale fields of Q5_0 / Q2_K / Q3_K / Q5_K
+        for off in {Q5_0: [0], Q2_K: [80, 82], Q3_K: [108], Q5_K: [0, 2]}[t]:
+            b[:, off:off + 2] = f16(0.01)
     return w
 
 
@@ -134,7 +150,7 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
         # the kernel that computes y in a step: for Q4_K at M = 1 the step is
         # one launch (the GEMV quantizes x itself); otherwise the GEMV on the
         # step's quantized activations
-        if fused:
+        if fused or t in FACT_TYPES:
             step(i)
         else:
             g.check(g.L.lp_gemm_q_dev(ws.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),
@@ -449,7 +465,10 @@ def main():
                 (Q4_K, 18944, 3584, 1), (Q4_K, 18944, 3584, 4), (Q4_K, 18944, 3584, 8),
                 (Q6_K, 3584, 18944, 1), (Q6_K, 3584, 18944, 4), (Q6_K, 3584, 18944, 8),
                 # LM head, the largest single weight stream (tests/bench_cpu_gpu.cpp:58)
-                (Q4_K, 262144, 2816, 1)]
+                (Q4_K, 262144, 2816, 1),
+                # fp32-activation types (the reference's scalar path): MoE router, FFN
+                (F32, 128, 2816, 1), (Q5_K, 14336, 4096, 1), (Q2_K, 14336, 4096, 1),
+                (BF16, 4096, 4096, 1)]
         for (tt, n, k, m) in cfgs:
             e = measure_gemv(g, tt, n, k, m, max(64, args.steps // 4), 16)
             extra.append({"workload": f"{TNAME[tt]} GEMV {n}x{k} M={m}",

@@ -113,6 +113,24 @@ static bool type_handled(uint32_t t) {
 // Shape/alignment preconditions of the kernels. Returns LP_OK or the status
 // to report.
 static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
+    if (fact_type(type)) {
+        // fp32-activation path: whole 32-element chunks (whole super-blocks for K-quants)
+        if (M < 0 || K <= 0 || N < 0) {
+            set_err("bad shape M=%d K=%d N=%d", M, K, N);
+            return LP_EINVAL;
+        }
+        const int need = (type == T_Q2_K || type == T_Q3_K || type == T_Q5_K) ? 256 : 32;
+        if (K % need != 0) {
+            set_err("K=%d must be a multiple of %d for type %u", K, need, type);
+            return LP_UNSUPPORTED;
+        }
+        const uintptr_t align = (type == T_F32 || type == T_Q2_K || type == T_Q5_K) ? 4 : 2;
+        if (reinterpret_cast<uintptr_t>(w) % align != 0) {
+            set_err("weights must be %zu-byte aligned for type %u", (size_t)align, type);
+            return LP_UNSUPPORTED;
+        }
+        return LP_OK;
+    }
     if (!type_handled(type)) {
         set_err("type %u not handled on the GPU", type);
         return LP_UNSUPPORTED;
@@ -262,7 +280,8 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     const size_t xb = sizeof(float) * (size_t)M * K, yb = sizeof(float) * (size_t)M * N;
     const uint8_t* wd = nullptr;
     int rc;
-    if ((rc = resolve_weights(*c, w, row_bytes(type, K) * (size_t)N, &wd)) != LP_OK) return rc;
+    const size_t rbytes = fact_type(type) ? fact_row_bytes(type, K) : row_bytes(type, K);
+    if ((rc = resolve_weights(*c, w, rbytes * (size_t)N, &wd)) != LP_OK) return rc;
     if ((rc = grow_dev(c->xd, c->xd_cap, xb)) != LP_OK) return rc;
     if ((rc = grow_dev(c->yd, c->yd_cap, yb)) != LP_OK) return rc;
     if ((rc = grow_dev(c->ws, c->ws_cap, ws_bytes(M, K))) != LP_OK) return rc;
@@ -270,7 +289,9 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, yb)) != LP_OK) return rc;
     std::memcpy(c->x_pin, x, xb);
     LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
-    if (gemv_fused_supported(type, M, K, wd)) {
+    if (fact_type(type)) {
+        LP_HIP(launch_gemv_fact(type, wd, c->xd, c->yd, M, K, N, c->stream));
+    } else if (gemv_fused_supported(type, M, K, wd)) {
         LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
     } else if (gemm_supported(type, M, K)) {
         void* planes = ws_planes(c->ws, M, K);
@@ -298,6 +319,12 @@ static size_t moe_ws_bytes(int T, int topk, int E, int K, int multi) {
 }
 
 static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K, int N) {
+    if (fact_type(type)) {
+        // the caller's per-expert fallback (src/matmul.cpp:467-479) then runs
+        // each expert through lp_gemm, which takes these types
+        set_err("type %u: grouped MoE takes the int8 types only", type);
+        return LP_UNSUPPORTED;
+    }
     int st = check_shape(type, w, 1, K, N);
     if (st != LP_OK) return st;
     if (T < 0 || topk < 0 || (T > 0 && topk > 0 && (E <= 0 || E > kMoeMaxExperts))) {
@@ -382,6 +409,7 @@ static int host_moe_grouped(const float* x, int multi, const int* idx, const uin
 // so the selected indices bound the device copy.
 static int host_moe(const float* x, const uint8_t* w, uint32_t type, const int* idx, int n_exp,
                     float* y, int K, int N, bool multi) {
+    if (fact_type(type)) return check_moe(type, w, 1, n_exp, 1, K, N);
     if (n_exp <= 0 || N == 0) return check_shape(type, w, 1, K, N);
     int E = 0;
     for (int k = 0; k < n_exp; k++) {
@@ -517,6 +545,10 @@ int lp_act_unpack_dev(const void* ws, int M, int K, float* d, float* sum, int32_
 
 int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
                   void* stream) {
+    if (fact_type(type)) {
+        set_err("type %u takes fp32 activations (lp_gemm_dev), not quantized blocks", type);
+        return LP_UNSUPPORTED;
+    }
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
     return gemm_q(ws_view(const_cast<void*>(ws), M, K), ws_planes(const_cast<void*>(ws), M, K), w,
@@ -527,6 +559,19 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
                 void* ws, size_t wsb, void* stream) {
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
+    if (fact_type(type)) {
+        // fp32 activations straight into the GEMV (no workspace)
+        if (M > 0 && N > 0 && (!x || !y)) {
+            set_err("null pointer");
+            return LP_EINVAL;
+        }
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+            set_err("x must be 16-byte aligned");
+            return LP_EINVAL;
+        }
+        LP_HIP(launch_gemv_fact(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
+        return LP_OK;
+    }
     if (gemv_fused_supported(type, M, K, w)) {
         // one launch: the GEMV quantizes x itself (bit-identical blocks)
         if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
@@ -562,6 +607,10 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
 
 int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M, int K,
                       int N, void* stream) {
+    if (fact_type(type)) {
+        set_err("type %u has no int8 block sums", type);
+        return LP_UNSUPPORTED;
+    }
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
     LP_HIP(launch_block_sums(type, w, ws_view(const_cast<void*>(ws), M, K), out, M, K, N,

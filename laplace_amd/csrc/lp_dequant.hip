@@ -35,7 +35,7 @@ __device__ __forceinline__ int q3k_scale(const uint8_t* s, int j) {
 }
 
 #pragma clang fp contract(off)
-__device__ float dequant_one(uint32_t type, const uint8_t* __restrict__ w, long i) {
+__device__ __forceinline__ float dequant_one(uint32_t type, const uint8_t* __restrict__ w, long i) {
     switch (type) {
         case T_F32: return reinterpret_cast<const float*>(w)[i];
         case T_F16: return h2f(rd16(w + 2 * i));
@@ -123,7 +123,199 @@ dequant_kernel(uint32_t type, const uint8_t* __restrict__ w, float* __restrict__
         dst[i] = dequant_one(type, w, i);
 }
 
+// ---------------------------------------------------------------------------
+// GEMV with fp32 activations for the types the reference's int8 back-end does
+// not take (F32, F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K): the reference then runs
+// gemm_scalar<dot_row_*> (src/matmul.cpp:320-353, dots at :63-314), fp32 x
+// against the decoded weights. One wave per weight row at a time, lane l
+// taking the 32-element chunks l, l+64, ...: it decodes the chunk once
+// (dequant_one, the dequantize arithmetic, with the block header loads shared
+// by the 32 inlined calls) and dots it with the MR activation rows; a
+// butterfly sum over the wave. The fp32 sums are reassociated against the
+// reference's sequential loop, so results agree to fp32 rounding.
+// One 32-element chunk c of a row: codes q[32] and, per 16-element half h,
+// (a[h], b[h]) with chunk value = sum_h a[h] * sum(x * q) + b[h] * sum(x).
+// Generic form: q = the dequantized values, a = 1, b = 0. The K-quants load
+// their chunk's code bytes as whole dwords and keep the reference's integer
+// codes (Q2_K: 2-bit q with d*sc and -dmin*m per 16; Q3_K: signed 3-bit a
+// with d*(sc-32) per 16; Q5_K: 5-bit v with d*sc and -dmin*m per 32).
+template <uint32_t T>
+__device__ __forceinline__ void chunk_decode(const uint8_t* __restrict__ wr, int c, float (&q)[32], float (&a)[2],
+                                             float (&b)[2]) {
+    if constexpr (T == T_Q5_K) {
+        const uint8_t* blk = wr + (size_t)(c >> 3) * 176;
+        const int j = c & 7, jb = j >> 1, hi = j & 1;
+        const uint32_t* qs = reinterpret_cast<const uint32_t*>(blk + 48 + 32 * jb);
+        const uint32_t* qh = reinterpret_cast<const uint32_t*>(blk + 16);
+        const int bit = 2 * jb + hi;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = ((qs[k] >> (4 * hi)) & 0x0f0f0f0fu) | (((qh[k] >> bit) & 0x01010101u) << 4);
+            q[4 * k] = (float)(v & 0xff);
+            q[4 * k + 1] = (float)((v >> 8) & 0xff);
+            q[4 * k + 2] = (float)((v >> 16) & 0xff);
+            q[4 * k + 3] = (float)(v >> 24);
+        }
+        int sc, m;
+        scale_min(j, blk + 4, sc, m);
+        const float d1 = h2f(rd16(blk)) * (float)sc, m1 = h2f(rd16(blk + 2)) * (float)m;
+        a[0] = a[1] = d1;
+        b[0] = b[1] = -m1;
+    } else if constexpr (T == T_Q2_K) {
+        const uint8_t* blk = wr + (size_t)(c >> 3) * 84;
+        const int j = c & 7;
+        const uint32_t* qs = reinterpret_cast<const uint32_t*>(blk + 16 + 32 * (j >> 2));
+        const int sh = 2 * (j & 3);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = (qs[k] >> sh) & 0x03030303u;
+            q[4 * k] = (float)(v & 0xff);
+            q[4 * k + 1] = (float)((v >> 8) & 0xff);
+            q[4 * k + 2] = (float)((v >> 16) & 0xff);
+            q[4 * k + 3] = (float)(v >> 24);
+        }
+        const float d = h2f(rd16(blk + 80)), dmin = h2f(rd16(blk + 82));
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint8_t s = blk[2 * j + h];
+            a[h] = d * (float)(s & 0xF);
+            b[h] = -(dmin * (float)(s >> 4));
+        }
+    } else if constexpr (T == T_Q3_K) {
+        const uint8_t* blk = wr + (size_t)(c >> 3) * 110;
+        const int g = c & 7;
+        // 2-byte aligned block: bytes via 16-bit loads
+        const uint16_t* hm = reinterpret_cast<const uint16_t*>(blk);
+        const uint16_t* qs = reinterpret_cast<const uint16_t*>(blk + 32 + 32 * (g >> 2));
+        const int sh = 2 * (g & 3);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const uint32_t lo = ((uint32_t)qs[k] >> sh) & 0x0303u;
+            const uint32_t hb = ((uint32_t)hm[k] >> g) & 0x0101u;
+            q[2 * k] = (float)((int)(lo & 0xff) - 4 + 4 * (int)(hb & 0xff));
+            q[2 * k + 1] = (float)((int)(lo >> 8) - 4 + 4 * (int)(hb >> 8));
+        }
+        const float d = h2f(rd16(blk + 108));
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            a[h] = d * (float)(q3k_scale(blk + 96, 2 * g + h) - 32);
+            b[h] = 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int l = 0; l < 32; l++) q[l] = dequant_one(T, wr, 32 * c + l);
+        a[0] = a[1] = 1.0f;
+        b[0] = b[1] = 0.0f;
+    }
+}
+
+template <uint32_t T, int MR>
+__global__ void __launch_bounds__(256)
+gemv_fact_kernel(const uint8_t* __restrict__ w, size_t rb, const float* __restrict__ x, float* __restrict__ y,
+                 int K, int N, int ldy) {
+    const int lane = threadIdx.x & 63;
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    const int nch = K >> 5;
+    for (long row = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; row < N; row += nwaves) {
+        const uint8_t* wr = w + (size_t)row * rb;
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+        for (int c = lane; c < nch; c += 64) {
+            float wv[32], ca[2], cb[2];
+            chunk_decode<T>(wr, c, wv, ca, cb);
+            const bool need_x = cb[0] != 0.0f || cb[1] != 0.0f;
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const float4* xp = reinterpret_cast<const float4*>(x + (size_t)m * K + 32 * c);
+                float t = acc[m];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float s = 0.0f, xs = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v = xp[4 * h + q];
+                        const float* wq = wv + 16 * h + 4 * q;
+                        s = fmaf(v.x, wq[0], s);
+                        s = fmaf(v.y, wq[1], s);
+                        s = fmaf(v.z, wq[2], s);
+                        s = fmaf(v.w, wq[3], s);
+                        xs += (v.x + v.y) + (v.z + v.w);
+                    }
+                    t = fmaf(ca[h], s, t);
+                    if (need_x) t = fmaf(cb[h], xs, t);
+                }
+                acc[m] = t;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float v = acc[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0) y[(size_t)m * ldy + row] = v;
+        }
+    }
+}
+
+template <uint32_t T>
+static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int M, int K, int N, hipStream_t st) {
+    const size_t rb = fact_row_bytes(T, K);
+    long waves = N;
+    const long cap = (long)device_cu_count() * 32;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int mr = M - m0 < 4 ? M - m0 : 4;
+        const float* xm = x + (size_t)m0 * K;
+        float* ym = y + (size_t)m0 * N;
+        switch (mr) {
+            case 1: hipLaunchKernelGGL((gemv_fact_kernel<T, 1>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+            case 2: hipLaunchKernelGGL((gemv_fact_kernel<T, 2>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+            case 3: hipLaunchKernelGGL((gemv_fact_kernel<T, 3>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+            default: hipLaunchKernelGGL((gemv_fact_kernel<T, 4>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace
+
+bool fact_type(uint32_t type) {
+    switch (type) {
+        case T_F32: case T_F16: case T_BF16: case T_Q5_0: case T_Q2_K: case T_Q3_K: case T_Q5_K: return true;
+        default: return false;
+    }
+}
+
+size_t fact_row_bytes(uint32_t type, int K) {
+    switch (type) {
+        case T_F32: return (size_t)K * 4;
+        case T_F16: case T_BF16: return (size_t)K * 2;
+        case T_Q5_0: return (size_t)(K / 32) * 22;
+        case T_Q2_K: return (size_t)(K / 256) * 84;
+        case T_Q3_K: return (size_t)(K / 256) * 110;
+        case T_Q5_K: return (size_t)(K / 256) * 176;
+        default: return 0;
+    }
+}
+
+hipError_t launch_gemv_fact(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K, int N,
+                            hipStream_t st) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    switch (type) {
+        case T_F32: return launch_fact_t<T_F32>(w, x, y, M, K, N, st);
+        case T_F16: return launch_fact_t<T_F16>(w, x, y, M, K, N, st);
+        case T_BF16: return launch_fact_t<T_BF16>(w, x, y, M, K, N, st);
+        case T_Q5_0: return launch_fact_t<T_Q5_0>(w, x, y, M, K, N, st);
+        case T_Q2_K: return launch_fact_t<T_Q2_K>(w, x, y, M, K, N, st);
+        case T_Q3_K: return launch_fact_t<T_Q3_K>(w, x, y, M, K, N, st);
+        case T_Q5_K: return launch_fact_t<T_Q5_K>(w, x, y, M, K, N, st);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 int dequant_block_elems(uint32_t type) {
     switch (type) {

@@ -26,6 +26,13 @@ inline size_t row_bytes(uint32_t type, int K) {
 // Multiprocessor count of the current device (cached per device).
 int device_cu_count();
 
+// Types the reference's int8 back-end leaves to its scalar fp32 path (F32,
+// F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K): GEMV with fp32 activations (lp_dequant.hip).
+bool fact_type(uint32_t type);
+size_t fact_row_bytes(uint32_t type, int K);
+hipError_t launch_gemv_fact(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K, int N,
+                            hipStream_t st);
+
 hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st);
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
                        int N, hipStream_t st);

@@ -56,7 +56,11 @@ _BPB = {GGMLType.F32: 4, GGMLType.F16: 2, GGMLType.BF16: 2, GGMLType.Q4_0: 18,
         GGMLType.Q5_K: 176, GGMLType.Q6_K: 210}
 _EPB = {GGMLType.F32: 1, GGMLType.F16: 1, GGMLType.BF16: 1}
 
+# int8-activation types (the reference's SIMD back-end set, src/matmul_simd.cpp:480-496)
 GPU_TYPES = (GGMLType.Q8_0, GGMLType.Q4_0, GGMLType.Q4_K, GGMLType.Q6_K)
+# fp32-activation types (the reference's scalar gemm_fallback, src/matmul.cpp:331-353)
+GPU_FP32_TYPES = (GGMLType.F32, GGMLType.F16, GGMLType.BF16, GGMLType.Q5_0, GGMLType.Q2_K,
+                  GGMLType.Q3_K, GGMLType.Q5_K)
 
 
 def bytes_per_block(t: int) -> int:
@@ -117,7 +121,8 @@ def _workspace(M: int, K: int, device):
 
 
 def matmul_rows(x, w: Tensor, y, M: int, K: int, N: int) -> None:
-    """src/matmul.cpp:408-433 (int8-activation back-end semantics)."""
+    """src/matmul.cpp:408-433: int8-activation semantics for GPU_TYPES, the
+    scalar path's fp32-activation semantics for GPU_FP32_TYPES."""
     if _is_torch(x):
         ws, nb = _workspace(M, K, x.device)
         rc = lib().lp_gemm_dev(_ptr(x), _ptr(w.data), int(w.type), _ptr(y), M, K, N,
@@ -205,4 +210,4 @@ def quantize_act(x: np.ndarray):
 __all__ = ["GGMLType", "Tensor", "matmul_row", "matmul_rows", "matmul_lm_head",
            "matmul_register_weights", "fused_moe_gemm_idx", "fused_moe_gemm_multi",
            "matmul_gemm_batch", "quantize_act", "dequantize", "bytes_per_block", "elements_per_block",
-           "row_bytes", "GPU_TYPES", "LaplaceHipError", "LP_OK"]
+           "row_bytes", "GPU_TYPES", "GPU_FP32_TYPES", "LaplaceHipError", "LP_OK"]
