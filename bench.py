@@ -45,7 +45,7 @@ INT8_PEAK_TOPS = 5000.0
 ROTATE_MIN_BYTES = 512 << 20
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
 F32, F16, Q5_0, Q2_K, Q3_K, Q5_K, BF16 = 0, 1, 6, 10, 11, 13, 30
-FACT_TYPES = (F32, F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K)   # fp32-activation GEMV
+FACT_TYPES = (F32, F16, BF16, Q2_K, Q3_K, Q5_K)   # fp32-activation GEMV
 TNAME = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", F32: "F32", F16: "F16",
          BF16: "BF16", Q5_0: "Q5_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q5_K: "Q5_K"}
 

@@ -150,6 +150,31 @@ int lp_moe_grouped_dev(const float* x, int multi, const int* topk_idx, const uin
 bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_t* w,
                     uint32_t type, float* y, int T, int topk, int n_experts, int K, int N);
 
+/* ---- 4. MoE feed-forward layer (router, experts, combine) ----------------- */
+
+/* The whole MoE feed-forward of Gemma4Arch::moe_ffn (src/arch_gemma4.cpp:507-641)
+ * for T tokens on the device:
+ *   router in  r = rmsnorm_no_scale(x) * router_scale / sqrt(H)     (:537-541)
+ *   logits     = r @ router_w^T  (n_exp rows of H, router_type)      (:543-544)
+ *   softmax, top-k (lowest index wins a tie), weights / their sum    (:546-563)
+ *   expert in  e = rmsnorm(x, pre_norm, rms_eps)                     (:567-571)
+ *   gu[p]      = e_t @ gate_up_w[idx[p]]^T   (2*inter rows of H)     (:598-605)
+ *   hidden[p]  = gelu_tanh(gu[p][0:inter]) * gu[p][inter:2*inter]    (:613-620)
+ *   eo[p]      = hidden[p] @ down_w[idx[p]]^T (H rows of inter)      (:623-628)
+ *   out[t]     = sum_k (w[t,k] * down_scale[idx[t,k]]) * eo[t*top_k + k]  (:632-639)
+ * x and out are T x H; p = t*top_k + k. The expert GEMVs are the grouped
+ * dispatch of section 3 (int8 types); the router takes every type lp_gemm
+ * takes. topk_idx / topk_w (T x top_k) receive the routing when not NULL.
+ * Constraints: n_exp <= 1024, 1 <= top_k <= min(16, n_exp). No single
+ * reference counterpart: the reference runs these steps per token on the CPU. */
+size_t lp_moe_ffn_workspace_bytes(int T, int H, int n_exp, int top_k, int inter, uint32_t router_type);
+
+int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32_t router_type,
+                   const float* router_scale, const float* pre_norm, float rms_eps,
+                   const uint8_t* gate_up_w, uint32_t gate_up_type, const uint8_t* down_w,
+                   uint32_t down_type, const float* down_scale, int n_exp, int top_k, int inter,
+                   float* out, int* topk_idx, float* topk_w, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- diagnostics ----------------------------------------------------------- */
 
 /* Text of the last error on this thread ("" if none). */

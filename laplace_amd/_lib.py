@@ -37,6 +37,9 @@ SIGNATURES = {
     "lp_moe_grouped": (_b, [_vp, _i, _vp, _vp, _u32, _vp, _i, _i, _i, _i, _i]),
     "lp_dequantize": (_i, [_vp, _u32, _vp, C.c_long]),
     "lp_dequantize_dev": (_i, [_vp, _u32, _vp, C.c_long, _vp]),
+    "lp_moe_ffn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _u32]),
+    "lp_moe_ffn_dev": (_i, [_vp, _i, _i, _vp, _u32, _vp, _vp, C.c_float, _vp, _u32, _vp, _u32, _vp,
+                            _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "lp_last_error": (C.c_char_p, []),
     "lp_device_ok": (_i, []),
 }

@@ -107,7 +107,7 @@ static ActView ws_view(void* ws, int M, int K) {
 }
 
 static bool type_handled(uint32_t t) {
-    return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K;
+    return t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0 || t == T_Q4_K || t == T_Q6_K;
 }
 
 // Shape/alignment preconditions of the kernels. Returns LP_OK or the status
@@ -139,13 +139,13 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
         set_err("bad shape M=%d K=%d N=%d", M, K, N);
         return LP_EINVAL;
     }
-    const int need = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;
+    const int need = (type == T_Q4_K || type == T_Q6_K) ? 256 : type == T_Q5_0 ? 32 : 64;
     if (K % need != 0 || K > 32768) {
         set_err("K=%d must be a multiple of %d and at most 32768", K, need);
         return LP_UNSUPPORTED;
     }
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
-    const uintptr_t align = (type == T_Q4_K) ? 16 : 4;
+    const uintptr_t align = (type == T_Q4_K) ? 16 : type == T_Q5_0 ? 2 : 4;
     if (a % align != 0) {
         set_err("weights must be %zu-byte aligned for type %u", (size_t)align, type);
         return LP_UNSUPPORTED;
@@ -319,7 +319,7 @@ static size_t moe_ws_bytes(int T, int topk, int E, int K, int multi) {
 }
 
 static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K, int N) {
-    if (fact_type(type)) {
+    if (fact_type(type) || type == T_Q5_0) {
         // the caller's per-expert fallback (src/matmul.cpp:467-479) then runs
         // each expert through lp_gemm, which takes these types
         set_err("type %u: grouped MoE takes the int8 types only", type);
@@ -409,7 +409,7 @@ static int host_moe_grouped(const float* x, int multi, const int* idx, const uin
 // so the selected indices bound the device copy.
 static int host_moe(const float* x, const uint8_t* w, uint32_t type, const int* idx, int n_exp,
                     float* y, int K, int N, bool multi) {
-    if (fact_type(type)) return check_moe(type, w, 1, n_exp, 1, K, N);
+    if (fact_type(type) || type == T_Q5_0) return check_moe(type, w, 1, n_exp, 1, K, N);
     if (n_exp <= 0 || N == 0) return check_shape(type, w, 1, K, N);
     int E = 0;
     for (int k = 0; k < n_exp; k++) {
@@ -607,8 +607,8 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
 
 int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M, int K,
                       int N, void* stream) {
-    if (fact_type(type)) {
-        set_err("type %u has no int8 block sums", type);
+    if (fact_type(type) || type == T_Q5_0) {
+        set_err("type %u: no block-sum probe", type);
         return LP_UNSUPPORTED;
     }
     int rc = check_shape(type, w, M, K, N);
@@ -643,6 +643,99 @@ int lp_moe_grouped_dev(const float* x, int multi, const int* topk_idx, const uin
     }
     return moe_q(x, multi ? 1 : 0, topk_idx, w, type, y, T, topk, n_experts, K, N, ws,
                  static_cast<hipStream_t>(stream));
+}
+
+// ---- MoE feed-forward --------------------------------------------------------
+
+namespace {
+struct FfnWs {
+    float *rin, *ein, *logits, *wts, *gu, *hidden, *eo;
+    int* idx;
+    void* rws;       // router GEMV workspace (int8 router types)
+    size_t rws_b;
+    void* mws;       // grouped-MoE workspace
+    size_t mws_b;
+    size_t total;
+};
+
+FfnWs ffn_layout(void* base, int T, int H, int n_exp, int top_k, int inter, uint32_t router_type) {
+    FfnWs f{};
+    const size_t P = (size_t)T * top_k;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += up256(bytes);
+        return static_cast<uint8_t*>(base) + o;
+    };
+    f.rin = reinterpret_cast<float*>(take(4 * (size_t)T * H));
+    f.ein = reinterpret_cast<float*>(take(4 * (size_t)T * H));
+    f.logits = reinterpret_cast<float*>(take(4 * (size_t)T * n_exp));
+    f.idx = reinterpret_cast<int*>(take(4 * P));
+    f.wts = reinterpret_cast<float*>(take(4 * P));
+    f.gu = reinterpret_cast<float*>(take(4 * P * 2 * inter));
+    f.hidden = reinterpret_cast<float*>(take(4 * P * inter));
+    f.eo = reinterpret_cast<float*>(take(4 * P * H));
+    f.rws_b = fact_type(router_type) ? 0 : ws_bytes(T, H);
+    f.rws = take(f.rws_b);
+    const size_t m0 = moe_ws_bytes(T, top_k, n_exp, H, 0), m1 = moe_ws_bytes(T, top_k, n_exp, inter, 1);
+    f.mws_b = m0 > m1 ? m0 : m1;
+    f.mws = take(f.mws_b);
+    f.total = off;
+    return f;
+}
+}  // namespace
+
+size_t lp_moe_ffn_workspace_bytes(int T, int H, int n_exp, int top_k, int inter, uint32_t router_type) {
+    if (T < 0 || H <= 0 || n_exp <= 0 || top_k <= 0 || inter <= 0) return 0;
+    return ffn_layout(nullptr, T, H, n_exp, top_k, inter, router_type).total;
+}
+
+int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32_t router_type,
+                   const float* router_scale, const float* pre_norm, float rms_eps,
+                   const uint8_t* gate_up_w, uint32_t gate_up_type, const uint8_t* down_w,
+                   uint32_t down_type, const float* down_scale, int n_exp, int top_k, int inter,
+                   float* out, int* topk_idx, float* topk_w, void* ws, size_t wsb, void* stream) {
+    if (T < 0 || H <= 0 || n_exp <= 0 || inter <= 0 || top_k < 1 || top_k > 16 || top_k > n_exp ||
+        n_exp > moe_topk_max_experts()) {
+        set_err("bad MoE layer shape T=%d H=%d n_exp=%d top_k=%d inter=%d (n_exp <= %d, top_k <= 16)", T, H,
+                n_exp, top_k, inter, moe_topk_max_experts());
+        return LP_EINVAL;
+    }
+    int rc;
+    if ((rc = check_shape(router_type, router_w, T, H, n_exp)) != LP_OK) return rc;
+    if ((rc = check_moe(gate_up_type, gate_up_w, T, top_k, n_exp, H, 2 * inter)) != LP_OK) return rc;
+    if ((rc = check_moe(down_type, down_w, T, top_k, n_exp, inter, H)) != LP_OK) return rc;
+    if (T == 0) return LP_OK;
+    if (!x || !router_w || !router_scale || !pre_norm || !gate_up_w || !down_w || !down_scale || !out || !ws) {
+        set_err("null pointer");
+        return LP_EINVAL;
+    }
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(ws) % 256 != 0) {
+        set_err("x must be 16-byte and ws 256-byte aligned");
+        return LP_EINVAL;
+    }
+    const FfnWs f = ffn_layout(ws, T, H, n_exp, top_k, inter, router_type);
+    if (wsb < f.total) {
+        set_err("workspace %zu < %zu bytes", wsb, f.total);
+        return LP_EINVAL;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int* idx = topk_idx ? topk_idx : f.idx;
+    float* wts = topk_w ? topk_w : f.wts;
+    const int P = T * top_k;
+    LP_HIP(launch_moe_norms(x, T, H, router_scale, pre_norm, rms_eps, f.rin, f.ein, st));
+    if ((rc = lp_gemm_dev(f.rin, router_w, router_type, f.logits, T, H, n_exp, f.rws, f.rws_b, stream)) != LP_OK)
+        return rc;
+    LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
+    if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,
+                                 f.mws, f.mws_b, stream)) != LP_OK)
+        return rc;
+    LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, st));
+    if ((rc = lp_moe_grouped_dev(f.hidden, 1, idx, down_w, down_type, f.eo, T, top_k, n_exp, inter, H, f.mws,
+                                 f.mws_b, stream)) != LP_OK)
+        return rc;
+    LP_HIP(launch_moe_combine(f.eo, idx, wts, down_scale, T, top_k, H, out, st));
+    return LP_OK;
 }
 
 bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_t* w,

@@ -258,6 +258,72 @@ gemv_fact_kernel(const uint8_t* __restrict__ w, size_t rb, const float* __restri
     }
 }
 
+// Q5_0 with int8 activations (dot_row_q5_0_int_neon, src/matmul_simd.cpp:184-224):
+// per 32-element block the exact integer sum of (code - 16) * q, scaled by
+// fp16(d) * xd. Same layout as gemv_fact_kernel: one wave per row at a time,
+// lane l taking blocks l, l+64, ...; the 22-byte blocks are 2-byte aligned
+// (16-bit loads); the activation codes are 16-byte aligned rows of K.
+__device__ __forceinline__ int dot4s(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+template <int MR>
+__global__ void __launch_bounds__(256)
+gemv_q50_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, float* __restrict__ y, int K, int N) {
+    const int lane = threadIdx.x & 63;
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    const int nb = K >> 5;
+    for (long row = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; row < N; row += nwaves) {
+        const uint8_t* wr = w + (size_t)row * rb;
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+        for (int b = lane; b < nb; b += 64) {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(wr + (size_t)b * 22);
+            const float d = h2f(h[0]);
+            const uint32_t qh = (uint32_t)h[1] | ((uint32_t)h[2] << 16);
+            uint32_t qs[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs[k] = (uint32_t)h[3 + 2 * k] | ((uint32_t)h[4 + 2 * k] << 16);
+            // codes of elements 4k..4k+3 (low nibbles) and 16+4k.. (high nibbles), minus 16
+            uint32_t c[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t hb_lo = (qh >> (4 * k)) & 0xfu, hb_hi = (qh >> (16 + 4 * k)) & 0xfu;
+                // spread 4 bits into bit 4 of 4 bytes
+                const uint32_t s_lo = ((hb_lo & 1u) | ((hb_lo & 2u) << 7) | ((hb_lo & 4u) << 14) | ((hb_lo & 8u) << 21)) << 4;
+                const uint32_t s_hi = ((hb_hi & 1u) | ((hb_hi & 2u) << 7) | ((hb_hi & 4u) << 14) | ((hb_hi & 8u) << 21)) << 4;
+                // (v - 16) per byte: v in [0, 31] -> v ^ 16 flips bit 4; sign-extend 5 bits
+                const uint32_t lo = (qs[k] & 0x0f0f0f0fu) | s_lo;
+                const uint32_t hi = ((qs[k] >> 4) & 0x0f0f0f0fu) | s_hi;
+                // v - 16 in two's complement bytes: (v ^ 0x10) - 0x10 per byte, done as
+                // (v ^ 0x10) | (0xe0 where bit 4 of v ^ 0x10 is set)
+                const uint32_t lx = lo ^ 0x10101010u, hx = hi ^ 0x10101010u;
+                c[k] = lx | ((lx & 0x10101010u) * 0x0eu);
+                c[4 + k] = hx | ((hx & 0x10101010u) * 0x0eu);
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const uint4* aq = reinterpret_cast<const uint4*>(A.qs + (size_t)m * K + 32 * b);
+                const uint4 a0 = aq[0], a1 = aq[1];
+                int s0 = 0;
+                s0 = dot4s(c[0], a0.x, s0); s0 = dot4s(c[1], a0.y, s0);
+                s0 = dot4s(c[2], a0.z, s0); s0 = dot4s(c[3], a0.w, s0);
+                s0 = dot4s(c[4], a1.x, s0); s0 = dot4s(c[5], a1.y, s0);
+                s0 = dot4s(c[6], a1.z, s0); s0 = dot4s(c[7], a1.w, s0);
+                acc[m] = fmaf(d * A.d[(size_t)m * nb + b], (float)s0, acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float v = acc[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0) y[(size_t)m * N + row] = v;
+        }
+    }
+}
+
 template <uint32_t T>
 static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int M, int K, int N, hipStream_t st) {
     const size_t rb = fact_row_bytes(T, K);
@@ -283,9 +349,37 @@ static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int 
 
 }  // namespace
 
+hipError_t launch_gemv_q50(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    const size_t rb = (size_t)(K / 32) * 22;
+    long waves = N;
+    const long cap = (long)device_cu_count() * 32;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    const int nb = K / 32;
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int mr = M - m0 < 4 ? M - m0 : 4;
+        ActView Am = A;
+        Am.qs = A.qs + (size_t)m0 * K;
+        Am.d = A.d + (size_t)m0 * nb;
+        float* ym = y + (size_t)m0 * N;
+        switch (mr) {
+            case 1: hipLaunchKernelGGL((gemv_q50_kernel<1>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
+            case 2: hipLaunchKernelGGL((gemv_q50_kernel<2>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
+            case 3: hipLaunchKernelGGL((gemv_q50_kernel<3>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
+            default: hipLaunchKernelGGL((gemv_q50_kernel<4>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 bool fact_type(uint32_t type) {
+    // Q5_0 is not among them: the reference's int8 back-end takes it
+    // (gemm_simd, src/matmul_simd.cpp:486)
     switch (type) {
-        case T_F32: case T_F16: case T_BF16: case T_Q5_0: case T_Q2_K: case T_Q3_K: case T_Q5_K: return true;
+        case T_F32: case T_F16: case T_BF16: case T_Q2_K: case T_Q3_K: case T_Q5_K: return true;
         default: return false;
     }
 }

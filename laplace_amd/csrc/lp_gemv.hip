@@ -1130,6 +1130,7 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float*
         case T_Q4_0: return launch_gemv_type<T_Q4_0>(w, A, y, M, K, N, st);
         case T_Q4_K: return launch_gemv_type<T_Q4_K>(w, A, y, M, K, N, st);
         case T_Q6_K: return launch_gemv_type<T_Q6_K>(w, A, y, M, K, N, st);
+        case T_Q5_0: return launch_gemv_q50(w, A, y, M, K, N, st);
         default: return hipErrorInvalidValue;
     }
 }

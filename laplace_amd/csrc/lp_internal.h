@@ -17,6 +17,7 @@ inline size_t row_bytes(uint32_t type, int K) {
     switch (type) {
         case T_Q8_0: return (size_t)(K / 32) * 34;
         case T_Q4_0: return (size_t)(K / 32) * 18;
+        case T_Q5_0: return (size_t)(K / 32) * 22;
         case T_Q4_K: return (size_t)(K / 256) * 144;
         case T_Q6_K: return (size_t)(K / 256) * 210;
         default: return 0;
@@ -26,9 +27,21 @@ inline size_t row_bytes(uint32_t type, int K) {
 // Multiprocessor count of the current device (cached per device).
 int device_cu_count();
 
+// Gemma4 MoE feed-forward pieces (lp_moe_ffn.hip).
+int moe_topk_max_experts();
+hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
+                            float eps, float* rin, float* ein, hipStream_t st);
+hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
+                           hipStream_t st);
+hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, hipStream_t st);
+hipError_t launch_moe_combine(const float* eo, const int* idx, const float* wts, const float* down_scale, int T,
+                              int top_k, int H, float* out, hipStream_t st);
+
 // Types the reference's int8 back-end leaves to its scalar fp32 path (F32,
 // F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K): GEMV with fp32 activations (lp_dequant.hip).
 bool fact_type(uint32_t type);
+// Q5_0 with int8 activations (lp_dequant.hip)
+hipError_t launch_gemv_q50(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
 size_t fact_row_bytes(uint32_t type, int K);
 hipError_t launch_gemv_fact(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K, int N,
                             hipStream_t st);

@@ -1,0 +1,186 @@
+// lp_moe_ffn.hip - the element-wise and per-token parts of the Gemma4 MoE
+// feed-forward (src/arch_gemma4.cpp:507-641) around the grouped expert GEMVs:
+// router input and expert input norms, softmax + top-k + renormalisation,
+// GeGLU, and the weighted combine with the per-expert down scales.
+#include <hip/hip_runtime.h>
+
+#include "lp_internal.h"
+
+namespace lp {
+
+namespace {
+
+// Sum over a workgroup of 256 threads (fixed order: wave partials by
+// butterfly, then the 4 wave sums in index order).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Per token t (one workgroup): ms = sum x^2, inv = 1 / sqrt(ms / H + eps);
+//   router input  r[i] = (x[i] * inv) * (gate_scale[i] * inv_sqrt_h)
+//     (rmsnorm_no_scale, src/arch_gemma4.cpp:24-29, then :540-541)
+//   expert input  e[i] = x[i] * inv * pre_norm[i]   (ops::rmsnorm, src/ops.cpp:35-74)
+// Both norms of the reference sum the same squares in the same order, so
+// they share inv.
+__global__ void __launch_bounds__(256)
+moe_norms_kernel(const float* __restrict__ x, int H, const float* __restrict__ gate_scale,
+                 const float* __restrict__ pre_norm, float inv_sqrt_h, float eps, float* __restrict__ rin,
+                 float* __restrict__ ein) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    const float* xr = x + (size_t)blockIdx.x * H;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 256) ss += xr[i] * xr[i];
+    const float ms = block_sum256(ss, red);
+    const float inv = 1.0f / sqrtf(ms / (float)H + eps);
+    float* rr = rin + (size_t)blockIdx.x * H;
+    float* er = ein + (size_t)blockIdx.x * H;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float v = xr[i] * inv;
+        rr[i] = v * (gate_scale[i] * inv_sqrt_h);
+        er[i] = v * pre_norm[i];
+    }
+}
+
+// Per token (one wave): softmax over the n_exp router logits, top-k by
+// repeated arg-max (the lowest index wins a tie, as the reference's strict
+// '>' scan does), then the k weights divided by their sum
+// (src/arch_gemma4.cpp:546-563). n_exp <= 64 * kTopkPer.
+constexpr int kTopkPer = 16;
+
+__global__ void __launch_bounds__(64)
+moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __restrict__ idx,
+                float* __restrict__ wts) {
+    const int lane = threadIdx.x;
+    const float* l = logits + (size_t)blockIdx.x * n_exp;
+    float v[kTopkPer];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < n_exp ? l[e] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < n_exp ? expf(v[j] - mx) : 0.0f;
+        sum += v[j];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < n_exp ? v[j] / sum : -INFINITY;
+    }
+    // lane k keeps the k-th pick
+    float mine = 0.0f;
+    int mine_i = 0;
+    for (int k = 0; k < top_k; k++) {     // top_k <= 16 (the reference's top_idx[16])
+        // lane-local best: lowest index among equal values
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kTopkPer; j++) {
+            const int e = lane + 64 * j;
+            if (e < n_exp && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == k) { mine = bv; mine_i = bi; }
+        // remove it (the reference overwrites it with -1e30)
+        if ((bi & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < kTopkPer; j++)
+                if (lane + 64 * j == bi) v[j] = -1e30f;
+        }
+    }
+    // renormalise: the k weights summed in pick order
+    float wsum = 0.0f;
+    for (int k = 0; k < top_k; k++) wsum += __shfl(mine, k, 64);
+    if (lane < top_k) {
+        idx[(size_t)blockIdx.x * top_k + lane] = mine_i;
+        wts[(size_t)blockIdx.x * top_k + lane] = mine / wsum;
+    }
+}
+
+// hidden[p][i] = gelu_tanh(gate[p][i]) * up[p][i], gate|up = gu row p
+// (ops::geglu, src/ops.cpp:132-174: 0.5 * g * (1 + tanh(c * (g + 0.044715 g^3))))
+__global__ void __launch_bounds__(256)
+geglu_kernel(const float* __restrict__ gu, int inter, long n, float* __restrict__ hidden) {
+#pragma clang fp contract(off)
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const long p = i / inter, c = i - p * inter;
+    const float g = gu[p * 2 * inter + c], u = gu[p * 2 * inter + inter + c];
+    const float g3 = (g * g) * g;
+    const float cst = 0.7978845608028654f;
+    const float gelu = 0.5f * g * (1.0f + tanhf(cst * (g + 0.044715f * g3)));
+    hidden[i] = gelu * u;
+}
+
+// out[t][i] = sum_k (w[t,k] * down_scale[idx[t,k]]) * eo[t*k_ + k][i], k in
+// order from 0 (src/arch_gemma4.cpp:632-639).
+__global__ void __launch_bounds__(256)
+moe_combine_kernel(const float* __restrict__ eo, const int* __restrict__ idx, const float* __restrict__ wts,
+                   const float* __restrict__ down_scale, int top_k, int H, float* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    float acc = 0.0f;
+    for (int k = 0; k < top_k; k++) {
+        const float wgt = wts[(size_t)t * top_k + k] * down_scale[idx[(size_t)t * top_k + k]];
+        acc = fmaf(wgt, eo[((size_t)t * top_k + k) * H + i], acc);
+    }
+    out[(size_t)t * H + i] = acc;
+}
+
+}  // namespace
+
+int moe_topk_max_experts() { return 64 * kTopkPer; }
+
+hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
+                            float eps, float* rin, float* ein, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    const float inv_sqrt_h = 1.0f / sqrtf((float)H);
+    hipLaunchKernelGGL(moe_norms_kernel, dim3(T), dim3(256), 0, st, x, H, gate_scale, pre_norm, inv_sqrt_h, eps,
+                       rin, ein);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
+                           hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_topk_kernel, dim3(T), dim3(64), 0, st, logits, n_exp, top_k, idx, wts);
+    return hipGetLastError();
+}
+
+hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, hipStream_t st) {
+    const long n = (long)P * inter;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, inter, n, hidden);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float* eo, const int* idx, const float* wts, const float* down_scale, int T,
+                              int top_k, int H, float* out, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, eo, idx, wts, down_scale,
+                       top_k, H, out);
+    return hipGetLastError();
+}
+
+}  // namespace lp

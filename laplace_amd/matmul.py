@@ -56,11 +56,12 @@ _BPB = {GGMLType.F32: 4, GGMLType.F16: 2, GGMLType.BF16: 2, GGMLType.Q4_0: 18,
         GGMLType.Q5_K: 176, GGMLType.Q6_K: 210}
 _EPB = {GGMLType.F32: 1, GGMLType.F16: 1, GGMLType.BF16: 1}
 
-# int8-activation types (the reference's SIMD back-end set, src/matmul_simd.cpp:480-496)
-GPU_TYPES = (GGMLType.Q8_0, GGMLType.Q4_0, GGMLType.Q4_K, GGMLType.Q6_K)
-# fp32-activation types (the reference's scalar gemm_fallback, src/matmul.cpp:331-353)
-GPU_FP32_TYPES = (GGMLType.F32, GGMLType.F16, GGMLType.BF16, GGMLType.Q5_0, GGMLType.Q2_K,
-                  GGMLType.Q3_K, GGMLType.Q5_K)
+# int8-activation types (gemm_int in the reference's SIMD back-end, src/matmul_simd.cpp:484-488)
+GPU_TYPES = (GGMLType.Q8_0, GGMLType.Q4_0, GGMLType.Q5_0, GGMLType.Q4_K, GGMLType.Q6_K)
+# fp32-activation types (its fp32 dots, :489-493, and the scalar gemm_fallback,
+# src/matmul.cpp:331-353)
+GPU_FP32_TYPES = (GGMLType.F32, GGMLType.F16, GGMLType.BF16, GGMLType.Q2_K, GGMLType.Q3_K,
+                  GGMLType.Q5_K)
 
 
 def bytes_per_block(t: int) -> int:

@@ -1,8 +1,10 @@
-"""GEMV with fp32 activations for the types the reference's int8 back-end
-leaves to its scalar path (src/matmul.cpp:331-353: F32, F16, BF16, Q5_0,
-Q2_K, Q3_K, Q5_K), against the oracle's restatement of gemm_scalar<dot_row_*>
-(src/matmul.cpp:63-314). The GPU reassociates the fp32 sums, so the bar is
-normwise 2e-5 (fp32 rounding over K <= 4096), not bit equality."""
+"""GEMV with fp32 activations for F32, F16, BF16 (the reference's fp32 dots,
+src/matmul_simd.cpp:489-493) and Q2_K, Q3_K, Q5_K (its scalar fallback,
+src/matmul.cpp:331-353), against the oracle's restatement of
+gemm_scalar<dot_row_*> (src/matmul.cpp:63-314). The GPU reassociates the fp32
+sums, so the bar is normwise 2e-5 (fp32 rounding over K <= 4096), not bit
+equality. Q5_0, which the reference's int8 back-end takes
+(src/matmul_simd.cpp:486), is tested on the int8 path against gemm_int."""
 import numpy as np
 import pytest
 
@@ -11,7 +13,7 @@ from hip_util import L, normwise, to_dev, stream
 pytestmark = pytest.mark.gpu
 
 F32, F16, Q5_0, Q2_K, Q3_K, Q5_K, BF16 = 0, 1, 6, 10, 11, 13, 30
-FACT = {"F32": F32, "F16": F16, "BF16": BF16, "Q5_0": Q5_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q5_K": Q5_K}
+FACT = {"F32": F32, "F16": F16, "BF16": BF16, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q5_K": Q5_K}
 BLOCK = {Q5_0: (32, 22, [0]), Q2_K: (256, 84, [80, 82]), Q3_K: (256, 110, [108]), Q5_K: (256, 176, [0, 2])}
 TOL = 2e-5
 
@@ -40,7 +42,9 @@ def gemm_dev(t, x, w, N):
     M, K = x.shape
     xd, wd = to_dev(x), to_dev(w)
     y = torch.empty(M * N, dtype=torch.float32, device="cuda")
-    rc = L().lp_gemm_dev(xd.data_ptr(), wd.data_ptr(), t, y.data_ptr(), M, K, N, None, 0, stream())
+    from hip_util import workspace
+    ws, nb = workspace(M, K)
+    rc = L().lp_gemm_dev(xd.data_ptr(), wd.data_ptr(), t, y.data_ptr(), M, K, N, ws.data_ptr(), nb, stream())
     assert rc == 0, L().lp_last_error().decode()
     torch.cuda.synchronize()
     return y.cpu().numpy().reshape(M, N)
@@ -91,3 +95,24 @@ def test_fact_types_unsupported_where_int8_only():
     assert not L().lp_moe_gemv(x.ctypes.data, wh.ctypes.data, Q5_K, idx.ctypes.data, 1, yh.ctypes.data, K, N)
     # K not a whole number of super-blocks: unsupported (the scalar path keeps it)
     assert not L().lp_gemm(x.ctypes.data, wh.ctypes.data, Q5_K, yh.ctypes.data, 1, 320, N)
+
+
+@pytest.mark.parametrize("K,N,M", [(32, 5, 1), (512, 65, 3), (2048, 300, 5), (4096, 64, 8)])
+def test_q5_0_int8_path(orc, K, N, M):
+    """Q5_0 (dot_row_q5_0_int_neon, src/matmul_simd.cpp:184-224): int8
+    activations, exact per-block integer sums of (code - 16) * q; against the
+    oracle's gemm_int, and bit-identical to quantize + lp_gemm_q_dev."""
+    import torch
+    from hip_util import workspace
+    w = fact_weights(Q5_0, K, N, seed=K + N)
+    x = np.random.default_rng(M + K).standard_normal((M, K)).astype(np.float32)
+    x[0, :8] = [127.0, -127.0, 0.5, -0.5, 1.5, 2.5, 0.0, 3.0]
+    y = gemm_dev(Q5_0, x, w, N)
+    assert normwise(y, orc.gemm_int(Q5_0, x, w, N)) <= 1e-4
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(M, K)
+    y2 = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    assert L().lp_quantize_act_dev(xd.data_ptr(), M, K, ws.data_ptr(), nb, stream()) == 0
+    assert L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), Q5_0, y2.data_ptr(), M, K, N, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(M, N).view(np.uint32), y.view(np.uint32))

@@ -224,8 +224,15 @@ def test_unsupported_type_is_reported():
     x = np.zeros(256, np.float32)
     w = np.zeros(256 * 2, np.uint8)
     y = np.zeros(1, np.float32)
-    ok = _lib.lib().lp_gemm(x.ctypes.data, w.ctypes.data, 1, y.ctypes.data, 1, 256, 1)  # F16
+    # Q4_1 (3): neither the reference's back-ends nor this library take it
+    ok = _lib.lib().lp_gemm(x.ctypes.data, w.ctypes.data, 3, y.ctypes.data, 1, 256, 1)
     assert ok is False
+    assert b"not handled" in _lib.lib().lp_last_error()
+    # F16 (1) is taken (fp32-activation path): zero weights give zero
+    y[:] = 1.0
+    assert _lib.lib().lp_gemm(x.ctypes.data, w.ctypes.data, 1, y.ctypes.data, 1, 256, 1) is True
+    assert y[0] == 0.0
+    _lib.lib().lp_release_weights()
 
 
 # ---------------------------------------------------------------------------
