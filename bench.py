@@ -23,7 +23,8 @@ src/matmul.cpp:137-167, :320-334) as restated in oracle/liboracle.so, on the
 host cores, same weights, whole matrix, median of repeated runs.
 
 Extra lines (also in the JSON): the other BASELINE.json GEMV configs
-("extra"), the prefill GEMM ("gemm") and the grouped MoE layer ("moe").
+("extra"), the prefill GEMM ("gemm"), the grouped MoE expert GEMVs ("moe")
+and the whole MoE feed-forward layer ("moe_ffn": router to combine).
 """
 from __future__ import annotations
 
@@ -270,6 +271,72 @@ def measure_gemm(g: Gpu, N, K, M, reps=20, copies=2, seed=0):
             "frac_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)}
 
 
+def measure_moe_ffn(g: Gpu, T, reps=20, copies=2, seed=0):
+    """The whole MoE feed-forward layer on the device (lp_moe_ffn_dev) at
+    BASELINE.json config 5's shapes: F32 router 128 x 2048, 128 Q4_K experts
+    (gate_up 1536 x 2048, down 2048 x 768), top-8, T tokens. One step = router
+    norm + matmul + softmax/top-k, expert norm, grouped gate/up, GeGLU, grouped
+    down, combine; routing comes from the router, so the experts touched are
+    the ones the router picks. value = (router + unique-expert weight bytes +
+    x + out) / step time."""
+    torch = g.torch
+    E, topk, H, inter = 128, 8, 2048, 768
+    rng = np.random.default_rng(seed + 91)
+    router = (rng.standard_normal(E * H) * 0.5).astype(np.float32).view(np.uint8).copy()
+    wgu = synth_weights(Q4_K, H, 2 * inter * E, seed=seed + 5)
+    wd = synth_weights(Q4_K, inter, H * E, seed=seed + 6)
+    gu_list = g.copies(wgu, min_bytes=0, min_copies=copies)
+    d_list = g.copies(wd, min_bytes=0, min_copies=copies)
+    ncp = len(gu_list)
+    rd = torch.from_numpy(router).to(g.dev)
+    rs = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)).to(g.dev)
+    pn = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)).to(g.dev)
+    ds = torch.from_numpy((0.5 + rng.random(E)).astype(np.float32)).to(g.dev)
+    x = torch.from_numpy((rng.standard_normal((T, H)) * 2.0).astype(np.float32)).to(g.dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=g.dev)
+    idx = torch.empty((T, topk), dtype=torch.int32, device=g.dev)
+    wts = torch.empty((T, topk), dtype=torch.float32, device=g.dev)
+    nb = int(g.L.lp_moe_ffn_workspace_bytes(T, H, E, topk, inter, F32))
+    ws = torch.empty(nb, dtype=torch.uint8, device=g.dev)
+
+    def step(i):
+        g.check(g.L.lp_moe_ffn_dev(x.data_ptr(), T, H, rd.data_ptr(), F32, rs.data_ptr(), pn.data_ptr(), 1e-6,
+                                   gu_list[i % ncp].data_ptr(), Q4_K, d_list[i % ncp].data_ptr(), Q4_K,
+                                   ds.data_ptr(), E, topk, inter, out.data_ptr(), idx.data_ptr(), wts.data_ptr(),
+                                   ws.data_ptr(), nb, g.stream()), "lp_moe_ffn_dev")
+
+    step(0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(1)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(ncp):
+            step(i)
+    for _ in range(3):
+        graph.replay()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+    uniq = len(np.unique(idx.cpu().numpy()))
+    wbytes = router.nbytes + uniq * (row_bytes(Q4_K, H) * 2 * inter + row_bytes(Q4_K, inter) * H)
+    alg = wbytes + 8 * T * H
+    return {"workload": f"MoE feed-forward layer (lp_moe_ffn_dev): F32 router 128x2048, 128 Q4_K experts "
+                        f"(gate_up 1536x2048, down 2048x768), top-8, T={T}",
+            "unique_experts": uniq, "alg_bytes": int(alg), "us_step": round(us, 2),
+            "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
     """MoE layer dispatch: 128 Q4_K experts, 64
     tokens, top-8 routing (distinct experts per token, uniform). One step =
@@ -493,6 +560,8 @@ def main():
                        "all": gemms}
     if not args.no_moe:
         out["moe"] = measure_moe(g)
+        g.torch.cuda.empty_cache()
+        out["moe_ffn"] = [measure_moe_ffn(g, T) for T in (1, 64)]
         g.torch.cuda.empty_cache()
     print(json.dumps(out))
 

@@ -213,6 +213,9 @@ template <uint32_t T, int MR>
 __global__ void __launch_bounds__(256)
 gemv_fact_kernel(const uint8_t* __restrict__ w, size_t rb, const float* __restrict__ x, float* __restrict__ y,
                  int K, int N, int ldy) {
+    // blockIdx.y: which group of MR activation rows
+    x += (size_t)blockIdx.y * MR * K;
+    y += (size_t)blockIdx.y * MR * ldy;
     const int lane = threadIdx.x & 63;
     const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
     const int nch = K >> 5;
@@ -327,24 +330,25 @@ gemv_q50_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, float* __re
 template <uint32_t T>
 static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int M, int K, int N, hipStream_t st) {
     const size_t rb = fact_row_bytes(T, K);
-    long waves = N;
+    // one launch for the full groups of 4 activation rows (grid.y = group),
+    // one for the remainder
+    const int full = M / 4, rest = M % 4;
+    long waves = (long)N * (full + (rest ? 1 : 0));
     const long cap = (long)device_cu_count() * 32;
-    if (waves > cap) waves = cap;
-    const unsigned grid = (unsigned)((waves + 3) / 4);
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        const int mr = M - m0 < 4 ? M - m0 : 4;
-        const float* xm = x + (size_t)m0 * K;
-        float* ym = y + (size_t)m0 * N;
-        switch (mr) {
-            case 1: hipLaunchKernelGGL((gemv_fact_kernel<T, 1>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
-            case 2: hipLaunchKernelGGL((gemv_fact_kernel<T, 2>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
-            case 3: hipLaunchKernelGGL((gemv_fact_kernel<T, 3>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
-            default: hipLaunchKernelGGL((gemv_fact_kernel<T, 4>), dim3(grid), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+    const long per = waves > cap ? (cap + (full ? full : 1) - 1) / (full ? full : 1) : N;
+    const unsigned gx = (unsigned)((per + 3) / 4);
+    if (full) hipLaunchKernelGGL((gemv_fact_kernel<T, 4>), dim3(gx, full), dim3(256), 0, st, w, rb, x, y, K, N, N);
+    if (rest) {
+        const float* xm = x + (size_t)full * 4 * K;
+        float* ym = y + (size_t)full * 4 * N;
+        const unsigned g1 = (unsigned)(((N < cap ? N : cap) + 3) / 4);
+        switch (rest) {
+            case 1: hipLaunchKernelGGL((gemv_fact_kernel<T, 1>), dim3(g1), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+            case 2: hipLaunchKernelGGL((gemv_fact_kernel<T, 2>), dim3(g1), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
+            default: hipLaunchKernelGGL((gemv_fact_kernel<T, 3>), dim3(g1), dim3(256), 0, st, w, rb, xm, ym, K, N, N); break;
         }
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    return hipGetLastError();
 }
 
 }  // namespace

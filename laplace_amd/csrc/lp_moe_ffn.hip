@@ -4,6 +4,7 @@
 // GeGLU, and the weighted combine with the per-expert down scales.
 #include <hip/hip_runtime.h>
 
+#include "lp_device.h"
 #include "lp_internal.h"
 
 namespace lp {
@@ -47,10 +48,51 @@ moe_norms_kernel(const float* __restrict__ x, int H, const float* __restrict__ g
     }
 }
 
+// Wave-wide reductions with DPP lane moves (the pattern of group_sum: the
+// result lands in lane 63, read back as a wave-uniform value). A lane with no
+// source in a step keeps its own value, the identity of max / arg-max.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWMASK, 0xf, false)));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max_step<0xb1, 0xf>(v);
+    v = dpp_max_step<0x4e, 0xf>(v);
+    v = dpp_max_step<0x114, 0xf>(v);
+    v = dpp_max_step<0x118, 0xf>(v);
+    v = dpp_max_step<0x142, 0xa>(v);
+    v = dpp_max_step<0x143, 0xc>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// (value, index) pairs: larger value wins, the lower index on equal values
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ void dpp_argmax_step(float& v, int& i) {
+    const int b = __builtin_bit_cast(int, v);
+    const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWMASK, 0xf, false));
+    const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROWMASK, 0xf, false);
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+    dpp_argmax_step<0xb1, 0xf>(v, i);
+    dpp_argmax_step<0x4e, 0xf>(v, i);
+    dpp_argmax_step<0x114, 0xf>(v, i);
+    dpp_argmax_step<0x118, 0xf>(v, i);
+    dpp_argmax_step<0x142, 0xa>(v, i);
+    dpp_argmax_step<0x143, 0xc>(v, i);
+    v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    i = __builtin_amdgcn_readlane(i, 63);
+}
+
 // Per token (one wave): softmax over the n_exp router logits, top-k by
-// repeated arg-max (the lowest index wins a tie, as the reference's strict
-// '>' scan does), then the k weights divided by their sum
-// (src/arch_gemma4.cpp:546-563). n_exp <= 64 * kTopkPer.
+// repeated arg-max (the lower index wins a tie, as the reference's strict
+// '>' scan; a pick is then set to -1e30 as the reference does), and the k
+// weights divided by their sum (src/arch_gemma4.cpp:546-563). The sum of
+// exponentials is a wave reduction (reassociated against the reference's
+// loop); the k-weight sum runs in pick order. n_exp <= 64 * kTopkPer.
 constexpr int kTopkPer = 16;
 
 __global__ void __launch_bounds__(64)
@@ -66,51 +108,43 @@ moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __r
         v[j] = e < n_exp ? l[e] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kTopkPer; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < n_exp ? expf(v[j] - mx) : 0.0f;
-        sum += v[j];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    mx = wave_max(mx);
+    float sm = 0.0f;
 #pragma unroll
     for (int j = 0; j < kTopkPer; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < n_exp ? v[j] / sum : -INFINITY;
+        v[j] = lane + 64 * j < n_exp ? expf(v[j] - mx) : 0.0f;
+        sm += v[j];
     }
-    // lane k keeps the k-th pick
+    sm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, group_sum(sm, 64)), 63));
+#pragma unroll
+    for (int j = 0; j < kTopkPer; j++) v[j] = lane + 64 * j < n_exp ? v[j] / sm : -INFINITY;
     float mine = 0.0f;
     int mine_i = 0;
     for (int k = 0; k < top_k; k++) {     // top_k <= 16 (the reference's top_idx[16])
-        // lane-local best: lowest index among equal values
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
         for (int j = 0; j < kTopkPer; j++) {
             const int e = lane + 64 * j;
-            if (e < n_exp && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+            if (e < n_exp && v[j] > bv) {  // ascending e within the lane: strict '>' keeps the lowest
+                bv = v[j];
+                bi = e;
+            }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        wave_argmax(bv, bi);
+        if (lane == k) {
+            mine = bv;
+            mine_i = bi;
         }
-        if (lane == k) { mine = bv; mine_i = bi; }
-        // remove it (the reference overwrites it with -1e30)
         if ((bi & 63) == lane) {
 #pragma unroll
             for (int j = 0; j < kTopkPer; j++)
                 if (lane + 64 * j == bi) v[j] = -1e30f;
         }
     }
-    // renormalise: the k weights summed in pick order
     float wsum = 0.0f;
-    for (int k = 0; k < top_k; k++) wsum += __shfl(mine, k, 64);
+    for (int k = 0; k < top_k; k++)
+        wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), k));
     if (lane < top_k) {
         idx[(size_t)blockIdx.x * top_k + lane] = mine_i;
         wts[(size_t)blockIdx.x * top_k + lane] = mine / wsum;

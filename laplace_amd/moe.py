@@ -49,4 +49,28 @@ def moe_grouped(x, w: Tensor, y, topk_idx, T: int, topk: int, n_experts: int, K:
         raise ValueError(lib().lp_last_error().decode())
 
 
-__all__ = ["moe_grouped", "moe_workspace_bytes"]
+def moe_ffn(x, router: Tensor, router_scale, pre_norm, rms_eps: float, gate_up: Tensor, down: Tensor,
+            down_scale, n_experts: int, top_k: int, inter: int, out=None, return_routing: bool = False):
+    """Gemma4Arch::moe_ffn (src/arch_gemma4.cpp:507-641) for all rows of x
+    [T, H] on the device (torch CUDA tensors): router norm/scale/matmul,
+    softmax, top-k, renormalised weights, expert norm, grouped gate/up and
+    down GEMVs, GeGLU, weighted sum with the per-expert down scales."""
+    import torch
+    T, H = x.shape
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float32, device=x.device)
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    nb = int(lib().lp_moe_ffn_workspace_bytes(T, H, n_experts, top_k, inter, int(router.type)))
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=x.device)
+    rc = lib().lp_moe_ffn_dev(_ptr(x), T, H, _ptr(router.data), int(router.type), _ptr(router_scale),
+                              _ptr(pre_norm), float(rms_eps), _ptr(gate_up.data), int(gate_up.type),
+                              _ptr(down.data), int(down.type), _ptr(down_scale), n_experts, top_k, inter,
+                              _ptr(out), _ptr(idx), _ptr(wts), _ptr(ws), ws.numel(), _stream_ptr())
+    if rc == LP_UNSUPPORTED:
+        raise NotImplementedError(lib().lp_last_error().decode())
+    check(rc, "lp_moe_ffn_dev")
+    return (out, idx, wts) if return_routing else out
+
+
+__all__ = ["moe_grouped", "moe_workspace_bytes", "moe_ffn"]

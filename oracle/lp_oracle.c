@@ -1018,3 +1018,97 @@ void or_ref_test_x(int type, int K, float* out) {   /* :45-49, :59-60 */
     r.s = 7u + (uint32_t)type;
     for (int k = 0; k < K; k++) out[k] = xs_float(&r);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Gemma4 MoE feed-forward (src/arch_gemma4.cpp:507-641), all T tokens.     */
+/* Per token, in the reference's order:                                     */
+/*   rmsnorm_no_scale (:24-29), * router scale * 1/sqrt(H) (:540-541),      */
+/*   router matmul (:543-544: the int8 path for the types gemm_simd takes   */
+/*   with gemm_int, src/matmul_simd.cpp:484-488, the fp32 dot otherwise),   */
+/*   softmax (:546-550), top-k by strict '>' scans (:552-558), weights over */
+/*   their sum (:560-562), ops::rmsnorm (src/ops.cpp:68-73), the two expert */
+/*   GEMVs (moe_gemv_int / multi), ops::geglu (src/ops.cpp:165-172), the     */
+/*   weighted sum (:632-639). Sequential fp32 loops as the reference's       */
+/*   non-NEON code.                                                          */
+static int int8_type(int t) {
+    return t == OR_Q8_0 || t == OR_Q4_0 || t == OR_Q5_0 || t == OR_Q4_K || t == OR_Q6_K;
+}
+
+int or_moe_ffn(const float* x, int T, int H, const uint8_t* router_w, int router_type,
+               const float* router_scale, const float* pre_norm, float eps,
+               const uint8_t* gu_w, int gu_type, const uint8_t* dn_w, int dn_type,
+               const float* down_scale, int n_exp, int top_k, int inter,
+               float* out, int* idx_out, float* w_out) {
+    if (top_k < 1 || top_k > 16 || top_k > n_exp) return -1;
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)H);
+    float* moe_in = (float*)malloc(sizeof(float) * (size_t)H);
+    float* logits = (float*)malloc(sizeof(float) * (size_t)n_exp);
+    float* gu = (float*)malloc(sizeof(float) * (size_t)top_k * 2 * inter);
+    float* hidden = (float*)malloc(sizeof(float) * (size_t)top_k * inter);
+    float* eo = (float*)malloc(sizeof(float) * (size_t)top_k * H);
+    int rc = 0;
+    const float inv_sqrt_h = 1.0f / sqrtf((float)H);
+    for (int m = 0; m < T && rc == 0; m++) {
+        const float* xr = x + (size_t)m * H;
+        float* o = out + (size_t)m * H;
+        for (int i = 0; i < H; i++) o[i] = 0.0f;
+        float ms = 0.0f;
+        for (int i = 0; i < H; i++) ms += xr[i] * xr[i];
+        float inv = 1.0f / sqrtf(ms / H + eps);
+        for (int i = 0; i < H; i++) tmp[i] = xr[i] * inv;
+        for (int i = 0; i < H; i++) tmp[i] *= router_scale[i] * inv_sqrt_h;
+        rc = int8_type(router_type) ? or_gemm_int(router_type, tmp, router_w, logits, 1, H, n_exp, 1)
+                                    : or_gemm_scalar(router_type, tmp, router_w, logits, 1, H, n_exp, 1);
+        if (rc) break;
+        float maxl = logits[0];
+        for (int e = 1; e < n_exp; e++) if (logits[e] > maxl) maxl = logits[e];
+        float suml = 0.0f;
+        for (int e = 0; e < n_exp; e++) { logits[e] = expf(logits[e] - maxl); suml += logits[e]; }
+        for (int e = 0; e < n_exp; e++) logits[e] /= suml;
+        int idx[16];
+        float wk[16];
+        for (int k = 0; k < top_k; k++) {
+            int best = 0;
+            for (int e = 1; e < n_exp; e++) if (logits[e] > logits[best]) best = e;
+            idx[k] = best;
+            wk[k] = logits[best];
+            logits[best] = -1e30f;
+        }
+        float wsum = 0.0f;
+        for (int k = 0; k < top_k; k++) wsum += wk[k];
+        for (int k = 0; k < top_k; k++) wk[k] /= wsum;
+        /* ops::rmsnorm: its own sum of squares, the same loop */
+        float ms2 = 0.0f;
+        for (int i = 0; i < H; i++) ms2 += xr[i] * xr[i];
+        float inv2 = 1.0f / sqrtf(ms2 / H + eps);
+        for (int i = 0; i < H; i++) moe_in[i] = xr[i] * inv2 * pre_norm[i];
+        rc = or_moe_gemv_int(gu_type, moe_in, gu_w, idx, top_k, gu, H, 2 * inter, 0, 1);
+        if (rc) break;
+        const float c = 0.7978845608028654f;
+        for (int k = 0; k < top_k; k++) {
+            const float* g = gu + (size_t)k * 2 * inter;
+            const float* u = g + inter;
+            float* hd = hidden + (size_t)k * inter;
+            for (int i = 0; i < inter; i++) {
+                float gg = g[i];
+                float g2 = gg * gg;
+                float g3 = g2 * gg;
+                float gelu = 0.5f * gg * (1.0f + tanhf(c * (gg + 0.044715f * g3)));
+                hd[i] = gelu * u[i];
+            }
+        }
+        rc = or_moe_gemv_int(dn_type, hidden, dn_w, idx, top_k, eo, inter, H, 1, 1);
+        if (rc) break;
+        for (int k = 0; k < top_k; k++) {
+            float weight = wk[k] * down_scale[idx[k]];
+            const float* e = eo + (size_t)k * H;
+            for (int i = 0; i < H; i++) o[i] += weight * e[i];
+        }
+        for (int k = 0; k < top_k; k++) {
+            if (idx_out) idx_out[(size_t)m * top_k + k] = idx[k];
+            if (w_out) w_out[(size_t)m * top_k + k] = wk[k];
+        }
+    }
+    free(tmp); free(moe_in); free(logits); free(gu); free(hidden); free(eo);
+    return rc;
+}

@@ -116,6 +116,17 @@ int or_dequantize(int type, const uint8_t* w, float* dst, int n);
 int  or_ref_test_weights(int type, int K, int N, uint8_t* out);
 void or_ref_test_x(int type, int K, float* out);
 
+/* Gemma4Arch::moe_ffn (src/arch_gemma4.cpp:507-641) for T tokens of H:
+ * router rmsnorm + scale + matmul, softmax, top-k, renormalised weights,
+ * expert rmsnorm, gate/up and down expert GEMVs (int8 path), GeGLU, weighted
+ * sum with down_scale. out is T x H; idx_out / w_out (T x top_k) may be NULL.
+ * Returns 0, or -1 for an unsupported type or top_k. */
+int or_moe_ffn(const float* x, int T, int H, const uint8_t* router_w, int router_type,
+               const float* router_scale, const float* pre_norm, float eps,
+               const uint8_t* gu_w, int gu_type, const uint8_t* dn_w, int dn_type,
+               const float* down_scale, int n_exp, int top_k, int inter,
+               float* out, int* idx_out, float* w_out);
+
 #ifdef __cplusplus
 }
 #endif

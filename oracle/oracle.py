@@ -83,6 +83,10 @@ def lib():
         L.or_dequantize.argtypes = [C.c_int, _u8p, _f32p, C.c_int]
         L.or_ref_test_weights.restype = C.c_int
         L.or_ref_test_weights.argtypes = [C.c_int, C.c_int, C.c_int, _u8p]
+        L.or_moe_ffn.restype = C.c_int
+        L.or_moe_ffn.argtypes = [_f32p, C.c_int, C.c_int, _u8p, C.c_int, _f32p, _f32p, C.c_float,
+                                 _u8p, C.c_int, _u8p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int,
+                                 _f32p, _i32p, _f32p]
         L.or_ref_test_x.argtypes = [C.c_int, C.c_int, _f32p]
         _lib = L
     return _lib
@@ -193,6 +197,24 @@ def moe_gemv_int(t: int, x: np.ndarray, w: np.ndarray, expert_idx, K: int, N: in
     if rc:
         raise ValueError(f"unsupported type {t}")
     return y
+
+
+def moe_ffn(x, router_w, router_type, router_scale, pre_norm, eps, gu_w, gu_type, dn_w, dn_type,
+            down_scale, n_exp, top_k, inter):
+    """Gemma4 MoE feed-forward of x [T, H]; returns (out [T, H], idx, w [T, top_k])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    out = np.zeros((T, H), np.float32)
+    idx = np.zeros((T, top_k), np.int32)
+    wts = np.zeros((T, top_k), np.float32)
+    f = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+    u = lambda a: np.ascontiguousarray(a, dtype=np.uint8)
+    rc = lib().or_moe_ffn(x, T, H, u(router_w), router_type, f(router_scale), f(pre_norm), eps,
+                          u(gu_w), gu_type, u(dn_w), dn_type, f(down_scale), n_exp, top_k, inter,
+                          out, idx, wts)
+    if rc:
+        raise ValueError("unsupported type or top_k")
+    return out, idx, wts
 
 
 def dequantize(t: int, w: np.ndarray, n: int) -> np.ndarray:

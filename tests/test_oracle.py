@@ -317,3 +317,39 @@ def test_scalar_dot_matches_own_dequantize(orc, t):
     y = orc.gemm_scalar(t, x, w, N)[0]
     exact = (x.astype(np.float64) @ rows.T)[0]
     assert np.abs(y - exact).max() <= 1e-5 * max(np.abs(exact).max(), 1e-3)
+
+
+from moe_layer import moe_layer_inputs as _moe_layer_inputs  # noqa: E402
+
+
+def test_moe_ffn_restatement_against_float64(orc):
+    """or_moe_ffn (Gemma4Arch::moe_ffn, src/arch_gemma4.cpp:507-641) against
+    an independent float64 evaluation of the same mathematics, with the
+    expert GEMVs taken from the oracle's moe_gemv_int (pinned separately):
+    router norm and scale, softmax, top-k, renormalised weights (checked
+    against argsort), expert norm, GeGLU with gate = the first `inter`
+    outputs, weighted sum with down_scale."""
+    rng = np.random.default_rng(5)
+    T, H, n_exp, top_k, inter = 3, 512, 16, 4, 256
+    p = _moe_layer_inputs(rng, H, n_exp, inter, Q4_K, Q4_K)
+    x = (rng.standard_normal((T, H)) * 2.0).astype(np.float32)
+    out, idx, wts = orc.moe_ffn(x, p["router_w"], F32, p["router_scale"], p["pre_norm"], p["eps"],
+                                p["gu_w"], Q4_K, p["dn_w"], Q4_K, p["down_scale"], n_exp, top_k, inter)
+    rw = p["router_w"].view(np.float32).reshape(n_exp, H).astype(np.float64)
+    for t in range(T):
+        xr = x[t].astype(np.float64)
+        inv = 1.0 / np.sqrt(np.mean(xr * xr) + p["eps"])
+        logits = (xr * inv * p["router_scale"] / np.sqrt(H)) @ rw.T
+        prob = np.exp(logits - logits.max())
+        prob /= prob.sum()
+        order = np.argsort(-prob, kind="stable")[:top_k]
+        assert np.array_equal(idx[t], order)
+        wk = prob[order] / prob[order].sum()
+        assert np.allclose(wts[t], wk, rtol=1e-5, atol=1e-7)
+        ein = (xr * inv * p["pre_norm"]).astype(np.float32)
+        gu = orc.moe_gemv_int(Q4_K, ein[None, :], p["gu_w"], idx[t], H, 2 * inter, False).astype(np.float64)
+        g, u = gu[:, :inter], gu[:, inter:]
+        hidden = 0.5 * g * (1.0 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3))) * u
+        eo = orc.moe_gemv_int(Q4_K, hidden.astype(np.float32), p["dn_w"], idx[t], inter, H, True).astype(np.float64)
+        ref = ((wk * p["down_scale"][idx[t]])[:, None] * eo).sum(axis=0)
+        assert np.abs(out[t] - ref).max() <= 1e-4 * np.abs(ref).max()
