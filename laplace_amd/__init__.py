@@ -9,8 +9,9 @@ from .matmul import (GGMLType, Tensor, bytes_per_block, dequantize, elements_per
                      fused_moe_gemm_multi, matmul_gemm_batch, matmul_lm_head,
                      matmul_register_weights, matmul_row, matmul_rows, quantize_act, row_bytes)
 from .moe import moe_ffn, moe_grouped, moe_workspace_bytes
+from .gguf import GGUFFile, write_gguf
 
 __all__ = ["GGMLType", "Tensor", "bytes_per_block", "dequantize", "elements_per_block", "fused_moe_gemm_idx",
            "fused_moe_gemm_multi", "matmul_gemm_batch", "matmul_lm_head",
            "matmul_register_weights", "matmul_row", "matmul_rows", "quantize_act", "row_bytes",
-           "moe_ffn", "moe_grouped", "moe_workspace_bytes"]
+           "moe_ffn", "moe_grouped", "moe_workspace_bytes", "GGUFFile", "write_gguf"]
