@@ -56,6 +56,14 @@ def lib() -> C.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is not built: run `python -m laplace_amd.build`")
+        # PyTorch-ROCm ships its own libamdhip64 with the same soname as the
+        # system one this library links. Whichever loads first serves both;
+        # if the system runtime came first, torch's HIP would not initialise.
+        # Load torch (when installed) first so the process has one runtime.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name, None)

@@ -396,14 +396,29 @@ struct Q8Group {
     int32_t s16;
 };
 
+// Lane exchanges inside 8-lane groups with DPP moves (no LDS round trip):
+// X = 1 and 2 swap neighbours / pairs inside a quad, X = 4 pairs lane i with
+// lane 7 - i (row_half_mirror), which for a quad-uniform value is the other
+// quad's value, all a reduction over the 8 lanes needs.
+template <int X>
+__device__ __forceinline__ uint32_t dpp_x8(uint32_t v) {
+    constexpr int ctrl = X == 1 ? 0xb1 : X == 2 ? 0x4e : 0x141;
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, ctrl, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dpp_x8f(float v, int x) {
+    const uint32_t b = __float_as_uint(v);
+    return __uint_as_float(x == 1 ? dpp_x8<1>(b) : x == 2 ? dpp_x8<2>(b) : dpp_x8<4>(b));
+}
+
 __device__ __forceinline__ Q8Group quant_group8(const float4 v) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    int nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 8));
-        nan |= __shfl_xor(nan, off, 8);
-    }
+    uint32_t nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+    amax = fmaxf(amax, dpp_x8f(amax, 1));
+    nan |= dpp_x8<1>(nan);
+    amax = fmaxf(amax, dpp_x8f(amax, 2));
+    nan |= dpp_x8<2>(nan);
+    amax = fmaxf(amax, dpp_x8f(amax, 4));
+    nan |= dpp_x8<4>(nan);
     if (nan) amax = __builtin_nanf("");                // FMAX propagates NaN
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
@@ -411,9 +426,9 @@ __device__ __forceinline__ Q8Group quant_group8(const float4 v) {
     const int32_t q2 = cvt_rne_sat(v.z * id), q3 = cvt_rne_sat(v.w * id);
     // int32 sums wrap modulo 2^32 as the NEON lane adds do.
     uint32_t s = (uint32_t)q0 + (uint32_t)q1 + (uint32_t)q2 + (uint32_t)q3;
-    s += __shfl_xor(s, 1, 8);
-    s += __shfl_xor(s, 2, 8);                          // lanes 0-3: elems 0-15, 4-7: 16-31
-    const uint32_t s_other = __shfl_xor(s, 4, 8);
+    s += dpp_x8<1>(s);
+    s += dpp_x8<2>(s);                                 // lanes 0-3: elems 0-15, 4-7: 16-31
+    const uint32_t s_other = dpp_x8<4>(s);
     const bool first_half = (threadIdx.x & 4) == 0;
     const uint32_t s_lo = first_half ? s : s_other, s_hi = first_half ? s_other : s;
     Q8Group r;
