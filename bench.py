@@ -413,6 +413,60 @@ def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
             "per_pair_bytes_reference": int(per_pair)}
 
 
+def _graph_us(g: Gpu, fn, reps=50, inner=8):
+    """Average microseconds of fn() over graph replays of `inner` calls."""
+    torch = g.torch
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    for _ in range(3):
+        graph.replay()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / (reps * inner)
+
+
+def measure_aux(g: Gpu):
+    """The quantizer at prefill size (quantize_act_q8_neon over M 2048 x K
+    4096: 33.5 MB of fp32 read, 8.9 MB of blocks written) and dequantize of a
+    Q4_K 14336 x 4096 weight to fp32 (33 MB read, 235 MB written): both
+    HBM-bound, value = bytes moved / time."""
+    torch = g.torch
+    out = []
+    M, K = 2048, 4096
+    x = torch.from_numpy(synth_x(M, K, 3)).to(g.dev)
+    nb = int(g.L.lp_act_workspace_bytes(M, K))
+    ws = torch.empty(nb, dtype=torch.uint8, device=g.dev)
+    us = _graph_us(g, lambda: g.check(g.L.lp_quantize_act_dev(x.data_ptr(), M, K, ws.data_ptr(), nb, g.stream()),
+                                      "quantize"))
+    byt = 4 * M * K + M * K + M * (K // 32) * 16
+    out.append({"workload": "ActQ8 quantizer M=2048 K=4096", "us": round(us, 2),
+                "gbs": round(byt / (us * 1e-6) / 1e9, 1), "hbm_frac": round(byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    N, K = 14336, 4096
+    w = torch.from_numpy(synth_weights(Q4_K, K, N, 4)).to(g.dev)
+    dst = torch.empty(N * K, dtype=torch.float32, device=g.dev)
+    us = _graph_us(g, lambda: g.check(g.L.lp_dequantize_dev(w.data_ptr(), Q4_K, dst.data_ptr(), N * K, g.stream()),
+                                      "dequantize"), reps=20, inner=4)
+    byt = w.numel() + 4 * N * K
+    out.append({"workload": "dequantize Q4_K 14336x4096 -> fp32", "us": round(us, 2),
+                "gbs": round(byt / (us * 1e-6) / 1e9, 1), "hbm_frac": round(byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    return out
+
+
 def measure_host_api(g: Gpu, w, x, t, N, K, reps=200):
     """The drop-in host-pointer entry (lp_gemm, the gemm_fn contract):
     weights registered once (device-resident), x and y staged over PCIe
@@ -562,6 +616,9 @@ def main():
         out["moe"] = measure_moe(g)
         g.torch.cuda.empty_cache()
         out["moe_ffn"] = [measure_moe_ffn(g, T) for T in (1, 64)]
+    if not args.no_extra:
+        g.torch.cuda.empty_cache()
+        out["aux"] = measure_aux(g)
         g.torch.cuda.empty_cache()
     print(json.dumps(out))
 

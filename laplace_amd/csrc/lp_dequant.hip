@@ -123,6 +123,23 @@ dequant_kernel(uint32_t type, const uint8_t* __restrict__ w, float* __restrict__
         dst[i] = dequant_one(type, w, i);
 }
 
+// Eight consecutive outputs per thread (two 16-byte stores; the type is a
+// template constant, so the eight inlined decodes share their block-header
+// loads). n % 8 == 0 and dst 16-byte aligned.
+template <uint32_t T>
+__global__ void __launch_bounds__(256)
+dequant8_kernel(const uint8_t* __restrict__ w, float* __restrict__ dst, long n8) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j < n8; j += stride) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = dequant_one(T, w, 8 * j + k);
+        float4* o = reinterpret_cast<float4*>(dst + 8 * j);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // GEMV with fp32 activations for the types the reference's int8 back-end does
 // not take (F32, F16, BF16, Q5_0, Q2_K, Q3_K, Q5_K): the reference then runs
@@ -445,6 +462,19 @@ size_t dequant_src_bytes(uint32_t type, long n) {
 
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
+    if (n % 8 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+        const long n8 = n / 8;
+        long g8 = (n8 + 255) / 256;
+        if (g8 > 65536) g8 = 65536;
+        const dim3 grid((unsigned)g8);
+        switch (type) {
+#define LP_D(TT) case TT: hipLaunchKernelGGL((dequant8_kernel<TT>), grid, dim3(256), 0, st, w, dst, n8); return hipGetLastError();
+            LP_D(T_F32) LP_D(T_F16) LP_D(T_BF16) LP_D(T_Q4_0) LP_D(T_Q5_0) LP_D(T_Q8_0) LP_D(T_Q2_K) LP_D(T_Q3_K)
+            LP_D(T_Q4_K) LP_D(T_Q5_K) LP_D(T_Q6_K)
+#undef LP_D
+            default: break;
+        }
+    }
     long grid = (n + 255) / 256;
     if (grid > 65536) grid = 65536;
     hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)grid), dim3(256), 0, st, type, w, dst, n);
