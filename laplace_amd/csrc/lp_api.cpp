@@ -655,6 +655,8 @@ struct FfnWs {
     size_t rws_b;
     void* mws;       // grouped-MoE workspace
     size_t mws_b;
+    ActView eq, hq;  // int8 blocks of ein [T, H] and hidden [P, inter] (fused quantization)
+    void* route;     // route table shared by both expert passes
     size_t total;
 };
 
@@ -680,6 +682,9 @@ FfnWs ffn_layout(void* base, int T, int H, int n_exp, int top_k, int inter, uint
     const size_t m0 = moe_ws_bytes(T, top_k, n_exp, H, 0), m1 = moe_ws_bytes(T, top_k, n_exp, inter, 1);
     f.mws_b = m0 > m1 ? m0 : m1;
     f.mws = take(f.mws_b);
+    f.eq = ws_view(take(act_bytes(T, H)), T, H);
+    f.hq = ws_view(take(act_bytes((int)P, inter)), (int)P, inter);
+    f.route = take(moe_route_bytes((int)P, n_exp));
     f.total = off;
     return f;
 }
@@ -723,17 +728,34 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
     int* idx = topk_idx ? topk_idx : f.idx;
     float* wts = topk_w ? topk_w : f.wts;
     const int P = T * top_k;
-    LP_HIP(launch_moe_norms(x, T, H, router_scale, pre_norm, rms_eps, f.rin, f.ein, st));
+    // Decode-sized batches (neither expert pass on the MFMA kernel): the norm
+    // and GeGLU kernels also write the int8 blocks the expert GEMVs read, and
+    // one route table serves both passes.
+    const bool fused = !(moe_mf_supported(gate_up_type, H) && P >= 8 * n_exp) &&
+                       !(moe_mf_supported(down_type, inter) && P >= 8 * n_exp) && H % 32 == 0 &&
+                       inter % 32 == 0 && reinterpret_cast<uintptr_t>(router_scale) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(pre_norm) % 16 == 0;
+    LP_HIP(launch_moe_norms(x, T, H, router_scale, pre_norm, rms_eps, f.rin, f.ein, fused ? f.eq : ActView{},
+                            st));
     if ((rc = lp_gemm_dev(f.rin, router_w, router_type, f.logits, T, H, n_exp, f.rws, f.rws_b, stream)) != LP_OK)
         return rc;
     LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
-    if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,
-                                 f.mws, f.mws_b, stream)) != LP_OK)
-        return rc;
-    LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, st));
-    if ((rc = lp_moe_grouped_dev(f.hidden, 1, idx, down_w, down_type, f.eo, T, top_k, n_exp, inter, H, f.mws,
-                                 f.mws_b, stream)) != LP_OK)
-        return rc;
+    if (fused) {
+        LP_HIP(launch_moe_route(idx, P, n_exp, f.route, false, st));
+        LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, nullptr, T, P, n_exp, 0, top_k, f.route,
+                                         f.gu, H, 2 * inter, st));
+        LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, f.hq, st));
+        LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, nullptr, P, P, n_exp, 1, top_k, f.route, f.eo,
+                                         inter, H, st));
+    } else {
+        if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,
+                                     f.mws, f.mws_b, stream)) != LP_OK)
+            return rc;
+        LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, ActView{}, st));
+        if ((rc = lp_moe_grouped_dev(f.hidden, 1, idx, down_w, down_type, f.eo, T, top_k, n_exp, inter, H, f.mws,
+                                     f.mws_b, stream)) != LP_OK)
+            return rc;
+    }
     LP_HIP(launch_moe_combine(f.eo, idx, wts, down_scale, T, top_k, H, out, st));
     return LP_OK;
 }

@@ -29,11 +29,13 @@ int device_cu_count();
 
 // Gemma4 MoE feed-forward pieces (lp_moe_ffn.hip).
 int moe_topk_max_experts();
+// norms of x [T, H]; when Aq.qs is set, ein is also quantized into Aq (H % 32 == 0)
 hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
-                            float eps, float* rin, float* ein, hipStream_t st);
+                            float eps, float* rin, float* ein, const ActView& Aq, hipStream_t st);
 hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
                            hipStream_t st);
-hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, hipStream_t st);
+// hidden [P, inter]; when Aq.qs is set, also quantized into Aq (inter % 32 == 0)
+hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, const ActView& Aq, hipStream_t st);
 hipError_t launch_moe_combine(const float* eo, const int* idx, const float* wts, const float* down_scale, int T,
                               int top_k, int H, float* out, hipStream_t st);
 
@@ -82,6 +84,13 @@ size_t moe_route_bytes(int P, int E);
 hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
                               int rows, const int* idx, int P, int E, int multi, int topk, void* route,
                               float* y, int K, int N, hipStream_t st);
+// The two halves of launch_moe_grouped: the route table of the pairs (groups
+// of <= 16 pairs for the MFMA kernel, mf_groups, else <= 4), and the grouped
+// products on a route table built for the same pairs and group size.
+hipError_t launch_moe_route(const int* idx, int P, int E, void* route, bool mf_groups, hipStream_t st);
+hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+                                     int rows, int P, int E, int multi, int topk, const void* route, float* y,
+                                     int K, int N, hipStream_t st);
 // dequantize (lp_dequant.hip): elements per block (0 = type not handled)
 // and source bytes of n elements.
 int dequant_block_elems(uint32_t type);

@@ -4,7 +4,7 @@
 // GeGLU, and the weighted combine with the per-expert down scales.
 #include <hip/hip_runtime.h>
 
-#include "lp_device.h"
+#include "lp_chunks.h"
 #include "lp_internal.h"
 
 namespace lp {
@@ -22,6 +22,19 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// The 8 threads of a 32-element block quantize it as quantize_act_kernel does
+// (same arithmetic, same stores).
+__device__ __forceinline__ void store_q8_block(const ActView& A, long m, int K, int i4, float4 v) {
+    const Q8Group q = quant_group8(v);
+    *reinterpret_cast<uint32_t*>(A.qs + m * K + 4 * i4) = q.packed;
+    if ((i4 & 7) == 0) {
+        const long blk = m * (K >> 5) + (i4 >> 3);
+        A.d[blk] = q.d;
+        A.sum[blk] = q.sum;
+        A.s16[blk] = q.s16;
+    }
+}
+
 // Per token t (one workgroup): ms = sum x^2, inv = 1 / sqrt(ms / H + eps);
 //   router input  r[i] = (x[i] * inv) * (gate_scale[i] * inv_sqrt_h)
 //     (rmsnorm_no_scale, src/arch_gemma4.cpp:24-29, then :540-541)
@@ -31,7 +44,7 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 __global__ void __launch_bounds__(256)
 moe_norms_kernel(const float* __restrict__ x, int H, const float* __restrict__ gate_scale,
                  const float* __restrict__ pre_norm, float inv_sqrt_h, float eps, float* __restrict__ rin,
-                 float* __restrict__ ein) {
+                 float* __restrict__ ein, ActView Aq) {
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const float* xr = x + (size_t)blockIdx.x * H;
@@ -41,10 +54,25 @@ moe_norms_kernel(const float* __restrict__ x, int H, const float* __restrict__ g
     const float inv = 1.0f / sqrtf(ms / (float)H + eps);
     float* rr = rin + (size_t)blockIdx.x * H;
     float* er = ein + (size_t)blockIdx.x * H;
-    for (int i = threadIdx.x; i < H; i += 256) {
-        const float v = xr[i] * inv;
-        rr[i] = v * (gate_scale[i] * inv_sqrt_h);
-        er[i] = v * pre_norm[i];
+    if (Aq.qs) {
+        // float4 per thread; H % 32 == 0, so a block's 8 threads are all in or all out
+        for (int i4 = threadIdx.x; i4 < (H >> 2); i4 += 256) {
+            const float4 xv = reinterpret_cast<const float4*>(xr)[i4];
+            const float4 gs = reinterpret_cast<const float4*>(gate_scale)[i4];
+            const float4 pn = reinterpret_cast<const float4*>(pre_norm)[i4];
+            const float v0 = xv.x * inv, v1 = xv.y * inv, v2 = xv.z * inv, v3 = xv.w * inv;
+            reinterpret_cast<float4*>(rr)[i4] = make_float4(v0 * (gs.x * inv_sqrt_h), v1 * (gs.y * inv_sqrt_h),
+                                                            v2 * (gs.z * inv_sqrt_h), v3 * (gs.w * inv_sqrt_h));
+            const float4 e = make_float4(v0 * pn.x, v1 * pn.y, v2 * pn.z, v3 * pn.w);
+            reinterpret_cast<float4*>(er)[i4] = e;
+            store_q8_block(Aq, blockIdx.x, H, i4, e);
+        }
+    } else {
+        for (int i = threadIdx.x; i < H; i += 256) {
+            const float v = xr[i] * inv;
+            rr[i] = v * (gate_scale[i] * inv_sqrt_h);
+            er[i] = v * pre_norm[i];
+        }
     }
 }
 
@@ -153,17 +181,36 @@ moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __r
 
 // hidden[p][i] = gelu_tanh(gate[p][i]) * up[p][i], gate|up = gu row p
 // (ops::geglu, src/ops.cpp:132-174: 0.5 * g * (1 + tanh(c * (g + 0.044715 g^3))))
-__global__ void __launch_bounds__(256)
-geglu_kernel(const float* __restrict__ gu, int inter, long n, float* __restrict__ hidden) {
+__device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
 #pragma clang fp contract(off)
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const long p = i / inter, c = i - p * inter;
-    const float g = gu[p * 2 * inter + c], u = gu[p * 2 * inter + inter + c];
     const float g3 = (g * g) * g;
     const float cst = 0.7978845608028654f;
     const float gelu = 0.5f * g * (1.0f + tanhf(cst * (g + 0.044715f * g3)));
-    hidden[i] = gelu * u;
+    return gelu * u;
+}
+
+__global__ void __launch_bounds__(256)
+geglu_kernel(const float* __restrict__ gu, int inter, long n, float* __restrict__ hidden) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const long p = i / inter, c = i - p * inter;
+    hidden[i] = gelu_tanh_mul(gu[p * 2 * inter + c], gu[p * 2 * inter + inter + c]);
+}
+
+// The same, four outputs per thread, and each 32-element block quantized
+// (inter % 32 == 0).
+__global__ void __launch_bounds__(256)
+geglu_q_kernel(const float* __restrict__ gu, int inter, long n4, float* __restrict__ hidden, ActView Aq) {
+    const long i4 = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i4 >= n4) return;                                // n4 % 8 == 0: whole blocks
+    const int q4 = inter >> 2;
+    const long p = i4 / q4, c4 = i4 - p * q4;
+    const float4 g = reinterpret_cast<const float4*>(gu + p * 2 * inter)[c4];
+    const float4 u = reinterpret_cast<const float4*>(gu + p * 2 * inter + inter)[c4];
+    const float4 h = make_float4(gelu_tanh_mul(g.x, u.x), gelu_tanh_mul(g.y, u.y), gelu_tanh_mul(g.z, u.z),
+                                 gelu_tanh_mul(g.w, u.w));
+    reinterpret_cast<float4*>(hidden)[i4] = h;
+    store_q8_block(Aq, p, inter, (int)c4, h);
 }
 
 // out[t][i] = sum_k (w[t,k] * down_scale[idx[t,k]]) * eo[t*k_ + k][i], k in
@@ -187,11 +234,12 @@ moe_combine_kernel(const float* __restrict__ eo, const int* __restrict__ idx, co
 int moe_topk_max_experts() { return 64 * kTopkPer; }
 
 hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
-                            float eps, float* rin, float* ein, hipStream_t st) {
+                            float eps, float* rin, float* ein, const ActView& Aq, hipStream_t st) {
     if (T <= 0) return hipSuccess;
+    if (Aq.qs && H % 32 != 0) return hipErrorInvalidValue;
     const float inv_sqrt_h = 1.0f / sqrtf((float)H);
     hipLaunchKernelGGL(moe_norms_kernel, dim3(T), dim3(256), 0, st, x, H, gate_scale, pre_norm, inv_sqrt_h, eps,
-                       rin, ein);
+                       rin, ein, Aq);
     return hipGetLastError();
 }
 
@@ -202,10 +250,17 @@ hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int
     return hipGetLastError();
 }
 
-hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, hipStream_t st) {
+hipError_t launch_geglu(const float* gu, int P, int inter, float* hidden, const ActView& Aq, hipStream_t st) {
     const long n = (long)P * inter;
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, inter, n, hidden);
+    if (Aq.qs) {
+        if (inter % 32 != 0) return hipErrorInvalidValue;
+        const long n4 = n / 4;
+        hipLaunchKernelGGL(geglu_q_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, gu, inter, n4,
+                           hidden, Aq);
+    } else {
+        hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, inter, n, hidden);
+    }
     return hipGetLastError();
 }
 
