@@ -467,6 +467,54 @@ def measure_aux(g: Gpu):
     return out
 
 
+def measure_batch(g: Gpu, copies=8):
+    """matmul_gemm_batch at Llama-3-8B decode shapes (Q4_K, K 4096): Q/K/V
+    (4096 + 1024 + 1024 rows) and gate/up (2 x 14336 rows), each a batch of
+    specs sharing one x. One lp_gemm_batch_dev call (one launch per batch)
+    against the same specs as separate lp_gemm_dev calls. Weight copies
+    rotate so every launch streams from HBM. value = weight bytes + x + y per
+    step / step time."""
+    from laplace_amd._lib import BatchSpec
+    torch = g.torch
+    K = 4096
+    x = torch.from_numpy(synth_x(1, K, 17)).to(g.dev)
+    out = []
+    for name, Ns in (("Q/K/V 4096+1024+1024", (4096, 1024, 1024)), ("gate/up 2x14336", (14336, 14336))):
+        mats = [[torch.from_numpy(synth_weights(Q4_K, K, N, 60 + i)).to(g.dev) for N in Ns] for i in range(copies)]
+        ys = [torch.empty(N, dtype=torch.float32, device=g.dev) for N in Ns]
+        arrs = []
+        for c in range(copies):
+            arr = (BatchSpec * len(Ns))()
+            for i, N in enumerate(Ns):
+                arr[i] = BatchSpec(x.data_ptr(), mats[c][i].data_ptr(), Q4_K, ys[i].data_ptr(), K, N)
+            arrs.append(arr)
+        nb = int(g.L.lp_gemm_batch_workspace_bytes(arrs[0], len(Ns)))
+        ws = torch.empty(nb, dtype=torch.uint8, device=g.dev)
+        state = {"i": 0}
+
+        def batched():
+            c = state["i"] % copies
+            state["i"] += 1
+            g.check(g.L.lp_gemm_batch_dev(arrs[c], len(Ns), ws.data_ptr(), nb, g.stream()), "batch")
+
+        def separate():
+            c = state["i"] % copies
+            state["i"] += 1
+            for i, N in enumerate(Ns):
+                g.check(g.L.lp_gemm_dev(x.data_ptr(), mats[c][i].data_ptr(), Q4_K, ys[i].data_ptr(), 1, K, N,
+                                        ws.data_ptr(), nb, g.stream()), "gemm")
+
+        us_b = _graph_us(g, batched, reps=40, inner=copies)
+        us_s = _graph_us(g, separate, reps=40, inner=copies)
+        byt = sum(row_bytes(Q4_K, K) * N + 4 * N for N in Ns) + 4 * K
+        out.append({"workload": f"matmul_gemm_batch Q4_K {name}, K=4096", "us_batch": round(us_b, 2),
+                    "us_separate": round(us_s, 2), "gbs_batch": round(byt / (us_b * 1e-6) / 1e9, 1),
+                    "hbm_frac_batch": round(byt / (us_b * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del mats
+        torch.cuda.empty_cache()
+    return out
+
+
 def measure_host_api(g: Gpu, w, x, t, N, K, reps=200):
     """The drop-in host-pointer entry (lp_gemm, the gemm_fn contract):
     weights registered once (device-resident), x and y staged over PCIe
@@ -620,6 +668,7 @@ def main():
         g.torch.cuda.empty_cache()
         out["aux"] = measure_aux(g)
         g.torch.cuda.empty_cache()
+        out["batch"] = measure_batch(g)
     print(json.dumps(out))
 
 

@@ -124,6 +124,30 @@ int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* 
 /* Device-pointer dequantize, stream-ordered. */
 int lp_dequantize_dev(const uint8_t* w, uint32_t type, float* dst, long n, void* stream);
 
+/* ---- 2b. batched M=1 matmuls ------------------------------------------------ */
+
+/* One M=1 matmul of a batch: y[N] = x[K] @ W^T. Mirrors MatmulBatchSpec
+ * (src/matmul.h:46-53) with the Tensor replaced by (w, type). */
+typedef struct lp_batch_spec {
+    const float* x;
+    const uint8_t* w;
+    uint32_t type;
+    float* y;
+    int K, N;
+} lp_batch_spec;
+
+/* n matmuls, host pointers, synchronous. Replaces matmul_gemm_batch
+ * (src/matmul.h:54, src/matmul.cpp:450-454). Consecutive Q4_K specs with the
+ * same x and K (the Q/K/V and gate/up batches of src/arch_gemma4.cpp:318-327,
+ * :694-700) run as one launch of up to 4 matrices. false = not handled
+ * (caller loops over matmul_rows). */
+bool lp_gemm_batch(const lp_batch_spec* specs, int n);
+
+/* Device-pointer form (x, w, y device pointers; the specs array itself in
+ * host memory), stream-ordered; ws of lp_gemm_batch_workspace_bytes. */
+size_t lp_gemm_batch_workspace_bytes(const lp_batch_spec* specs, int n);
+int lp_gemm_batch_dev(const lp_batch_spec* specs, int n, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- 3. grouped MoE dispatch ---------------------------------------------- */
 
 /* The MoE layer of T tokens, each routed to topk experts of a stacked weight

@@ -16,6 +16,13 @@ STATUS_NAMES = {0: "LP_OK", 1: "LP_UNSUPPORTED", 2: "LP_EINVAL", 3: "LP_EHIP", 4
 
 # Every symbol the header declares, with (restype, argtypes).
 _vp, _i, _u32, _sz, _b = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_bool
+
+
+class BatchSpec(C.Structure):
+    """lp_batch_spec of include/laplace_hip.h."""
+    _fields_ = [("x", _vp), ("w", _vp), ("type", _u32), ("y", _vp), ("K", _i), ("N", _i)]
+
+
 SIGNATURES = {
     "lp_gemm": (_b, [_vp, _vp, _u32, _vp, _i, _i, _i]),
     "lp_moe_gemv": (_b, [_vp, _vp, _u32, _vp, _i, _vp, _i, _i]),
@@ -40,6 +47,9 @@ SIGNATURES = {
     "lp_moe_ffn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _u32]),
     "lp_moe_ffn_dev": (_i, [_vp, _i, _i, _vp, _u32, _vp, _vp, C.c_float, _vp, _u32, _vp, _u32, _vp,
                             _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "lp_gemm_batch": (_b, [C.POINTER(BatchSpec), _i]),
+    "lp_gemm_batch_workspace_bytes": (_sz, [C.POINTER(BatchSpec), _i]),
+    "lp_gemm_batch_dev": (_i, [C.POINTER(BatchSpec), _i, _vp, _sz, _vp]),
     "lp_last_error": (C.c_char_p, []),
     "lp_device_ok": (_i, []),
 }

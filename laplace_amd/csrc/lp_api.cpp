@@ -760,6 +760,135 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
     return LP_OK;
 }
 
+// ---- Batched M=1 matmuls (matmul_gemm_batch) ---------------------------------
+
+// Specs i..j-1 can share one multi-matrix launch: same activation row and K,
+// Q4_K weights the fused GEMV takes.
+static bool batch_fusable(const lp_batch_spec& a, const lp_batch_spec& b) {
+    return a.x == b.x && a.K == b.K && a.type == T_Q4_K && b.type == T_Q4_K &&
+           gemv_fused_supported(T_Q4_K, 1, a.K, a.w) && gemv_fused_supported(T_Q4_K, 1, b.K, b.w);
+}
+
+static int check_batch(const lp_batch_spec* specs, int n) {
+    if (n < 0 || (n > 0 && !specs)) {
+        set_err("bad batch: n=%d", n);
+        return LP_EINVAL;
+    }
+    for (int i = 0; i < n; i++) {
+        const lp_batch_spec& s = specs[i];
+        int rc = check_shape(s.type, s.w, 1, s.K, s.N);
+        if (rc != LP_OK) return rc;
+        if (s.N > 0 && (!s.x || !s.y)) {
+            set_err("spec %d: null pointer", i);
+            return LP_EINVAL;
+        }
+        if (reinterpret_cast<uintptr_t>(s.x) % 16 != 0) {
+            set_err("spec %d: x must be 16-byte aligned", i);
+            return LP_EINVAL;
+        }
+    }
+    return LP_OK;
+}
+
+size_t lp_gemm_batch_workspace_bytes(const lp_batch_spec* specs, int n) {
+    size_t b = 0;
+    for (int i = 0; specs && i < n; i++) {
+        const size_t w = specs[i].K > 0 ? ws_bytes(1, specs[i].K) : 0;
+        if (w > b) b = w;
+    }
+    return b;
+}
+
+// Specs already validated; device pointers.
+static int batch_dev(const lp_batch_spec* specs, int n, void* ws, size_t wsb, hipStream_t st) {
+    int i = 0;
+    while (i < n) {
+        int j = i + 1;
+        while (j < n && j - i < kBatchMax && batch_fusable(specs[i], specs[j])) j++;
+        if (j - i >= 2) {
+            const uint8_t* w[kBatchMax];
+            float* y[kBatchMax];
+            int nn[kBatchMax];
+            for (int k = i; k < j; k++) {
+                w[k - i] = specs[k].w;
+                y[k - i] = specs[k].y;
+                nn[k - i] = specs[k].N;
+            }
+            LP_HIP(launch_gemv_fused_batch(w, y, nn, j - i, specs[i].x, specs[i].K, st));
+        } else {
+            const lp_batch_spec& s = specs[i];
+            const int rc = lp_gemm_dev(s.x, s.w, s.type, s.y, 1, s.K, s.N, ws, wsb, st);
+            if (rc != LP_OK) return rc;
+        }
+        i = j;
+    }
+    return LP_OK;
+}
+
+int lp_gemm_batch_dev(const lp_batch_spec* specs, int n, void* ws, size_t wsb, void* stream) {
+    int rc = check_batch(specs, n);
+    if (rc != LP_OK) return rc;
+    return batch_dev(specs, n, ws, wsb, static_cast<hipStream_t>(stream));
+}
+
+// Host pointers, synchronous: every spec's x is staged once (specs naming the
+// same x with the same K share the staged copy), weights resolve through the
+// registered regions or the per-pointer cache, all outputs come back with one
+// copy.
+static int host_gemm_batch(const lp_batch_spec* specs, int n) {
+    int rc = check_batch(specs, n);
+    if (rc != LP_OK) return rc;
+    if (n == 0) return LP_OK;
+    if (!dev_info().ok) {
+        set_err("no gfx950 device");
+        return LP_ENODEV;
+    }
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) {
+        set_err("no HIP device/stream");
+        return LP_ENODEV;
+    }
+    // offsets (floats, 16-byte aligned) of each spec's staged x and y
+    std::vector<size_t> xo(n), yo(n);
+    size_t xt = 0, yt = 0;
+    for (int i = 0; i < n; i++) {
+        int share = -1;
+        for (int k = 0; k < i; k++)
+            if (specs[k].x == specs[i].x && specs[k].K == specs[i].K) { share = k; break; }
+        if (share >= 0) xo[i] = xo[share];
+        else { xo[i] = xt; xt += ((size_t)specs[i].K + 3) & ~size_t(3); }
+        yo[i] = yt;
+        yt += ((size_t)specs[i].N + 3) & ~size_t(3);
+    }
+    if ((rc = grow_dev(c->xd, c->xd_cap, 4 * xt)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->yd, c->yd_cap, 4 * yt)) != LP_OK) return rc;
+    if ((rc = grow_dev(c->ws, c->ws_cap, lp_gemm_batch_workspace_bytes(specs, n))) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->x_pin, c->x_pin_cap, 4 * xt)) != LP_OK) return rc;
+    if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, 4 * yt)) != LP_OK) return rc;
+    std::vector<lp_batch_spec> ds(specs, specs + n);
+    for (int i = 0; i < n; i++) {
+        const lp_batch_spec& s = specs[i];
+        const size_t rbytes = fact_type(s.type) ? fact_row_bytes(s.type, s.K) : row_bytes(s.type, s.K);
+        if (s.N > 0 && (rc = resolve_weights(*c, s.w, rbytes * (size_t)s.N, &ds[i].w)) != LP_OK) return rc;
+        std::memcpy(c->x_pin + xo[i], s.x, sizeof(float) * (size_t)s.K);
+        ds[i].x = c->xd + xo[i];
+        ds[i].y = c->yd + yo[i];
+    }
+    if (xt) LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, 4 * xt, hipMemcpyHostToDevice, c->stream));
+    if ((rc = batch_dev(ds.data(), n, c->ws, c->ws_cap, c->stream)) != LP_OK) return rc;
+    if (yt) LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, 4 * yt, hipMemcpyDeviceToHost, c->stream));
+    LP_HIP(hipStreamSynchronize(c->stream));
+    for (int i = 0; i < n; i++) std::memcpy(specs[i].y, c->y_pin + yo[i], sizeof(float) * (size_t)specs[i].N);
+    return LP_OK;
+}
+
+bool lp_gemm_batch(const lp_batch_spec* specs, int n) {
+    int rc = host_gemm_batch(specs, n);
+    if (rc != LP_OK && rc != LP_UNSUPPORTED) fprintf(stderr, "[laplace_hip] %s\n", g_err);
+    return rc == LP_OK;
+}
+
 bool lp_moe_grouped(const float* x, int multi, const int* topk_idx, const uint8_t* w,
                     uint32_t type, float* y, int T, int topk, int n_experts, int K, int N) {
     int rc = host_moe_grouped(x, multi ? 1 : 0, topk_idx, w, type, y, T, topk, n_experts, K, N);

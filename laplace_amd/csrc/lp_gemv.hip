@@ -268,16 +268,34 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // FUSEQ: the workgroup quantizes the fp32 activation row x itself (same
 // arithmetic as quantize_act_kernel) into its LDS copy, so a GEMV step is
 // one launch; otherwise it copies the quantizer's codes from A.
-template <int L, bool XPOSE, bool FUSEQ>
+// MULTI: the launch covers up to kBatchMax weight matrices of the same K that
+// share the activation row (matmul_gemm_batch's Q/K/V and gate/up specs,
+// src/arch_gemma4.cpp:318-327, :694-700): matrix i owns row groups
+// [gstart[i], gstart[i+1]) of one index space, so one launch (one ramp-up and
+// one tail) serves all of them.
+template <int L, bool XPOSE, bool FUSEQ, bool MULTI = false>
 __global__ void __launch_bounds__(1024)
 gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
-            int K, int N) {
+            int K, int N, SbBatch bt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int RPW = 64 / L;                   // rows per wave per step
     const int lane = threadIdx.x & 63;
     const int nsb = K >> 8;
     const long rb = (long)nsb * 144;
-    const long total = (long)N * rb;
+    long total = (long)N * rb;
+    // row groups g < gend are this launch's work; `cur` is the matrix of the
+    // group being loaded (MULTI only: its weights, output, rows, first group)
+    const long gend = MULTI ? bt.gstart[bt.count] : ((long)N + RPW - 1) / RPW;
+    long gfirst = 0;
+    auto select = [&](long g) {
+        if constexpr (MULTI) {
+            const int i = (g >= bt.gstart[1]) + (g >= bt.gstart[2]) + (g >= bt.gstart[3]);
+            w = i == 0 ? bt.w[0] : i == 1 ? bt.w[1] : i == 2 ? bt.w[2] : bt.w[3];
+            N = i == 0 ? bt.n[0] : i == 1 ? bt.n[1] : i == 2 ? bt.n[2] : bt.n[3];
+            gfirst = i == 0 ? bt.gstart[0] : i == 1 ? bt.gstart[1] : i == 2 ? bt.gstart[2] : bt.gstart[3];
+            total = (long)N * rb;
+        }
+    };
     const int sl = lane & (L - 1);
     const int rsub = lane / L;
     const bool active = sl < nsb;
@@ -290,7 +308,9 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
     uint8_t* wbuf = smem + xbuf_off + (size_t)((threadIdx.x >> 6) * 9216);
     const uint32_t act_l = lds_addr_of(smem) + sb * 272;
 
-    auto load_group = [&](long g, u32x4 (&v)[9]) {
+    auto load_group = [&](long gg, u32x4 (&v)[9]) {
+        select(gg);
+        const long g = gg - gfirst;
         if constexpr (XPOSE) {
             const long gbeg = g * RPW * rb;
             const long gend_full = gbeg + RPW * rb;
@@ -332,7 +352,7 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
             xd[k] = dl[8 * sb + k];
             xs[k] = sl_[8 * sb + k];
         }
-        if (g * RPW < N) load_group(g, v);
+        if (g < gend) load_group(g, v);
     } else {
         for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
             const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
@@ -344,12 +364,18 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
             xs[k] = A.sum[8 * sb + k];
         }
         __syncthreads();
-        if (g * RPW < N) load_group(g, v);
+        if (g < gend) load_group(g, v);
     }
 
     // 4. row groups
-    while (g * RPW < N) {
-        const long row = g * RPW + rsub;
+    while (g < gend) {
+        const long row = (g - gfirst) * RPW + rsub;
+        float* yc = y;
+        if constexpr (MULTI) {
+            const int i = (g >= bt.gstart[1]) + (g >= bt.gstart[2]) + (g >= bt.gstart[3]);
+            yc = i == 0 ? bt.y[0] : i == 1 ? bt.y[1] : i == 2 ? bt.y[2] : bt.y[3];
+        }
+        const int nc = N;
         if constexpr (XPOSE) {
 #pragma unroll
             for (int k = 0; k < 9; k++) *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v[k];
@@ -395,9 +421,9 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         }
         t = active ? t : 0.0f;
         const float sum = group_sum(t, L);        // lands in lane L-1 of the group
-        if (sl == L - 1 && row < N) y[row] = sum;
+        if (sl == L - 1 && row < nc) yc[row] = sum;
         g += nwaves;
-        if (g * RPW < N) load_group(g, v);
+        if (g < gend) load_group(g, v);
     }
 }
 
@@ -1061,8 +1087,53 @@ static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, const float*
     const size_t shm = act_lds + (XPOSE ? wg_waves * 9216 : 0);
 #define LP_S(LL)                                                                                       \
     case LL:                                                                                           \
-        if (x) hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, true>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N); \
-        else hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, false>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N); \
+        if (x) hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, true>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N, SbBatch{}); \
+        else hipLaunchKernelGGL((gemv_q4k_sb<LL, XPOSE, false>), dim3(grid), dim3(64 * wg_waves), shm, st, w, A, x, y, K, N, SbBatch{}); \
+        break;
+    switch (L) {
+        LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef LP_S
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, const int* n, int count,
+                                   const float* x, int K, hipStream_t st) {
+    const int L = sb_lanes(K);
+    if (count < 1 || count > kBatchMax || L == 0) return hipErrorInvalidValue;
+    const int rpw = 64 / L;
+    SbBatch bt{};
+    bt.count = count;
+    long groups = 0;
+    for (int i = 0; i < kBatchMax; i++) {
+        bt.gstart[i] = groups;
+        if (i < count) {
+            if (n[i] < 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0) return hipErrorInvalidValue;
+            bt.w[i] = w[i];
+            bt.y[i] = y[i];
+            bt.n[i] = n[i];
+            groups += ((long)n[i] + rpw - 1) / rpw;
+        }
+    }
+    bt.gstart[kBatchMax] = groups;
+    if (groups == 0) return hipSuccess;
+    // matrices with no rows own an empty range; give them a valid pointer anyway
+    for (int i = 0; i < count; i++) if (bt.n[i] == 0) { bt.w[i] = bt.w[0]; }
+    const int wg_waves_max = 16;
+    const size_t act_lds = ((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
+    int wg_waves = (int)((160 * 1024 - act_lds) / 9216);
+    if (wg_waves > wg_waves_max) wg_waves = wg_waves_max;
+    if (wg_waves < 1) return hipErrorInvalidValue;
+    long waves = groups;
+    const long cap = (long)device_cu_count() * 16;
+    if (waves > cap) waves = cap;
+    const unsigned grid = (unsigned)((waves + wg_waves - 1) / wg_waves);
+    const size_t shm = act_lds + (size_t)wg_waves * 9216;
+#define LP_S(LL)                                                                                       \
+    case LL:                                                                                           \
+        hipLaunchKernelGGL((gemv_q4k_sb<LL, true, true, true>), dim3(grid), dim3(64 * wg_waves), shm, st, \
+                           bt.w[0], ActView{}, x, bt.y[0], K, bt.n[0], bt);                             \
         break;
     switch (L) {
         LP_S(2) LP_S(4) LP_S(8) LP_S(16) LP_S(32) LP_S(64)

@@ -56,6 +56,21 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float*
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w);
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, float* y, int M, int K,
                              int N, hipStream_t st);
+// Q4_K weight matrices of one multi-matrix GEMV launch (same K, same
+// activation row): matrix i is n[i] rows at w[i], output y[i], and owns the
+// row groups [gstart[i], gstart[i+1]) of the launch (gstart[count..] = total).
+constexpr int kBatchMax = 4;
+struct SbBatch {
+    const uint8_t* w[kBatchMax];
+    float* y[kBatchMax];
+    int n[kBatchMax];
+    long gstart[kBatchMax + 1];
+    int count;
+};
+// One launch of quantize + Q4_K GEMV over count <= kBatchMax matrices sharing x
+// (each supported by gemv_fused_supported).
+hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, const int* n, int count,
+                                   const float* x, int K, hipStream_t st);
 // Q4_K products for M >= 2 activation rows (lp_gemm.hip), on the fp16
 // "planes" of the activations (gemm_planes_bytes(M, K) bytes of scratch):
 // M <= 16 on the small-M MFMA kernel, larger M on the tiled GEMM.

@@ -185,9 +185,34 @@ def dequantize(w: Tensor, dst, n: int) -> None:
 
 
 def matmul_gemm_batch(specs) -> bool:
-    """src/matmul.cpp:450-454: each spec (x, w, y, K, N) is an M = 1 matmul."""
-    for x, w, y, K, N in specs:
-        matmul_rows(x, w, y, 1, K, N)
+    """src/matmul.h:46-54, src/matmul.cpp:450-454: each spec (x, w, y, K, N)
+    is an M = 1 matmul. One C-ABI call for the whole batch (lp_gemm_batch /
+    lp_gemm_batch_dev): consecutive Q4_K specs sharing x and K run as one
+    launch. All x/y are numpy arrays (host path) or all torch GPU tensors."""
+    from ._lib import BatchSpec
+    specs = list(specs)
+    if not specs:
+        return True
+    arr = (BatchSpec * len(specs))()
+    dev = _is_torch(specs[0][0])
+    for i, (x, w, y, K, N) in enumerate(specs):
+        if _is_torch(x) != dev or _is_torch(y) != dev:
+            raise TypeError("a batch is all host arrays or all device tensors")
+        if not dev:
+            assert x.dtype == np.float32 and y.dtype == np.float32
+        arr[i] = BatchSpec(_ptr(x), _ptr(w.data), int(w.type), _ptr(y), K, N)
+    L = lib()
+    if dev:
+        import torch
+        nb = int(L.lp_gemm_batch_workspace_bytes(arr, len(specs)))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=specs[0][0].device)
+        rc = L.lp_gemm_batch_dev(arr, len(specs), ws.data_ptr(), nb, _stream_ptr())
+        if rc == LP_UNSUPPORTED:
+            raise NotImplementedError(L.lp_last_error().decode())
+        check(rc, "lp_gemm_batch_dev")
+        return True
+    if not L.lp_gemm_batch(arr, len(specs)):
+        raise NotImplementedError(f"lp_gemm_batch: {L.lp_last_error().decode()}")
     return True
 
 
