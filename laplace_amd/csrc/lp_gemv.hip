@@ -1154,6 +1154,13 @@ static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t s
     if (ngroups == 1) {
         const long cap = (long)device_cu_count() * 16;
         if (waves > cap) waves = cap;
+    } else if (((groups + 1) / 2 + kSbmWaves - 1) / kSbmWaves * (long)ngroups >= 4L * device_cu_count()) {
+        // MoE groups, when there are enough of them to fill the GPU: each wave
+        // takes two row groups of its expert, so a workgroup's activation
+        // staging serves twice the weight bytes (measured: 161 -> 147 us per
+        // layer at 64 tokens; three or four groups per wave were no faster,
+        // and at one token the halved grid was slower)
+        waves = (groups + 1) / 2;
     }
     const unsigned gx = (unsigned)((waves + kSbmWaves - 1) / kSbmWaves);
     const int nsb = args.K / 256, nb = args.K / 32;
