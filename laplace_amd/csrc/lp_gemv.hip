@@ -330,7 +330,8 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         }
     };
     const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
-    long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    // wave-uniform (scalar registers)
+    long g = (long)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     u32x4 v[9];
 
     // 1. activation codes -> LDS; the lane's block scales and sums -> registers
@@ -383,6 +384,12 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
 #pragma unroll
             for (int k = 0; k < 9; k++) v[k] = mine[k];
         }
+        // the wave's next row group (if any) is requested before this one is
+        // computed (single matrix: the multi-matrix form has no registers left
+        // for a second set and requests it after)
+        u32x4 vn[9];
+        const bool more = g + nwaves < gend;
+        if (!MULTI && more) load_group(g + nwaves, vn);
         const u32x4 h = v[0];
         const float d = fp16_bits_to_f32(h.x), dmin = fp16_bits_to_f32(h.x >> 16);
         float t = 0.0f;
@@ -423,7 +430,11 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         const float sum = group_sum(t, L);        // lands in lane L-1 of the group
         if (sl == L - 1 && row < nc) yc[row] = sum;
         g += nwaves;
-        if (g < gend) load_group(g, v);
+        if (MULTI && more) load_group(g, v);
+        if (!MULTI && more) {
+#pragma unroll
+            for (int k = 0; k < 9; k++) v[k] = vn[k];
+        }
     }
 }
 
@@ -1107,16 +1118,17 @@ hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, con
     bt.count = count;
     long groups = 0;
     for (int i = 0; i < kBatchMax; i++) {
-        bt.gstart[i] = groups;
+        bt.gstart[i] = (int)groups;
         if (i < count) {
             if (n[i] < 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0) return hipErrorInvalidValue;
             bt.w[i] = w[i];
             bt.y[i] = y[i];
             bt.n[i] = n[i];
             groups += ((long)n[i] + rpw - 1) / rpw;
+            if (groups > (1L << 30)) return hipErrorInvalidValue;
         }
     }
-    bt.gstart[kBatchMax] = groups;
+    bt.gstart[kBatchMax] = (int)groups;
     if (groups == 0) return hipSuccess;
     // matrices with no rows own an empty range; give them a valid pointer anyway
     for (int i = 0; i < count; i++) if (bt.n[i] == 0) { bt.w[i] = bt.w[0]; }

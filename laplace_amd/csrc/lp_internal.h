@@ -64,7 +64,7 @@ struct SbBatch {
     const uint8_t* w[kBatchMax];
     float* y[kBatchMax];
     int n[kBatchMax];
-    long gstart[kBatchMax + 1];
+    int gstart[kBatchMax + 1];
     int count;
 };
 // One launch of quantize + Q4_K GEMV over count <= kBatchMax matrices sharing x
