@@ -344,9 +344,138 @@ gemv_q50_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, float* __re
     }
 }
 
+// The K-quant types with LDS staging: per-lane loads of a chunk's scattered
+// fields (scales, code bytes, high bits) and of its 32 x values are bound by
+// the texture-address unit. Instead each wave loads its row with coalesced
+// 16-byte loads (lane l: bytes 16l of each KiB), writes it to a per-wave LDS
+// buffer and decodes its chunks from there (chunk_decode on LDS pointers);
+// the workgroup stages the MR activation rows in LDS once (144-byte stride
+// per 32-element chunk, so the 8 float4 reads of a chunk are conflict-free
+// across lanes). The next row's bytes are requested before the current row is
+// computed. Same per-chunk arithmetic and wave sum as gemv_fact_kernel.
+constexpr int kFactLdsPieces = 11;          // row <= 11 KiB: Q5_K K <= 16384
+constexpr int kFactChunkStride = 144;       // LDS bytes per 32-element x chunk
+
+template <uint32_t T, int MR>
+__global__ void __launch_bounds__(256)
+gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict__ x, float* __restrict__ y,
+              int K, int N, int ldy) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    x += (size_t)blockIdx.y * MR * K;
+    y += (size_t)blockIdx.y * MR * ldy;
+    const int lane = threadIdx.x & 63;
+    const int nch = K >> 5;
+    const size_t xrow = (size_t)nch * kFactChunkStride;
+    // activation rows -> LDS
+    for (int m = 0; m < MR; m++) {
+        for (int i = threadIdx.x; i < (K >> 2); i += blockDim.x) {
+            const float4 v = reinterpret_cast<const float4*>(x + (size_t)m * K)[i];
+            *reinterpret_cast<float4*>(smem + m * xrow + (i >> 3) * kFactChunkStride + (i & 7) * 16) = v;
+        }
+    }
+    const size_t rbuf = (rb + 1023) & ~size_t(1023);
+    uint8_t* wb = smem + MR * xrow + (threadIdx.x >> 6) * rbuf;
+    const int nld = (int)((rb + 1023) / 1024);
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    long row = (long)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    u32x4 v[kFactLdsPieces];
+    auto load_row = [&](long r) {
+        const uint8_t* src = w + (size_t)r * rb;
+#pragma unroll
+        for (int k = 0; k < kFactLdsPieces; k++) {
+            if (k < nld) {
+                size_t o = 1024 * (size_t)k + 16 * lane;
+                o = o + 16 <= rb ? o : rb - 16;
+                v[k] = *reinterpret_cast<const u32x4*>(src + o);
+            }
+        }
+    };
+    if (row < N) load_row(row);
+    __syncthreads();
+    for (; row < N; row += nwaves) {
+        // a piece clamped to the row's last 16 bytes goes back to where it came
+        // from (rows need not be a multiple of 16 bytes)
+#pragma unroll
+        for (int k = 0; k < kFactLdsPieces; k++) {
+            if (k < nld) {
+                size_t o = 1024 * (size_t)k + 16 * lane;
+                o = o + 16 <= rb ? o : rb - 16;
+                *reinterpret_cast<u32x4*>(wb + o) = v[k];
+            }
+        }
+        if (row + nwaves < N) load_row(row + nwaves);
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+        for (int c = lane; c < nch; c += 64) {
+            float wv[32], ca[2], cb[2];
+            chunk_decode<T>(wb, c, wv, ca, cb);
+            const bool need_x = cb[0] != 0.0f || cb[1] != 0.0f;
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const float4* xp = reinterpret_cast<const float4*>(smem + m * xrow + (size_t)c * kFactChunkStride);
+                float t = acc[m];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float sx = 0.0f, xs = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 xv = xp[4 * h + q];
+                        const float* wq = wv + 16 * h + 4 * q;
+                        sx = fmaf(xv.x, wq[0], sx);
+                        sx = fmaf(xv.y, wq[1], sx);
+                        sx = fmaf(xv.z, wq[2], sx);
+                        sx = fmaf(xv.w, wq[3], sx);
+                        xs += (xv.x + xv.y) + (xv.z + xv.w);
+                    }
+                    t = fmaf(ca[h], sx, t);
+                    if (need_x) t = fmaf(cb[h], xs, t);
+                }
+                acc[m] = t;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float s2 = acc[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off, 64);
+            if (lane == 0) y[(size_t)m * ldy + row] = s2;
+        }
+    }
+}
+
+// LDS bytes of gemv_fact_lds for MR activation rows; 0 when it does not apply.
+static size_t fact_lds_bytes(uint32_t T, int MR, int K, size_t rb) {
+    if (!(T == T_Q2_K || T == T_Q3_K || T == T_Q5_K)) return 0;
+    if (rb % 4 != 0 || rb < 16 || (rb + 1023) / 1024 > kFactLdsPieces) return 0;
+    const size_t b = (size_t)MR * (K / 32) * kFactChunkStride + 4 * ((rb + 1023) & ~size_t(1023));
+    return b <= 160 * 1024 ? b : 0;
+}
+
 template <uint32_t T>
 static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int M, int K, int N, hipStream_t st) {
     const size_t rb = fact_row_bytes(T, K);
+    if constexpr (T == T_Q2_K || T == T_Q3_K || T == T_Q5_K) {
+        // one row group of up to 4 activation rows per launch (grid.y = group)
+        if (reinterpret_cast<uintptr_t>(w) % 4 == 0 && fact_lds_bytes(T, M < 4 ? M : 4, K, rb)) {
+            const long cap = (long)device_cu_count() * 12;    // 3 workgroups per CU
+            const long waves = N < cap ? N : cap;
+            const unsigned gx = (unsigned)((waves + 3) / 4);
+            for (int m0 = 0; m0 < M; m0 += 4) {
+                const int mr = M - m0 < 4 ? M - m0 : 4;
+                const float* xm = x + (size_t)m0 * K;
+                float* ym = y + (size_t)m0 * N;
+                const size_t shm = fact_lds_bytes(T, mr, K, rb);
+                switch (mr) {
+                    case 1: hipLaunchKernelGGL((gemv_fact_lds<T, 1>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                    case 2: hipLaunchKernelGGL((gemv_fact_lds<T, 2>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                    case 3: hipLaunchKernelGGL((gemv_fact_lds<T, 3>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                    default: hipLaunchKernelGGL((gemv_fact_lds<T, 4>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                }
+            }
+            return hipGetLastError();
+        }
+    }
     // one launch for the full groups of 4 activation rows (grid.y = group),
     // one for the remainder
     const int full = M / 4, rest = M % 4;
