@@ -444,6 +444,80 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
     }
 }
 
+// F32 / F16 / BF16 weights: a lane takes 8 consecutive elements of every
+// 512-element slab of the row (16-byte loads for the 2-byte types, two for
+// F32; x the same way), so each wave streams its row with fully coalesced
+// loads, four slabs in flight; fp32 products summed per lane, then over the
+// wave (dot_row_f16 / dot_row_bf16 / dot_row_f32, src/matmul.cpp:63-101,
+// reassociated).
+template <uint32_t T>
+__device__ __forceinline__ void dense8(const uint8_t* __restrict__ p, float (&o)[8]) {
+    if constexpr (T == T_F32) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (T == T_F16) {
+                o[2 * k] = h2f(u[k] & 0xffffu);
+                o[2 * k + 1] = h2f(u[k] >> 16);
+            } else {
+                o[2 * k] = __uint_as_float(u[k] << 16);
+                o[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+template <uint32_t T, int MR>
+__global__ void __launch_bounds__(256)
+gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int K,
+                  int N, int ldy) {
+    constexpr int EB = T == T_F32 ? 4 : 2;        // bytes per element
+    x += (size_t)blockIdx.y * MR * K;
+    y += (size_t)blockIdx.y * MR * ldy;
+    const int lane = threadIdx.x & 63;
+    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
+    for (long row = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; row < N; row += nwaves) {
+        const uint8_t* wr = w + (size_t)row * K * EB;
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+        for (int e0 = 8 * lane; e0 < K; e0 += 4 * 512) {
+            float wv[4][8];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (e0 + 512 * u < K) dense8<T>(wr + (size_t)(e0 + 512 * u) * EB, wv[u]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int e = e0 + 512 * u;
+                if (e < K) {
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)m * K + e);
+                        const float4 a = xp[0], b = xp[1];
+                        float t = acc[m];
+                        t = fmaf(a.x, wv[u][0], t); t = fmaf(a.y, wv[u][1], t);
+                        t = fmaf(a.z, wv[u][2], t); t = fmaf(a.w, wv[u][3], t);
+                        t = fmaf(b.x, wv[u][4], t); t = fmaf(b.y, wv[u][5], t);
+                        t = fmaf(b.z, wv[u][6], t); t = fmaf(b.w, wv[u][7], t);
+                        acc[m] = t;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float s2 = acc[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off, 64);
+            if (lane == 0) y[(size_t)m * ldy + row] = s2;
+        }
+    }
+}
+
 // LDS bytes of gemv_fact_lds for MR activation rows; 0 when it does not apply.
 static size_t fact_lds_bytes(uint32_t T, int MR, int K, size_t rb) {
     if (!(T == T_Q2_K || T == T_Q3_K || T == T_Q5_K)) return 0;
@@ -471,6 +545,25 @@ static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int 
                     case 2: hipLaunchKernelGGL((gemv_fact_lds<T, 2>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
                     case 3: hipLaunchKernelGGL((gemv_fact_lds<T, 3>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
                     default: hipLaunchKernelGGL((gemv_fact_lds<T, 4>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                }
+            }
+            return hipGetLastError();
+        }
+    }
+    if constexpr (T == T_F32 || T == T_F16 || T == T_BF16) {
+        if (reinterpret_cast<uintptr_t>(w) % 16 == 0 && K % 8 == 0) {
+            const long cap = (long)device_cu_count() * 32;
+            const long waves = N < cap ? N : cap;
+            const unsigned gx = (unsigned)((waves + 3) / 4);
+            for (int m0 = 0; m0 < M; m0 += 4) {
+                const int mr = M - m0 < 4 ? M - m0 : 4;
+                const float* xm = x + (size_t)m0 * K;
+                float* ym = y + (size_t)m0 * N;
+                switch (mr) {
+                    case 1: hipLaunchKernelGGL((gemv_dense_kernel<T, 1>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
+                    case 2: hipLaunchKernelGGL((gemv_dense_kernel<T, 2>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
+                    case 3: hipLaunchKernelGGL((gemv_dense_kernel<T, 3>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
+                    default: hipLaunchKernelGGL((gemv_dense_kernel<T, 4>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
                 }
             }
             return hipGetLastError();
