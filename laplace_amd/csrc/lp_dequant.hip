@@ -447,7 +447,7 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
 // F32 / F16 / BF16 weights: a lane takes 8 consecutive elements of every
 // 512-element slab of the row (16-byte loads for the 2-byte types, two for
 // F32; x the same way), so each wave streams its row with fully coalesced
-// loads, four slabs in flight; fp32 products summed per lane, then over the
+// loads, eight slabs in flight; fp32 products summed per lane, then over the
 // wave (dot_row_f16 / dot_row_bf16 / dot_row_f32, src/matmul.cpp:63-101,
 // reassociated).
 template <uint32_t T>
@@ -471,6 +471,8 @@ __device__ __forceinline__ void dense8(const uint8_t* __restrict__ p, float (&o)
     }
 }
 
+constexpr int kDenseU = 8;                  // slabs in flight per lane
+
 template <uint32_t T, int MR>
 __global__ void __launch_bounds__(256)
 gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int K,
@@ -485,13 +487,13 @@ gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, fl
         float acc[MR];
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[m] = 0.0f;
-        for (int e0 = 8 * lane; e0 < K; e0 += 4 * 512) {
-            float wv[4][8];
+        for (int e0 = 8 * lane; e0 < K; e0 += kDenseU * 512) {
+            float wv[kDenseU][8];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
+            for (int u = 0; u < kDenseU; u++)
                 if (e0 + 512 * u < K) dense8<T>(wr + (size_t)(e0 + 512 * u) * EB, wv[u]);
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < kDenseU; u++) {
                 const int e = e0 + 512 * u;
                 if (e < K) {
 #pragma unroll
