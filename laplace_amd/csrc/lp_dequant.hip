@@ -199,24 +199,37 @@ __device__ __forceinline__ void chunk_decode(const uint8_t* __restrict__ wr, int
             b[h] = -(dmin * (float)(s >> 4));
         }
     } else if constexpr (T == T_Q3_K) {
+        // The 110-byte block is 2-byte aligned: its 32 hmask bytes and the 32
+        // code bytes of chunk g are read as dwords from the aligned-down
+        // address and funnel-shifted. Per byte u = low2 | hbit << 2 (0..7),
+        // the reference's code being u - 4: chunk = a * sum(x*u) - 4a * sum(x).
         const uint8_t* blk = wr + (size_t)(c >> 3) * 110;
         const int g = c & 7;
-        // 2-byte aligned block: bytes via 16-bit loads
-        const uint16_t* hm = reinterpret_cast<const uint16_t*>(blk);
-        const uint16_t* qs = reinterpret_cast<const uint16_t*>(blk + 32 + 32 * (g >> 2));
-        const int sh = 2 * (g & 3);
+        const uintptr_t ab = reinterpret_cast<uintptr_t>(blk);
+        const uint32_t sh = (uint32_t)(ab & 3);
+        const uint32_t* hp = reinterpret_cast<const uint32_t*>(ab - sh);
+        const uint32_t* qp = reinterpret_cast<const uint32_t*>(ab - sh + 32 + 32 * (g >> 2));
+        uint32_t hw_[9], qw_[9];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const uint32_t lo = ((uint32_t)qs[k] >> sh) & 0x0303u;
-            const uint32_t hb = ((uint32_t)hm[k] >> g) & 0x0101u;
-            q[2 * k] = (float)((int)(lo & 0xff) - 4 + 4 * (int)(hb & 0xff));
-            q[2 * k + 1] = (float)((int)(lo >> 8) - 4 + 4 * (int)(hb >> 8));
+        for (int k = 0; k < 9; k++) {
+            hw_[k] = hp[k];
+            qw_[k] = qp[k];
+        }
+        const int s2 = 2 * (g & 3);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t hv = alignb(hw_[k + 1], hw_[k], sh), qv = alignb(qw_[k + 1], qw_[k], sh);
+            const uint32_t u = ((qv >> s2) & 0x03030303u) | (((hv >> g) & 0x01010101u) << 2);
+            q[4 * k] = (float)(u & 0xff);
+            q[4 * k + 1] = (float)((u >> 8) & 0xff);
+            q[4 * k + 2] = (float)((u >> 16) & 0xff);
+            q[4 * k + 3] = (float)(u >> 24);
         }
         const float d = h2f(rd16(blk + 108));
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             a[h] = d * (float)(q3k_scale(blk + 96, 2 * g + h) - 32);
-            b[h] = 0.0f;
+            b[h] = -4.0f * a[h];
         }
     } else {
 #pragma unroll
@@ -366,11 +379,25 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
     const int lane = threadIdx.x & 63;
     const int nch = K >> 5;
     const size_t xrow = (size_t)nch * kFactChunkStride;
-    // activation rows -> LDS
+    // activation rows -> LDS; each chunk's 16-element half sums go into the
+    // chunk's 16 padding bytes (the same for every weight row)
     for (int m = 0; m < MR; m++) {
         for (int i = threadIdx.x; i < (K >> 2); i += blockDim.x) {
             const float4 v = reinterpret_cast<const float4*>(x + (size_t)m * K)[i];
             *reinterpret_cast<float4*>(smem + m * xrow + (i >> 3) * kFactChunkStride + (i & 7) * 16) = v;
+        }
+    }
+    __syncthreads();
+    for (int m = 0; m < MR; m++) {
+        for (int i = threadIdx.x; i < 2 * nch; i += blockDim.x) {
+            const float4* xp = reinterpret_cast<const float4*>(smem + m * xrow + (i >> 1) * kFactChunkStride) + 4 * (i & 1);
+            float xs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 xv = xp[q];
+                xs += (xv.x + xv.y) + (xv.z + xv.w);
+            }
+            reinterpret_cast<float*>(smem + m * xrow + (i >> 1) * kFactChunkStride + 128)[i & 1] = xs;
         }
     }
     const size_t rbuf = (rb + 1023) & ~size_t(1023);
@@ -414,10 +441,11 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
 #pragma unroll
             for (int m = 0; m < MR; m++) {
                 const float4* xp = reinterpret_cast<const float4*>(smem + m * xrow + (size_t)c * kFactChunkStride);
+                const float2 xsum = *reinterpret_cast<const float2*>(smem + m * xrow + (size_t)c * kFactChunkStride + 128);
                 float t = acc[m];
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    float sx = 0.0f, xs = 0.0f;
+                    float sx = 0.0f;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const float4 xv = xp[4 * h + q];
@@ -426,10 +454,9 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
                         sx = fmaf(xv.y, wq[1], sx);
                         sx = fmaf(xv.z, wq[2], sx);
                         sx = fmaf(xv.w, wq[3], sx);
-                        xs += (xv.x + xv.y) + (xv.z + xv.w);
                     }
                     t = fmaf(ca[h], sx, t);
-                    if (need_x) t = fmaf(cb[h], xs, t);
+                    if (need_x) t = fmaf(cb[h], h ? xsum.y : xsum.x, t);
                 }
                 acc[m] = t;
             }
