@@ -564,16 +564,20 @@ static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int 
             const long cap = (long)device_cu_count() * 12;    // 3 workgroups per CU
             const long waves = N < cap ? N : cap;
             const unsigned gx = (unsigned)((waves + 3) / 4);
-            for (int m0 = 0; m0 < M; m0 += 4) {
-                const int mr = M - m0 < 4 ? M - m0 : 4;
-                const float* xm = x + (size_t)m0 * K;
-                float* ym = y + (size_t)m0 * N;
-                const size_t shm = fact_lds_bytes(T, mr, K, rb);
-                switch (mr) {
+            // full groups of 4 activation rows in one launch (grid.y = group),
+            // the remainder in a second
+            const int full = M / 4, rest = M % 4;
+            if (full)
+                hipLaunchKernelGGL((gemv_fact_lds<T, 4>), dim3(gx, full), dim3(256), fact_lds_bytes(T, 4, K, rb), st,
+                                   w, rb, x, y, K, N, N);
+            if (rest) {
+                const float* xm = x + (size_t)full * 4 * K;
+                float* ym = y + (size_t)full * 4 * N;
+                const size_t shm = fact_lds_bytes(T, rest, K, rb);
+                switch (rest) {
                     case 1: hipLaunchKernelGGL((gemv_fact_lds<T, 1>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
                     case 2: hipLaunchKernelGGL((gemv_fact_lds<T, 2>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
-                    case 3: hipLaunchKernelGGL((gemv_fact_lds<T, 3>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
-                    default: hipLaunchKernelGGL((gemv_fact_lds<T, 4>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
+                    default: hipLaunchKernelGGL((gemv_fact_lds<T, 3>), dim3(gx), dim3(256), shm, st, w, rb, xm, ym, K, N, N); break;
                 }
             }
             return hipGetLastError();
@@ -584,15 +588,16 @@ static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int 
             const long cap = (long)device_cu_count() * 32;
             const long waves = N < cap ? N : cap;
             const unsigned gx = (unsigned)((waves + 3) / 4);
-            for (int m0 = 0; m0 < M; m0 += 4) {
-                const int mr = M - m0 < 4 ? M - m0 : 4;
-                const float* xm = x + (size_t)m0 * K;
-                float* ym = y + (size_t)m0 * N;
-                switch (mr) {
+            const int full = M / 4, rest = M % 4;
+            if (full)
+                hipLaunchKernelGGL((gemv_dense_kernel<T, 4>), dim3(gx, full), dim3(256), 0, st, w, x, y, K, N, N);
+            if (rest) {
+                const float* xm = x + (size_t)full * 4 * K;
+                float* ym = y + (size_t)full * 4 * N;
+                switch (rest) {
                     case 1: hipLaunchKernelGGL((gemv_dense_kernel<T, 1>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
                     case 2: hipLaunchKernelGGL((gemv_dense_kernel<T, 2>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
-                    case 3: hipLaunchKernelGGL((gemv_dense_kernel<T, 3>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
-                    default: hipLaunchKernelGGL((gemv_dense_kernel<T, 4>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
+                    default: hipLaunchKernelGGL((gemv_dense_kernel<T, 3>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
                 }
             }
             return hipGetLastError();

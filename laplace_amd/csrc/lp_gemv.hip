@@ -1357,19 +1357,29 @@ moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict_
         sc += cnt[e];
         sg += (cnt[e] + gsize - 1) / gsize;
     }
-    part[2 * tid] = sc;
-    part[2 * tid + 1] = sg;
-    __syncthreads();
-    for (int o = 1; o < nt; o <<= 1) {
-        const int a = tid >= o ? part[2 * (tid - o)] : 0;
-        const int b = tid >= o ? part[2 * (tid - o) + 1] : 0;
-        __syncthreads();
-        part[2 * tid] += a;
-        part[2 * tid + 1] += b;
-        __syncthreads();
+    // inclusive scan of (sc, sg): within the wave by shuffles, then the
+    // preceding waves' totals from LDS (one barrier)
+    const int lane = tid & 63, wv = tid >> 6;
+    int ia = sc, ib = sg;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ta = __shfl_up(ia, o, 64), tb = __shfl_up(ib, o, 64);
+        if (lane >= o) {
+            ia += ta;
+            ib += tb;
+        }
     }
-    sc = part[2 * tid] - sc;        // exclusive prefix
-    sg = part[2 * tid + 1] - sg;
+    if (lane == 63) {
+        part[2 * wv] = ia;
+        part[2 * wv + 1] = ib;
+    }
+    __syncthreads();
+    for (int v = 0; v < wv; v++) {
+        ia += part[2 * v];
+        ib += part[2 * v + 1];
+    }
+    sc = ia - sc;                   // exclusive prefix
+    sg = ib - sg;
     for (int e = e0; e < e1; e++) {
         off[e] = sc;
         goff[e] = sg;
@@ -1381,7 +1391,7 @@ moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict_
         sc += c;
         sg += (c + gsize - 1) / gsize;
     }
-    if (tid == nt - 1) ngroups[0] = part[2 * tid + 1];
+    if (tid == nt - 1) ngroups[0] = ib;
     __syncthreads();
     // scatter: slot within the expert from a second round of atomics
     for (int e = tid; e < E; e += nt) cnt[e] = 0;
