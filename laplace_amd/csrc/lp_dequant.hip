@@ -306,6 +306,10 @@ gemv_q50_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, float* __re
     const int lane = threadIdx.x & 63;
     const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
     const int nb = K >> 5;
+    // blockIdx.y: which group of MR activation rows
+    A.qs += (size_t)blockIdx.y * MR * K;
+    A.d += (size_t)blockIdx.y * MR * nb;
+    y += (size_t)blockIdx.y * MR * N;
     for (long row = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; row < N; row += nwaves) {
         const uint8_t* wr = w + (size_t)row * rb;
         float acc[MR];
@@ -634,22 +638,22 @@ hipError_t launch_gemv_q50(const uint8_t* w, const ActView& A, float* y, int M, 
     if (waves > cap) waves = cap;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     const int nb = K / 32;
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        const int mr = M - m0 < 4 ? M - m0 : 4;
+    // full groups of 4 activation rows in one launch (grid.y = group), the
+    // remainder in a second
+    const int full = M / 4, rest = M % 4;
+    if (full) hipLaunchKernelGGL((gemv_q50_kernel<4>), dim3(grid, full), dim3(256), 0, st, w, rb, A, y, K, N);
+    if (rest) {
         ActView Am = A;
-        Am.qs = A.qs + (size_t)m0 * K;
-        Am.d = A.d + (size_t)m0 * nb;
-        float* ym = y + (size_t)m0 * N;
-        switch (mr) {
+        Am.qs = A.qs + (size_t)full * 4 * K;
+        Am.d = A.d + (size_t)full * 4 * nb;
+        float* ym = y + (size_t)full * 4 * N;
+        switch (rest) {
             case 1: hipLaunchKernelGGL((gemv_q50_kernel<1>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
             case 2: hipLaunchKernelGGL((gemv_q50_kernel<2>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
-            case 3: hipLaunchKernelGGL((gemv_q50_kernel<3>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
-            default: hipLaunchKernelGGL((gemv_q50_kernel<4>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
+            default: hipLaunchKernelGGL((gemv_q50_kernel<3>), dim3(grid), dim3(256), 0, st, w, rb, Am, ym, K, N); break;
         }
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    return hipGetLastError();
 }
 
 bool fact_type(uint32_t type) {
