@@ -155,6 +155,10 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
 
 static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t type, float* y,
                   int M, int K, int N, hipStream_t st) {
+    if (i8mf_supported(type, M, K, w)) {
+        LP_HIP(launch_gemv_i8mf(w, A, y, M, K, N, st));
+        return LP_OK;
+    }
     if (planes && gemm_supported(type, M, K)) {
         LP_HIP(launch_gemm(type, w, A, planes, y, M, K, N, st));
         return LP_OK;
@@ -293,6 +297,10 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         LP_HIP(launch_gemv_fact(type, wd, c->xd, c->yd, M, K, N, c->stream));
     } else if (gemv_fused_supported(type, M, K, wd)) {
         LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
+    } else if (i8mf_supported(type, M, K, wd)) {
+        const ActView A = ws_view(c->ws, M, K);
+        LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
+        LP_HIP(launch_gemv_i8mf(wd, A, c->yd, M, K, N, c->stream));
     } else if (gemm_supported(type, M, K)) {
         void* planes = ws_planes(c->ws, M, K);
         LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));
@@ -585,7 +593,7 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
         LP_HIP(launch_gemv_fused(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
         return LP_OK;
     }
-    if (gemm_supported(type, M, K)) {
+    if (gemm_supported(type, M, K) && !i8mf_supported(type, M, K, w)) {
         // fp16 planes straight from x (one pass), then the MFMA product
         if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
             set_err("workspace %zu < %zu bytes or null pointer", wsb, ws_bytes(M, K));

@@ -994,6 +994,9 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
 constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
 constexpr int kMfMaxM = 16;
+// Measured on MI355X (Q4_K 18944 x 3584): the GEMV tile kernel is faster
+// up to M = 4, the small-M MFMA kernels from M = 5 to 16.
+constexpr int kMfMinM = 5;
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 struct MfArgs {
@@ -1129,6 +1132,132 @@ gemv_q4k_mf(MfArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K for 5 <= M <= 16 activation rows on int8 MFMA (v_mfma_i32_16x16x32_i8,
+// one 32-element block per instruction): A = the tokens' int8 codes straight
+// from the quantized blocks (16 rows, unused rows zero), B = the weights'
+// 4-bit codes as int8 (16 weight rows), D = the exact per-block int32 sums
+// P_mnb of the reference's dot_row_q4_k_int_neon (src/matmul_simd.cpp:226-283).
+// Epilogue per block: acc += P * (xd_m * d_n*sc_nb); per super-block the min
+// term -dmin_n * sum_b m_nb * xs_mb. Same workgroup shape as gemv_q4k_mf
+// (32 weight rows x 8 waves, each wave a K-slice of whole super-blocks, slices
+// summed in a fixed order through LDS); the activation codes are read once
+// per workgroup (one byte per element, a quarter of the fp16 hi/lo planes'
+// traffic), and the block scales and sums are staged in LDS as [block][token]
+// so a lane's four tokens come in one read. Operand layout checked on the
+// device: A row = lane%16, k = 8*(lane/16)+e; B column = lane%16; D row =
+// 4*(lane/16)+r, column = lane%16.
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(64 * kMfWaves)
+gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N) {
+    __shared__ f4v red[kMfWaves][kMfTiles][64];
+    extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd, then [nb][16] xs
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int tok = lane & 15, g = lane >> 4;
+    const int nsb = K >> 8, nb = K >> 5;
+    float* sxs = sdx + (size_t)nb * 16;
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
+        const int b = i >> 4, t = i & 15;
+        sdx[i] = t < M ? A.d[(size_t)t * nb + b] : 0.0f;
+        sxs[i] = t < M ? A.sum[(size_t)t * nb + b] : 0.0f;
+    }
+    __syncthreads();
+    const bool tv = tok < M;
+    const int8_t* aq = A.qs + (size_t)(tv ? tok : 0) * K + 8 * g;
+    const int row0 = blockIdx.x * (16 * kMfTiles) + (lane & 15);
+    const int sb0 = wv * nsb / kMfWaves, sb1 = (wv + 1) * nsb / kMfWaves;
+    const uint8_t* wr[kMfTiles];
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) {
+        int row = row0 + 16 * t;
+        row = row < N ? row : N - 1;
+        wr[t] = w + (size_t)row * rb;
+    }
+    const i4v zi = {0, 0, 0, 0};
+    const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4v acc[kMfTiles];
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) acc[t] = z4;
+    for (int s = sb0; s < sb1; s++) {
+        u32x4 h[kMfTiles];
+        uint2 q[kMfTiles][4];
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) {
+            const uint8_t* blk = wr[t] + 144 * s;
+            h[t] = *reinterpret_cast<const u32x4*>(blk);
+#pragma unroll
+            for (int jb = 0; jb < 4; jb++) q[t][jb] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * jb + 8 * g);
+        }
+        long av[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) av[b] = tv ? *reinterpret_cast<const long*>(aq + 32 * (8 * s + b)) : 0L;
+        f4v mnacc[kMfTiles];
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) mnacc[t] = z4;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const f4v xd = *reinterpret_cast<const f4v*>(sdx + (size_t)(8 * s + b) * 16 + 4 * g);
+            const f4v xs = *reinterpret_cast<const f4v*>(sxs + (size_t)(8 * s + b) * 16 + 4 * g);
+#pragma unroll
+            for (int t = 0; t < kMfTiles; t++) {
+                uint32_t sc, mn;
+                scale_min_k4(b, h[t].y, h[t].z, h[t].w, sc, mn);
+                const uint2 u = q[t][b >> 1];
+                const uint32_t lo = (b & 1) ? (u.x >> 4) & 0x0f0f0f0fu : u.x & 0x0f0f0f0fu;
+                const uint32_t hi = (b & 1) ? (u.y >> 4) & 0x0f0f0f0fu : u.y & 0x0f0f0f0fu;
+                const long bw = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+                const i4v S = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[b], bw, zi, 0, 0, 0);
+                const float dsc = fp16_bits_to_f32(h[t].x) * (float)sc;
+                const float fm = (float)mn;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    acc[t][r] = fmaf((float)S[r], xd[r] * dsc, acc[t][r]);
+                    mnacc[t][r] = fmaf(fm, xs[r], mnacc[t][r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kMfTiles; t++) {
+            const float dmin = fp16_bits_to_f32(h[t].x >> 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[t][r] = fmaf(-dmin, mnacc[t][r], acc[t][r]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kMfTiles; t++) red[wv][t][lane] = acc[t];
+    __syncthreads();
+    // wave t sums tile t over the K-slices in a fixed order
+    if (wv < kMfTiles) {
+        const int t = wv;
+        f4v sum = red[0][t][lane];
+#pragma unroll
+        for (int i = 1; i < kMfWaves; i++) sum += red[i][t][lane];
+        const int row = row0 + 16 * t;
+        if (row < N) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tt = 4 * g + r;
+                if (tt < M) y[(size_t)tt * N + row] = sum[r];
+            }
+        }
+    }
+}
+
+bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w) {
+    return type == T_Q4_K && M >= kMfMinM && M <= kMfMaxM && K % 256 == 0 &&
+           (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+}
+
+hipError_t launch_gemv_i8mf(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (!i8mf_supported(T_Q4_K, M, K, w)) return hipErrorInvalidValue;
+    const size_t shm = (size_t)(K / 32) * 16 * 8;
+    hipLaunchKernelGGL(gemv_q4k_i8mf, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles)), dim3(64 * kMfWaves), shm, st,
+                       w, (long)row_bytes(T_Q4_K, K), A, y, M, K, N);
+    return hipGetLastError();
+}
+
 // y = 0 (a kernel, not a memset, so the sequence can be captured in a graph)
 __global__ void __launch_bounds__(256) zero_f32_kernel(float* __restrict__ y, size_t n) {
     const size_t i = (size_t)blockIdx.x * 1024 + threadIdx.x;   // y may be only 4-byte aligned
@@ -1143,9 +1272,6 @@ size_t gemm_planes_bytes(int M, int K) {
     return 2 * r((size_t)M * K * 2) + 2 * r((size_t)M * (K / 32) * 2) + r((size_t)M * 4);
 }
 
-// Measured on MI355X (Q4_K 18944 x 3584): the GEMV tile kernel is faster
-// up to M = 4, the small-M MFMA kernel from M = 5 to 16.
-constexpr int kMfMinM = 5;
 
 bool gemm_supported(uint32_t type, int M, int K) {
     return type == T_Q4_K && M >= kMfMinM && K % 256 == 0;
