@@ -156,7 +156,7 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
 static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t type, float* y,
                   int M, int K, int N, hipStream_t st) {
     if (i8mf_supported(type, M, K, w)) {
-        LP_HIP(launch_gemv_i8mf(w, A, y, M, K, N, st));
+        LP_HIP(launch_gemv_i8mf(type, w, A, y, M, K, N, st));
         return LP_OK;
     }
     if (planes && gemm_supported(type, M, K)) {
@@ -300,7 +300,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     } else if (i8mf_supported(type, M, K, wd)) {
         const ActView A = ws_view(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
-        LP_HIP(launch_gemv_i8mf(wd, A, c->yd, M, K, N, c->stream));
+        LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
     } else if (gemm_supported(type, M, K)) {
         void* planes = ws_planes(c->ws, M, K);
         LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));

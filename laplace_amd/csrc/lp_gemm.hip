@@ -1244,17 +1244,145 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
     }
 }
 
-bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w) {
-    return type == T_Q4_K && M >= kMfMinM && M <= kMfMaxM && K % 256 == 0 &&
-           (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+// Q6_K for 5 <= M <= 16 on the same int8 MFMA: B = the 6-bit codes minus 32
+// as int8 (ql nibble | qh bits << 4, then -32 per byte), so D is the exact
+// sum of (code - 32) * q. The two 16-element halves of a 32-element block
+// have their own int8 scale, so a block takes two MFMAs (lanes of the other
+// half zeroed in B) and the epilogue adds (xd*d) * (sc0*S0 + sc1*S1)
+// (dot_row_q6_k_int_neon, src/matmul_simd.cpp:285-342). The 210-byte blocks
+// are 2-byte aligned: each 8-byte piece is read as three dwords from the
+// aligned-down address and funnel-shifted.
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a - sh);
+    const uint32_t d0 = q[0], d1 = q[1];
+    const uint32_t d2 = sh ? q[2] : d1;         // a third dword only when needed (no read past the piece)
+    return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
 }
 
-hipError_t launch_gemv_i8mf(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {
+template <int TL, int NWV>
+__global__ void __launch_bounds__(64 * NWV)
+gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N) {
+    __shared__ f4v red[NWV][TL][64];
+    extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int tok = lane & 15, g = lane >> 4;
+    const int nsb = K >> 8, nb = K >> 5;
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
+        const int b = i >> 4, t = i & 15;
+        sdx[i] = t < M ? A.d[(size_t)t * nb + b] : 0.0f;
+    }
+    __syncthreads();
+    const bool tv = tok < M;
+    const int8_t* aq = A.qs + (size_t)(tv ? tok : 0) * K + 8 * g;
+    const int row0 = blockIdx.x * (16 * TL) + (lane & 15);
+    const int sb0 = wv * nsb / NWV, sb1 = (wv + 1) * nsb / NWV;
+    const uint8_t* wr[TL];
+#pragma unroll
+    for (int t = 0; t < TL; t++) {
+        int row = row0 + 16 * t;
+        row = row < N ? row : N - 1;
+        wr[t] = w + (size_t)row * rb;
+    }
+    const bool first_half = g < 2;                 // k 0..15 of the block
+    const i4v zi = {0, 0, 0, 0};
+    const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4v acc[TL];
+#pragma unroll
+    for (int t = 0; t < TL; t++) acc[t] = z4;
+    for (int s = sb0; s < sb1; s++) {
+        uint2 ql[TL][4], qh[TL][2];
+        uint32_t scw[TL][4];
+        float d[TL];
+#pragma unroll
+        for (int t = 0; t < TL; t++) {
+            const uint8_t* blk = wr[t] + 210 * (size_t)s;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ql[t][i] = ld8_a2(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 2; i++) qh[t][i] = ld8_a2(blk + 128 + 32 * i + 8 * g);
+            const uint2 s0 = ld8_a2(blk + 192), s1 = ld8_a2(blk + 200);
+            scw[t][0] = s0.x; scw[t][1] = s0.y; scw[t][2] = s1.x; scw[t][3] = s1.y;
+            d[t] = fp16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
+        }
+        long av[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) av[b] = tv ? *reinterpret_cast<const long*>(aq + 32 * (8 * s + b)) : 0L;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int h = b >> 2, g6 = b & 3;
+            const f4v xd = *reinterpret_cast<const f4v*>(sdx + (size_t)(8 * s + b) * 16 + 4 * g);
+#pragma unroll
+            for (int t = 0; t < TL; t++) {
+                const uint2 l = ql[t][2 * h + (g6 & 1)], hh = qh[t][h];
+                const int ns = 4 * (g6 >> 1), hs = 2 * g6;
+                uint32_t c0 = ((l.x >> ns) & 0x0f0f0f0fu) | (((hh.x >> hs) & 0x03030303u) << 4);
+                uint32_t c1 = ((l.y >> ns) & 0x0f0f0f0fu) | (((hh.y >> hs) & 0x03030303u) << 4);
+                // code - 32 per byte (codes 0..63: no borrow across bytes)
+                c0 = ((c0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                c1 = ((c1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                const long bw = (long)((unsigned long)c0 | ((unsigned long)c1 << 32));
+                const long b0 = first_half ? bw : 0L, b1 = first_half ? 0L : bw;
+                const i4v S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[b], b0, zi, 0, 0, 0);
+                const i4v S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[b], b1, zi, 0, 0, 0);
+                const int si = 8 * h + 2 * g6;          // scales of the block's two halves
+                const float sc0 = (float)(int8_t)(scw[t][si >> 2] >> (8 * (si & 3)));
+                const float sc1 = (float)(int8_t)(scw[t][(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float dx = d[t] * xd[r];
+                    acc[t][r] = fmaf(dx * sc0, (float)S0[r], acc[t][r]);
+                    acc[t][r] = fmaf(dx * sc1, (float)S1[r], acc[t][r]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TL; t++) red[wv][t][lane] = acc[t];
+    __syncthreads();
+    if (wv < TL) {
+        const int t = wv;
+        f4v sum = red[0][t][lane];
+#pragma unroll
+        for (int i = 1; i < NWV; i++) sum += red[i][t][lane];
+        const int row = row0 + 16 * t;
+        if (row < N) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tt = 4 * g + r;
+                if (tt < M) y[(size_t)tt * N + row] = sum[r];
+            }
+        }
+    }
+}
+
+bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w) {
+    // LDS: per block and token the scale (Q4_K also the sum), at most 64 KiB
+    if (M < kMfMinM || M > kMfMaxM || K % 256 != 0) return false;
+    if (type == T_Q4_K) return (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    if (type == T_Q6_K) return (size_t)(K / 32) * 16 * 4 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 2 == 0;
+    return false;
+}
+
+hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
+                            hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (!i8mf_supported(T_Q4_K, M, K, w)) return hipErrorInvalidValue;
-    const size_t shm = (size_t)(K / 32) * 16 * 8;
-    hipLaunchKernelGGL(gemv_q4k_i8mf, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles)), dim3(64 * kMfWaves), shm, st,
-                       w, (long)row_bytes(T_Q4_K, K), A, y, M, K, N);
+    if (!i8mf_supported(type, M, K, w)) return hipErrorInvalidValue;
+    const dim3 grid((N + 16 * kMfTiles - 1) / (16 * kMfTiles));
+    if (type == T_Q6_K) {
+        // few weight rows (e.g. a down projection, 3584 rows of K 18944): 16-row
+        // workgroups of 16 waves, so the K-slices spread over twice the CUs
+        const size_t shm = (size_t)(K / 32) * 16 * 4;
+        const long rbq = (long)row_bytes(T_Q6_K, K);
+        if ((N + 31) / 32 >= 2 * device_cu_count())
+            hipLaunchKernelGGL((gemv_q6k_i8mf<2, 8>), grid, dim3(512), shm, st, w, rbq, A, y, M, K, N);
+        else
+            hipLaunchKernelGGL((gemv_q6k_i8mf<1, 16>), dim3((N + 15) / 16), dim3(1024), shm, st, w, rbq, A, y, M, K, N);
+    } else {
+        hipLaunchKernelGGL(gemv_q4k_i8mf, grid, dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w,
+                           (long)row_bytes(T_Q4_K, K), A, y, M, K, N);
+    }
     return hipGetLastError();
 }
 

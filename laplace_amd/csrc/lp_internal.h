@@ -75,10 +75,11 @@ hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, con
 // "planes" of the activations (gemm_planes_bytes(M, K) bytes of scratch):
 // M <= 16 on the small-M MFMA kernel, larger M on the tiled GEMM.
 bool gemm_supported(uint32_t type, int M, int K);
-// Q4_K, 5 <= M <= 16, on int8 MFMA straight from the quantized blocks (no
-// planes); w 16-byte aligned.
+// Q4_K / Q6_K, 5 <= M <= 16, on int8 MFMA straight from the quantized blocks
+// (no planes).
 bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w);
-hipError_t launch_gemv_i8mf(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
+hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
+                            hipStream_t st);
 size_t gemm_planes_bytes(int M, int K);
 // planes from fp32 x (quantize + planes in one pass)
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st);

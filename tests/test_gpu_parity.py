@@ -372,11 +372,13 @@ def test_m1_gemv_shapes(orc, t, K, N):
     assert np.array_equal(y2.cpu().numpy().reshape(1, N).view(np.uint32), y.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 13, 16])
 @pytest.mark.parametrize("K,N", [(256, 7), (3584, 65), (18944, 40), (32768, 5)])
 def test_q6k_multi_row_gemv(orc, K, N, M):
-    """Q6_K GEMV for 2..8 activation rows (4 rows per weight pass; 5..8 take
-    two passes) over ragged N against the oracle, with activation outliers."""
+    """Q6_K for 2..16 activation rows over ragged N against the oracle, with
+    activation outliers: dot4 GEMV (4 rows per weight pass) up to M = 4, int8
+    MFMA from 5 (odd super-block counts give 2-byte aligned rows); K = 32768
+    stays on the GEMV passes."""
     _flush(f"q6k multi-row K={K} N={N} M={M}")
     w = synth_weights(Q6_K, K, N, seed=K + 7 * N + M)
     x = synth_x(M, K, seed=K + M, outliers=0.01)
