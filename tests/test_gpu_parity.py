@@ -377,8 +377,7 @@ def test_m1_gemv_shapes(orc, t, K, N):
 def test_q6k_multi_row_gemv(orc, K, N, M):
     """Q6_K for 2..16 activation rows over ragged N against the oracle, with
     activation outliers: dot4 GEMV (4 rows per weight pass) up to M = 4, int8
-    MFMA from 5 (odd super-block counts give 2-byte aligned rows); K = 32768
-    stays on the GEMV passes."""
+    MFMA from 5 (odd super-block counts give 2-byte aligned rows)."""
     _flush(f"q6k multi-row K={K} N={N} M={M}")
     w = synth_weights(Q6_K, K, N, seed=K + 7 * N + M)
     x = synth_x(M, K, seed=K + M, outliers=0.01)
