@@ -163,14 +163,18 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
         LP_HIP(launch_gemm(type, w, A, planes, y, M, K, N, st));
         return LP_OK;
     }
-    for (int m0 = 0; m0 < M; m0 += 8) {
-        const int mt = M - m0 < 8 ? M - m0 : 8;
+    // no GEMM kernel for the type: chunks of rows through the widest small-M
+    // path (16 rows on int8 MFMA where the type has it, else 8 on the GEMV)
+    const int chunk = i8mf_supported(type, 16, K, w) ? 16 : 8;
+    for (int m0 = 0; m0 < M; m0 += chunk) {
+        const int mt = M - m0 < chunk ? M - m0 : chunk;
         ActView sub;
         sub.qs = A.qs + (size_t)m0 * K;
         sub.d = A.d + (size_t)m0 * (K / 32);
         sub.sum = A.sum + (size_t)m0 * (K / 32);
         sub.s16 = A.s16 + (size_t)m0 * (K / 32);
-        LP_HIP(launch_gemv(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
+        if (i8mf_supported(type, mt, K, w)) LP_HIP(launch_gemv_i8mf(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
+        else LP_HIP(launch_gemv(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
     }
     return LP_OK;
 }

@@ -383,3 +383,17 @@ def test_q6k_multi_row_gemv(orc, K, N, M):
     x = synth_x(M, K, seed=K + M, outliers=0.01)
     y = gemm_dev(Q6_K, x, w, N)
     assert normwise(y, orc.gemm_int(Q6_K, x, w, N)) <= 1e-4
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q6_K], ids=["Q8_0", "Q4_0", "Q6_K"])
+@pytest.mark.parametrize("M", [21, 37, 64])
+def test_prefill_rows_other_types(orc, t, M):
+    """Prefill-sized M for the types without a GEMM kernel: chunks of rows
+    (16 on the int8 MFMA kernel for Q6_K, 8 on the GEMV otherwise, remainders
+    below 5 rows on the GEMV) against the oracle."""
+    _flush(f"prefill rows {NAMES[t]} M={M}")
+    K, N = 1024, 96
+    w = synth_weights(t, K, N, seed=500 + M + t)
+    x = synth_x(M, K, seed=501 + M, outliers=0.01)
+    y = gemm_dev(t, x, w, N)
+    assert normwise(y, orc.gemm_int(t, x, w, N)) <= TOL
