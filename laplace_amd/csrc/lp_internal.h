@@ -75,8 +75,8 @@ hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, con
 // "planes" of the activations (gemm_planes_bytes(M, K) bytes of scratch):
 // M <= 16 on the small-M MFMA kernel, larger M on the tiled GEMM.
 bool gemm_supported(uint32_t type, int M, int K);
-// Q4_K / Q6_K, 5 <= M <= 16, on int8 MFMA straight from the quantized blocks
-// (no planes).
+// Small M on int8 MFMA straight from the quantized blocks (no planes):
+// Q4_K and Q6_K for 5 <= M <= 16, Q8_0 for 9 <= M <= 16.
 bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w);
 hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
                             hipStream_t st);
