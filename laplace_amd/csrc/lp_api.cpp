@@ -327,7 +327,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
 // activation rows (T, or T*topk in the multi form), then the route table.
 static size_t moe_ws_bytes(int T, int topk, int E, int K, int multi) {
     const int P = T * topk, rows = multi ? P : T;
-    return act_bytes(rows, K) + gemm_planes_bytes(rows, K) + up256(moe_route_bytes(P, E));
+    return act_bytes(rows, K) + up256(moe_route_bytes(P, E));
 }
 
 static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K, int N) {
@@ -355,16 +355,13 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
                  float* y, int T, int topk, int E, int K, int N, void* ws, hipStream_t st) {
     const int P = T * topk, rows = multi ? P : T;
     const ActView A = ws_view(ws, rows, K);
-    void* planes = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
-    void* route = static_cast<uint8_t*>(planes) + gemm_planes_bytes(rows, K);
-    // groups of <= 16 pairs on the MFMA kernel pay off when experts are
-    // chosen by many pairs on average (prefill); decode-sized batches
-    // (a few pairs per expert) stay on the GEMV tile kernel
+    void* route = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
+    // groups of <= 16 pairs on the int8 MFMA kernel pay off when experts are
+    // chosen by many pairs on average (prefill); decode-sized batches (a few
+    // pairs per expert) stay on the GEMV kernels
     const bool mf = moe_mf_supported(type, K) && P >= 8 * E;
-    if (mf) LP_HIP(launch_planes_from_x(x, planes, rows, K, st));
-    else LP_HIP(launch_quantize(x, rows, K, A, st));
-    LP_HIP(launch_moe_grouped(type, w, A, mf ? planes : nullptr, rows, idx, P, E, multi, topk, route, y, K,
-                              N, st));
+    LP_HIP(launch_quantize(x, rows, K, A, st));
+    LP_HIP(launch_moe_grouped(type, w, A, mf, rows, idx, P, E, multi, topk, route, y, K, N, st));
     return LP_OK;
 }
 
@@ -754,10 +751,10 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
     LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
     if (fused) {
         LP_HIP(launch_moe_route(idx, P, n_exp, f.route, false, st));
-        LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, nullptr, T, P, n_exp, 0, top_k, f.route,
+        LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, false, T, P, n_exp, 0, top_k, f.route,
                                          f.gu, H, 2 * inter, st));
         LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, f.hq, st));
-        LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, nullptr, P, P, n_exp, 1, top_k, f.route, f.eo,
+        LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, false, P, P, n_exp, 1, top_k, f.route, f.eo,
                                          inter, H, st));
     } else {
         if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,

@@ -989,7 +989,7 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
 // (weight row) l%16, k = 8*(l/16) .. +8 of the sub-block; D: weight row
 // l%16, tokens 4*(l/16) .. +4. Lanes load their row's super-block header
 // and their 8-byte slice of each 32-byte code quarter directly (cached).
-// MOE: blockIdx.y is a routed group (expert, first pair, n <= 16 pairs).
+// Used for K beyond the int8 kernel's LDS limit (gemv_q4k_i8mf below).
 
 constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
@@ -1002,43 +1002,20 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 struct MfArgs {
     const uint8_t* w;
     long rb;              // bytes per weight row
-    long ebytes;          // bytes per expert (MOE)
     int N, K, M;
     Planes P;
     float* y;
-    const uint8_t* route; // MOE route table (see moe_route_kernel)
-    int max_groups, multi, topk;
 };
 
-template <bool MOE>
 __global__ void __launch_bounds__(64 * kMfWaves)
 gemv_q4k_mf(MfArgs a) {
     __shared__ f4v red[kMfWaves][kMfTiles][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int tok = lane & 15, g = lane >> 4;
-    int M = a.M;
+    const int M = a.M;
     const uint8_t* w = a.w;
-    const int* pairs = nullptr;
-    int first = 0;
-    if constexpr (MOE) {
-        if ((int)blockIdx.y >= *reinterpret_cast<const int*>(a.route)) return;
-        const int4 gd = reinterpret_cast<const int4*>(a.route + 16)[blockIdx.y];
-        pairs = reinterpret_cast<const int*>(a.route + 16 + (size_t)a.max_groups * 16);
-        first = gd.y;
-        M = gd.z;
-        w += (size_t)gd.x * a.ebytes;
-    }
-    // activation row of token t (its planes)
-    auto act_row = [&](int t) -> int {
-        if constexpr (MOE) {
-            const int p = pairs[first + t];
-            return a.multi ? p : p / a.topk;
-        } else {
-            return t;
-        }
-    };
     const bool tv = tok < M;
-    const int arow = act_row(tv ? tok : 0);
+    const int arow = tv ? tok : 0;
     const int row0 = blockIdx.x * (16 * kMfTiles) + (lane & 15);
     const int nsb = a.K >> 8, nb = a.K >> 5;
     const int sb0 = wv * nsb / kMfWaves, sb1 = (wv + 1) * nsb / kMfWaves;
@@ -1121,12 +1098,7 @@ gemv_q4k_mf(MfArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int tt = 4 * g + r;
-                if (tt < M) {
-                    int yr;
-                    if constexpr (MOE) yr = pairs[first + tt];
-                    else yr = tt;
-                    a.y[(size_t)yr * a.N + row] = sum[r] * a.P.escale[act_row(tt)];
-                }
+                if (tt < M) a.y[(size_t)tt * a.N + row] = sum[r] * a.P.escale[tt];
             }
         }
     }
@@ -1149,22 +1121,46 @@ gemv_q4k_mf(MfArgs a) {
 // 4*(lane/16)+r, column = lane%16.
 typedef int i4v __attribute__((ext_vector_type(4)));
 
+// MOE: blockIdx.y is a routed group (expert, first pair, n <= 16 pairs): the
+// group's activation rows (token, or pair in the multi form) and outputs
+// (pair rows) replace rows 0..M-1.
+template <bool MOE>
 __global__ void __launch_bounds__(64 * kMfWaves)
-gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N) {
+gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N,
+              const uint8_t* __restrict__ route, int max_groups, int multi, int topk, long ebytes) {
     __shared__ f4v red[kMfWaves][kMfTiles][64];
     extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd, then [nb][16] xs
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int tok = lane & 15, g = lane >> 4;
     const int nsb = K >> 8, nb = K >> 5;
+    const int* pairs = nullptr;
+    int first = 0;
+    if constexpr (MOE) {
+        if ((int)blockIdx.y >= *reinterpret_cast<const int*>(route)) return;
+        const int4 gd = reinterpret_cast<const int4*>(route + 16)[blockIdx.y];
+        pairs = reinterpret_cast<const int*>(route + 16 + (size_t)max_groups * 16);
+        first = gd.y;
+        M = gd.z;
+        w += (size_t)gd.x * ebytes;
+    }
+    auto act_row = [&](int t) -> int {
+        if constexpr (MOE) {
+            const int p = pairs[first + t];
+            return multi ? p : p / topk;
+        } else {
+            return t;
+        }
+    };
     float* sxs = sdx + (size_t)nb * 16;
     for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
         const int b = i >> 4, t = i & 15;
-        sdx[i] = t < M ? A.d[(size_t)t * nb + b] : 0.0f;
-        sxs[i] = t < M ? A.sum[(size_t)t * nb + b] : 0.0f;
+        const size_t r = t < M ? (size_t)act_row(t) : 0;
+        sdx[i] = t < M ? A.d[r * nb + b] : 0.0f;
+        sxs[i] = t < M ? A.sum[r * nb + b] : 0.0f;
     }
     __syncthreads();
     const bool tv = tok < M;
-    const int8_t* aq = A.qs + (size_t)(tv ? tok : 0) * K + 8 * g;
+    const int8_t* aq = A.qs + (size_t)act_row(tv ? tok : 0) * K + 8 * g;
     const int row0 = blockIdx.x * (16 * kMfTiles) + (lane & 15);
     const int sb0 = wv * nsb / kMfWaves, sb1 = (wv + 1) * nsb / kMfWaves;
     const uint8_t* wr[kMfTiles];
@@ -1238,7 +1234,12 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int tt = 4 * g + r;
-                if (tt < M) y[(size_t)tt * N + row] = sum[r];
+                if (tt < M) {
+                    int yr;
+                    if constexpr (MOE) yr = pairs[first + tt];
+                    else yr = tt;
+                    y[(size_t)yr * N + row] = sum[r];
+                }
             }
         }
     }
@@ -1471,8 +1472,8 @@ hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, f
         else
             hipLaunchKernelGGL((gemv_q6k_i8mf<1, 16>), dim3((N + 15) / 16), dim3(1024), shm, st, w, rbq, A, y, M, K, N);
     } else {
-        hipLaunchKernelGGL(gemv_q4k_i8mf, grid, dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w,
-                           (long)row_bytes(T_Q4_K, K), A, y, M, K, N);
+        hipLaunchKernelGGL(gemv_q4k_i8mf<false>, grid, dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w,
+                           (long)row_bytes(T_Q4_K, K), A, y, M, K, N, nullptr, 0, 0, 1, 0L);
     }
     return hipGetLastError();
 }
@@ -1526,8 +1527,8 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
     if (M <= 0 || N <= 0) return hipSuccess;
     const Planes P = carve_planes(planes, M, K);
     if (M <= kMfMaxM) {
-        MfArgs a{w, (long)row_bytes(type, K), 0, N, K, M, P, y, nullptr, 0, 0, 1};
-        hipLaunchKernelGGL(gemv_q4k_mf<false>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles)), dim3(64 * kMfWaves),
+        MfArgs a{w, (long)row_bytes(type, K), N, K, M, P, y};
+        hipLaunchKernelGGL(gemv_q4k_mf, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles)), dim3(64 * kMfWaves),
                            0, st, a);
         return hipGetLastError();
     }
@@ -1561,15 +1562,17 @@ hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* 
     return launch_gemm_planes(type, w, planes, y, M, K, N, st);
 }
 
-bool moe_mf_supported(uint32_t type, int K) { return type == T_Q4_K && K % 256 == 0; }
+bool moe_mf_supported(uint32_t type, int K) {
+    return type == T_Q4_K && K % 256 == 0 && (size_t)(K / 32) * 16 * 8 <= 64 * 1024;
+}
 
-hipError_t launch_moe_mf(const uint8_t* w, const void* planes, int rows, const void* route, int max_groups,
-                         int multi, int topk, float* y, int K, int N, hipStream_t st) {
-    const Planes P = carve_planes(const_cast<void*>(planes), rows, K);
+hipError_t launch_moe_i8mf(const uint8_t* w, const ActView& A, const void* route, int max_groups, int multi,
+                           int topk, float* y, int K, int N, hipStream_t st) {
+    if ((size_t)(K / 32) * 16 * 8 > 64 * 1024) return hipErrorInvalidValue;
     const long rb = (long)row_bytes(T_Q4_K, K);
-    MfArgs a{w, rb, rb * N, N, K, 0, P, y, static_cast<const uint8_t*>(route), max_groups, multi, topk};
-    hipLaunchKernelGGL(gemv_q4k_mf<true>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles), max_groups),
-                       dim3(64 * kMfWaves), 0, st, a);
+    hipLaunchKernelGGL(gemv_q4k_i8mf<true>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles), max_groups),
+                       dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w, rb, A, y, 0, K, N,
+                       static_cast<const uint8_t*>(route), max_groups, multi, topk, rb * N);
     return hipGetLastError();
 }
 

@@ -1459,25 +1459,24 @@ hipError_t launch_moe_route(const int* idx, int P, int E, void* route, bool mf_g
     return hipGetLastError();
 }
 
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
                               int rows, const int* idx, int P, int E, int multi, int topk, void* route,
                               float* y, int K, int N, hipStream_t st) {
     if (P <= 0 || N <= 0) return hipSuccess;
     if (E <= 0 || E > kMoeMaxExperts || topk <= 0) return hipErrorInvalidValue;
-    const bool mf = planes != nullptr && moe_mf_supported(type, K);
+    const bool mf = mf_groups && moe_mf_supported(type, K);
     hipError_t e = launch_moe_route(idx, P, E, route, mf, st);
     if (e != hipSuccess) return e;
-    return launch_moe_grouped_routed(type, w, A, mf ? planes : nullptr, rows, P, E, multi, topk, route, y, K, N,
-                                     st);
+    return launch_moe_grouped_routed(type, w, A, mf, rows, P, E, multi, topk, route, y, K, N, st);
 }
 
-hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
                                      int K, int N, hipStream_t st) {
     if (P <= 0 || N <= 0) return hipSuccess;
-    const bool mf = planes != nullptr && moe_mf_supported(type, K);
+    const bool mf = mf_groups && moe_mf_supported(type, K);
     const int mg = moe_max_groups(P, E);
-    if (mf) return launch_moe_mf(w, planes, rows, route, mg, multi, topk, y, K, N, st);
+    if (mf) return launch_moe_i8mf(w, A, route, mg, multi, topk, y, K, N, st);
     if (type == T_Q4_K && sbm_supported(K, w)) {
         SbmArgs args{w, (long)row_bytes(type, K) * N, A, y, K, N, 0, static_cast<const uint8_t*>(route), mg, multi,
                      topk};

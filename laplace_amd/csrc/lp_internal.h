@@ -88,27 +88,27 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
 // planes from quantized activations A, then the product
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
                        int M, int K, int N, hipStream_t st);
-// grouped MoE on the small-M MFMA kernel (groups of <= 16 pairs), planes of
-// `rows` activation rows; route from launch_moe_route with group size 16.
+// grouped MoE on the int8 small-M MFMA kernel (groups of <= 16 pairs) from
+// the quantized activation rows A; route from launch_moe_route with group
+// size 16.
 bool moe_mf_supported(uint32_t type, int K);
-hipError_t launch_moe_mf(const uint8_t* w, const void* planes, int rows, const void* route, int max_groups,
-                         int multi, int topk, float* y, int K, int N, hipStream_t st);
+hipError_t launch_moe_i8mf(const uint8_t* w, const ActView& A, const void* route, int max_groups, int multi,
+                           int topk, float* y, int K, int N, hipStream_t st);
 // Grouped MoE dispatch (lp_gemv.hip). P = T * topk pairs, E experts stacked
 // in w (E x N rows). `route` is scratch of moe_route_bytes(P, E) bytes.
-// planes != nullptr (planes of `rows` activation rows): Q4_K runs on the
-// small-M MFMA kernel in groups of <= 16 pairs; otherwise the GEMV tile
-// kernel reads A in groups of <= 4.
+// mf_groups: Q4_K runs on the int8 small-M MFMA kernel in groups of <= 16
+// pairs; otherwise the GEMV kernels read A in groups of <= 4.
 constexpr int kMoeMaxExperts = 8192;
 int moe_max_groups(int P, int E);
 size_t moe_route_bytes(int P, int E);
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
                               int rows, const int* idx, int P, int E, int multi, int topk, void* route,
                               float* y, int K, int N, hipStream_t st);
 // The two halves of launch_moe_grouped: the route table of the pairs (groups
 // of <= 16 pairs for the MFMA kernel, mf_groups, else <= 4), and the grouped
 // products on a route table built for the same pairs and group size.
 hipError_t launch_moe_route(const int* idx, int P, int E, void* route, bool mf_groups, hipStream_t st);
-hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, const void* planes,
+hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
                                      int K, int N, hipStream_t st);
 // dequantize (lp_dequant.hip): elements per block (0 = type not handled)
