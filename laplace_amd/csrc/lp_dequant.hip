@@ -430,8 +430,13 @@ gemv_fact_lds(const uint8_t* __restrict__ w, size_t rb, const float* __restrict_
         for (int k = 0; k < kFactLdsPieces; k++) {
             if (k < nld) {
                 size_t o = 1024 * (size_t)k + 16 * lane;
-                o = o + 16 <= rb ? o : rb - 16;
-                *reinterpret_cast<u32x4*>(wb + o) = v[k];
+                if (o + 16 <= rb) {
+                    *reinterpret_cast<u32x4*>(wb + o) = v[k];
+                } else {
+                    o = rb - 16;                            // 4-byte aligned (rb % 4 == 0)
+                    uint32_t* d4 = reinterpret_cast<uint32_t*>(wb + o);
+                    d4[0] = v[k].x; d4[1] = v[k].y; d4[2] = v[k].z; d4[3] = v[k].w;
+                }
             }
         }
         if (row + nwaves < N) load_row(row + nwaves);
