@@ -337,16 +337,17 @@ def measure_moe_ffn(g: Gpu, T, reps=20, copies=2, seed=0):
             "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
-    """MoE layer dispatch: 128 Q4_K experts, 64
-    tokens, top-8 routing (distinct experts per token, uniform). One step =
-    grouped gate/up (N=1536, K=2048, one activation row per token) + grouped
-    down (N=2048, K=768, one activation row per pair), each with its
-    quantization and routing. Layer copies rotate so every step streams its
-    experts from HBM. value = (unique-expert weight bytes + x + y bytes) /
-    step time."""
+def measure_moe(g: Gpu, T=64, reps=20, copies=2, seed=0):
+    """MoE layer dispatch: 128 Q4_K experts, T
+    tokens (64 in the config), top-8 routing (distinct experts per token,
+    uniform). One step = grouped gate/up (N=1536, K=2048, one activation row
+    per token) + grouped down (N=2048, K=768, one activation row per pair),
+    each with its quantization and routing. Layer copies rotate so every step
+    streams its experts from HBM. value = (unique-expert weight bytes + x + y
+    bytes) / step time. At T >= 128 (>= 8 pairs per expert) the groups run on
+    the int8 MFMA kernel."""
     torch = g.torch
-    t, E, T, topk = Q4_K, 128, 64, 8
+    t, E, topk = Q4_K, 128, 8
     P = T * topk
     Ngu, Kgu, Nd, Kd = 1536, 2048, 2048, 768
     rng = np.random.default_rng(seed + 77)
@@ -405,7 +406,7 @@ def measure_moe(g: Gpu, reps=20, copies=2, seed=0):
     wbytes = uniq * (row_bytes(t, Kgu) * Ngu + row_bytes(t, Kd) * Nd)
     alg = wbytes + 4 * (T * Kgu + P * Kd) + 4 * P * (Ngu + Nd)
     per_pair = P * (row_bytes(t, Kgu) * Ngu + row_bytes(t, Kd) * Nd)
-    return {"workload": "Q4_K MoE layer: 128 experts, 64 tokens, top-8; gate_up 1536x2048 + "
+    return {"workload": f"Q4_K MoE layer: 128 experts, {T} tokens, top-8; gate_up 1536x2048 + "
                         "down 2048x768 (grouped by expert)",
             "unique_experts": uniq, "alg_bytes": int(alg), "us_step": round(us, 2),
             "gbs": round(alg / (us * 1e-6) / 1e9, 1),
@@ -663,6 +664,9 @@ def main():
     if not args.no_moe:
         out["moe"] = measure_moe(g)
         g.torch.cuda.empty_cache()
+        if not args.no_extra:
+            out["moe_prefill"] = measure_moe(g, T=256)
+            g.torch.cuda.empty_cache()
         out["moe_ffn"] = [measure_moe_ffn(g, T) for T in (1, 64)]
     if not args.no_extra:
         g.torch.cuda.empty_cache()
