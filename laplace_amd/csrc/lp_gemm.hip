@@ -1535,11 +1535,13 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
     const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
     const long cus = device_cu_count();
     GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K, 1};
-    if ((long)ntn * ntm < cus) {
-        // fewer 128-token tiles than CUs: 64-token tiles (two workgroups per CU),
-        // and when even those leave CUs idle, K split over two workgroups that
-        // add into a zeroed y (two fp32 additions onto 0 give the same sum in
-        // either order). Measured: Q4_K 4096 x 4096, M 512: 130 -> 80 us.
+    if ((long)ntn * ntm < cus || N >= 8192) {
+        // fewer 128-token tiles than CUs, or wide weights: 64-token tiles (two
+        // workgroups per CU), and when even those leave CUs idle, K split over
+        // two workgroups that add into a zeroed y (two fp32 additions onto 0
+        // give the same sum in either order). Measured: Q4_K 4096 x 4096, M 512:
+        // 130 -> 80 us; 14336 x 4096, M 2048: 615 -> 598 us (4096 x 4096, M 2048:
+        // no difference).
         const long t64 = (long)ntn * ((M + 63) / 64);
         g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
         if (g.ksplit == 2) {
