@@ -500,6 +500,7 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
                 if (s < 3) wait_afrag<4>(o);
                 else wait_afrag<0>(o);
                 __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(1);          // the MFMA burst issues ahead of the other waves
                 const h8 (&vs)[CT] = v[s & 1];
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++)
@@ -526,6 +527,7 @@ gemm_q4k_kernel(GemmArgs g, int ntn) {
                     __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(0);
                 // the next-but-one activation fragments go into this sub-step's buffer
                 if (s == 0) read_afrag<2>(af[0], st_off, a_base, a_x);
                 if (s == 1) read_afrag<3>(af[1], st_off, a_base, a_x);
@@ -780,6 +782,7 @@ gemm_q4k_m64(GemmArgs g, int ntn) {
                 if (s < 3) wait_afrag<4>(o);
                 else wait_afrag<0>(o);
                 __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(1);          // the MFMA burst issues ahead of the other waves
                 const h8 (&vs)[CT] = v[s & 1];
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++)
@@ -806,6 +809,7 @@ gemm_q4k_m64(GemmArgs g, int ntn) {
                     __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(0);
                 // the next-but-one activation fragments go into this sub-step's buffer
                 if (s == 0) read_afrag<2, A_PLANE64>(af[0], st_off, a_base, a_x);
                 if (s == 1) read_afrag<3, A_PLANE64>(af[1], st_off, a_base, a_x);
