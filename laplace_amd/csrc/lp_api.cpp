@@ -357,9 +357,10 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
     const ActView A = ws_view(ws, rows, K);
     void* route = static_cast<uint8_t*>(ws) + act_bytes(rows, K);
     // groups of <= 16 pairs on the int8 MFMA kernel pay off when experts are
-    // chosen by many pairs on average (prefill); decode-sized batches (a few
-    // pairs per expert) stay on the GEMV kernels
-    const bool mf = moe_mf_supported(type, K) && P >= 8 * E;
+    // chosen by more than 8 pairs on average (prefill; at 128 experts, top-8:
+    // 10 per expert 259 vs 274 us on the GEMV kernels, 8 per expert 246 vs
+    // 236 us); decode-sized batches stay on the GEMV kernels
+    const bool mf = moe_mf_supported(type, K) && P > 8 * E;
     LP_HIP(launch_quantize(x, rows, K, A, st));
     LP_HIP(launch_moe_grouped(type, w, A, mf, rows, idx, P, E, multi, topk, route, y, K, N, st));
     return LP_OK;
@@ -740,8 +741,8 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
     // Decode-sized batches (neither expert pass on the MFMA kernel): the norm
     // and GeGLU kernels also write the int8 blocks the expert GEMVs read, and
     // one route table serves both passes.
-    const bool fused = !(moe_mf_supported(gate_up_type, H) && P >= 8 * n_exp) &&
-                       !(moe_mf_supported(down_type, inter) && P >= 8 * n_exp) && H % 32 == 0 &&
+    const bool fused = !(moe_mf_supported(gate_up_type, H) && P > 8 * n_exp) &&
+                       !(moe_mf_supported(down_type, inter) && P > 8 * n_exp) && H % 32 == 0 &&
                        inter % 32 == 0 && reinterpret_cast<uintptr_t>(router_scale) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(pre_norm) % 16 == 0;
     LP_HIP(launch_moe_norms(x, T, H, router_scale, pre_norm, rms_eps, f.rin, f.ein, fused ? f.eq : ActView{},

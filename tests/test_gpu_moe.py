@@ -154,7 +154,7 @@ def test_moe_empty():
 
 @pytest.mark.parametrize("multi", [False, True])
 def test_moe_many_pairs_per_expert_mfma(orc, multi):
-    """When experts average >= 8 pairs (prefill-sized batches), Q4_K groups of
+    """When experts average more than 8 pairs (prefill-sized batches), Q4_K groups of
     up to 16 pairs run on the small-M MFMA kernel: 8 experts, 96 tokens,
     top-2, ragged groups, against the oracle."""
     t, E, T, topk, K, N = Q4_K, 8, 96, 2, 1024, 80

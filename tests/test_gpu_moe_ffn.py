@@ -40,8 +40,9 @@ def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed):
     # Gemma4 26B layer shape (tests/bench_cpu_gpu.cpp:55-57): H 2816, 128
     # experts, top-8, expert inter 704 (down K = 704: a Q8_0 tensor)
     (2, 2816, 128, 8, 704, Q4_K, Q8_0, F32),
-    # 128 pairs over 16 experts: both expert passes on the MFMA group kernel
-    (64, 512, 16, 2, 256, Q4_K, Q4_K, F32),
+    # 144 pairs over 16 experts (9 per expert): both expert passes on the MFMA
+    # group kernel
+    (72, 512, 16, 2, 256, Q4_K, Q4_K, F32),
 ], ids=lambda v: str(v))
 def test_moe_ffn_matches_oracle(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t):
     (out, idx, wts), (ref, ridx, rw) = run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t,
