@@ -153,13 +153,25 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
     return LP_OK;
 }
 
+// Whether M > 16 rows run on the tiled GEMM. Q4_K at small prefill sizes
+// runs faster as 16-row chunks on the int8 MFMA kernel (one weight pass per
+// chunk) than on the GEMM's 64-token tiles (measured per call at
+// N x K = 14336 x 4096 / 4096 x 14336: M=17 32 vs 49 and 52 vs 136 us;
+// M=32 49 vs 54 and 82 vs 142; M=48 71 vs 59 and 122 vs 149; M=64 94 vs
+// 64 and 161 vs 155).
+static bool use_gemm(uint32_t type, int M, int K, int N, const uint8_t* w) {
+    if (!gemm_supported(type, M, K) || i8mf_supported(type, M, K, w)) return false;
+    if (type == T_Q4_K && i8mf_supported(type, 16, K, w) && (M <= 32 || (M <= 48 && N <= 4096))) return false;
+    return true;
+}
+
 static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t type, float* y,
                   int M, int K, int N, hipStream_t st) {
     if (i8mf_supported(type, M, K, w)) {
         LP_HIP(launch_gemv_i8mf(type, w, A, y, M, K, N, st));
         return LP_OK;
     }
-    if (planes && gemm_supported(type, M, K)) {
+    if (planes && use_gemm(type, M, K, N, w)) {
         LP_HIP(launch_gemm(type, w, A, planes, y, M, K, N, st));
         return LP_OK;
     }
@@ -305,7 +317,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         const ActView A = ws_view(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
-    } else if (gemm_supported(type, M, K)) {
+    } else if (use_gemm(type, M, K, N, wd)) {
         void* planes = ws_planes(c->ws, M, K);
         LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));
         LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
@@ -595,7 +607,7 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
         LP_HIP(launch_gemv_fused(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
         return LP_OK;
     }
-    if (gemm_supported(type, M, K) && !i8mf_supported(type, M, K, w)) {
+    if (use_gemm(type, M, K, N, w)) {
         // fp16 planes straight from x (one pass), then the MFMA product
         if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
             set_err("workspace %zu < %zu bytes or null pointer", wsb, ws_bytes(M, K));

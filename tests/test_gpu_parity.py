@@ -239,7 +239,7 @@ def test_unsupported_type_is_reported():
 # prefill GEMM (Q4_K, M > 8): MFMA path against the oracle's gemm_int
 
 
-GEMM_SHAPES = [(512, 256, 9), (512, 300, 33), (512, 256, 130), (2816, 300, 65), (4096, 512, 257)]
+GEMM_SHAPES = [(512, 256, 9), (512, 300, 49), (512, 256, 130), (2816, 300, 65), (4096, 512, 257)]
 
 
 @pytest.mark.parametrize("K,N,M", GEMM_SHAPES, ids=lambda v: str(v))
@@ -276,6 +276,22 @@ def test_gemm_q4k_prefill_configs(orc, N, M):
     ref = orc.gemm_int(Q4_K, x[toks], ws, len(rows))
     err = normwise(y[np.ix_(toks, rows)], ref)
     assert err <= TOL, f"normwise {err:.3g}"
+
+
+@pytest.mark.parametrize("K,N,M", [(512, 300, 17), (1024, 256, 24), (512, 300, 33), (2816, 4096, 48)],
+                         ids=lambda v: str(v))
+def test_gemm_q4k_small_prefill_chunks(orc, K, N, M):
+    """Q4_K at 17..48 rows (the GEMM's 64-token tiles would be mostly empty)
+    runs as 16-row chunks on the int8 MFMA kernel plus a GEMV remainder:
+    against the oracle's gemm_int, rows 16 apart are independent."""
+    _flush(f"gemm chunks Q4_K K={K} N={N} M={M}")
+    w = synth_weights(Q4_K, K, N, seed=K + M)
+    x = synth_x(M, K, seed=M + 7, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    assert normwise(y, orc.gemm_int(Q4_K, x, w, N)) <= TOL
+    for m0 in range(0, M, 16):
+        part = gemm_dev(Q4_K, x[m0:m0 + 16], w, N)
+        assert np.array_equal(part.view(np.uint32), y[m0:m0 + 16].view(np.uint32))
 
 
 def test_gemm_matches_gemv_rows(orc):
