@@ -161,7 +161,7 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
 // 64 and 161 vs 155).
 static bool use_gemm(uint32_t type, int M, int K, int N, const uint8_t* w) {
     if (!gemm_supported(type, M, K) || i8mf_supported(type, M, K, w)) return false;
-    if (type == T_Q4_K && i8mf_supported(type, 16, K, w) && (M <= 32 || (M <= 48 && N <= 4096))) return false;
+    if (type == T_Q4_K && i8mf_supported(type, 16, K, w) && (M <= 32 || (M <= 64 && N <= 4096))) return false;
     return true;
 }
 

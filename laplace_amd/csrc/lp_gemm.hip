@@ -1128,11 +1128,12 @@ typedef int i4v __attribute__((ext_vector_type(4)));
 // MOE: blockIdx.y is a routed group (expert, first pair, n <= 16 pairs): the
 // group's activation rows (token, or pair in the multi form) and outputs
 // (pair rows) replace rows 0..M-1.
-template <bool MOE>
-__global__ void __launch_bounds__(64 * kMfWaves)
+// TL 16-row tiles per workgroup, NWV waves (K-slices).
+template <bool MOE, int TL = kMfTiles, int NWV = kMfWaves>
+__global__ void __launch_bounds__(64 * NWV)
 gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N,
               const uint8_t* __restrict__ route, int max_groups, int multi, int topk, long ebytes) {
-    __shared__ f4v red[kMfWaves][kMfTiles][64];
+    __shared__ f4v red[NWV][TL][64];
     extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd, then [nb][16] xs
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int tok = lane & 15, g = lane >> 4;
@@ -1165,25 +1166,25 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
     __syncthreads();
     const bool tv = tok < M;
     const int8_t* aq = A.qs + (size_t)act_row(tv ? tok : 0) * K + 8 * g;
-    const int row0 = blockIdx.x * (16 * kMfTiles) + (lane & 15);
-    const int sb0 = wv * nsb / kMfWaves, sb1 = (wv + 1) * nsb / kMfWaves;
-    const uint8_t* wr[kMfTiles];
+    const int row0 = blockIdx.x * (16 * TL) + (lane & 15);
+    const int sb0 = wv * nsb / NWV, sb1 = (wv + 1) * nsb / NWV;
+    const uint8_t* wr[TL];
 #pragma unroll
-    for (int t = 0; t < kMfTiles; t++) {
+    for (int t = 0; t < TL; t++) {
         int row = row0 + 16 * t;
         row = row < N ? row : N - 1;
         wr[t] = w + (size_t)row * rb;
     }
     const i4v zi = {0, 0, 0, 0};
     const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    f4v acc[kMfTiles];
+    f4v acc[TL];
 #pragma unroll
-    for (int t = 0; t < kMfTiles; t++) acc[t] = z4;
+    for (int t = 0; t < TL; t++) acc[t] = z4;
     for (int s = sb0; s < sb1; s++) {
-        u32x4 h[kMfTiles];
-        uint2 q[kMfTiles][4];
+        u32x4 h[TL];
+        uint2 q[TL][4];
 #pragma unroll
-        for (int t = 0; t < kMfTiles; t++) {
+        for (int t = 0; t < TL; t++) {
             const uint8_t* blk = wr[t] + 144 * s;
             h[t] = *reinterpret_cast<const u32x4*>(blk);
 #pragma unroll
@@ -1192,15 +1193,15 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
         long av[8];
 #pragma unroll
         for (int b = 0; b < 8; b++) av[b] = tv ? *reinterpret_cast<const long*>(aq + 32 * (8 * s + b)) : 0L;
-        f4v mnacc[kMfTiles];
+        f4v mnacc[TL];
 #pragma unroll
-        for (int t = 0; t < kMfTiles; t++) mnacc[t] = z4;
+        for (int t = 0; t < TL; t++) mnacc[t] = z4;
 #pragma unroll
         for (int b = 0; b < 8; b++) {
             const f4v xd = *reinterpret_cast<const f4v*>(sdx + (size_t)(8 * s + b) * 16 + 4 * g);
             const f4v xs = *reinterpret_cast<const f4v*>(sxs + (size_t)(8 * s + b) * 16 + 4 * g);
 #pragma unroll
-            for (int t = 0; t < kMfTiles; t++) {
+            for (int t = 0; t < TL; t++) {
                 uint32_t sc, mn;
                 scale_min_k4(b, h[t].y, h[t].z, h[t].w, sc, mn);
                 const uint2 u = q[t][b >> 1];
@@ -1218,21 +1219,21 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
             }
         }
 #pragma unroll
-        for (int t = 0; t < kMfTiles; t++) {
+        for (int t = 0; t < TL; t++) {
             const float dmin = fp16_bits_to_f32(h[t].x >> 16);
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[t][r] = fmaf(-dmin, mnacc[t][r], acc[t][r]);
         }
     }
 #pragma unroll
-    for (int t = 0; t < kMfTiles; t++) red[wv][t][lane] = acc[t];
+    for (int t = 0; t < TL; t++) red[wv][t][lane] = acc[t];
     __syncthreads();
     // wave t sums tile t over the K-slices in a fixed order
-    if (wv < kMfTiles) {
+    if (wv < TL) {
         const int t = wv;
         f4v sum = red[0][t][lane];
 #pragma unroll
-        for (int i = 1; i < kMfWaves; i++) sum += red[i][t][lane];
+        for (int i = 1; i < NWV; i++) sum += red[i][t][lane];
         const int row = row0 + 16 * t;
         if (row < N) {
 #pragma unroll
@@ -1476,8 +1477,17 @@ hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, f
         else
             hipLaunchKernelGGL((gemv_q6k_i8mf<1, 16>), dim3((N + 15) / 16), dim3(1024), shm, st, w, rbq, A, y, M, K, N);
     } else {
-        hipLaunchKernelGGL(gemv_q4k_i8mf<false>, grid, dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w,
-                           (long)row_bytes(T_Q4_K, K), A, y, M, K, N, nullptr, 0, 0, 1, 0L);
+        const size_t shm = (size_t)(K / 32) * 16 * 8;
+        const long rbq = (long)row_bytes(T_Q4_K, K);
+        // fewer 32-row workgroups than CUs (e.g. a down projection, 4096 rows
+        // of K 14336): 16-row workgroups of 16 waves (M=16 42.6 -> 34.1 us
+        // there; at 14336 x 4096 the 32-row form is faster, 26.3 vs 36.7)
+        if ((N + 31) / 32 < device_cu_count())
+            hipLaunchKernelGGL((gemv_q4k_i8mf<false, 1, 16>), dim3((N + 15) / 16), dim3(1024), shm, st, w, rbq, A, y,
+                               M, K, N, nullptr, 0, 0, 1, 0L);
+        else
+            hipLaunchKernelGGL(gemv_q4k_i8mf<false>, grid, dim3(64 * kMfWaves), shm, st, w, rbq, A, y, M, K, N,
+                               nullptr, 0, 0, 1, 0L);
     }
     return hipGetLastError();
 }
