@@ -160,14 +160,14 @@ static int check_shape(uint32_t type, const void* w, int M, int K, int N) {
 // M=32 49 vs 54 and 82 vs 142; M=48 71 vs 59 and 122 vs 149; M=64 94 vs
 // 64 and 161 vs 155).
 static bool use_gemm(uint32_t type, int M, int K, int N, const uint8_t* w) {
-    if (!gemm_supported(type, M, K) || i8mf_supported(type, M, K, w)) return false;
-    if (type == T_Q4_K && i8mf_supported(type, 16, K, w) && (M <= 32 || (M <= 64 && N <= 4096))) return false;
+    if (!gemm_supported(type, M, K) || i8mf_supported(type, M, K, N, w)) return false;
+    if (type == T_Q4_K && i8mf_supported(type, 16, K, N, w) && (M <= 32 || (M <= 64 && N <= 4096))) return false;
     return true;
 }
 
 static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t type, float* y,
                   int M, int K, int N, hipStream_t st) {
-    if (i8mf_supported(type, M, K, w)) {
+    if (i8mf_supported(type, M, K, N, w)) {
         LP_HIP(launch_gemv_i8mf(type, w, A, y, M, K, N, st));
         return LP_OK;
     }
@@ -177,7 +177,7 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
     }
     // no GEMM kernel for the type: chunks of rows through the widest small-M
     // path (16 rows on int8 MFMA where the type has it, else 8 on the GEMV)
-    const int chunk = i8mf_supported(type, 16, K, w) ? 16 : 8;
+    const int chunk = i8mf_supported(type, 16, K, N, w) ? 16 : 8;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mt = M - m0 < chunk ? M - m0 : chunk;
         ActView sub;
@@ -185,7 +185,7 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
         sub.d = A.d + (size_t)m0 * (K / 32);
         sub.sum = A.sum + (size_t)m0 * (K / 32);
         sub.s16 = A.s16 + (size_t)m0 * (K / 32);
-        if (i8mf_supported(type, mt, K, w)) LP_HIP(launch_gemv_i8mf(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
+        if (i8mf_supported(type, mt, K, N, w)) LP_HIP(launch_gemv_i8mf(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
         else LP_HIP(launch_gemv(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
     }
     return LP_OK;
@@ -313,7 +313,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         LP_HIP(launch_gemv_fact(type, wd, c->xd, c->yd, M, K, N, c->stream));
     } else if (gemv_fused_supported(type, M, K, wd)) {
         LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
-    } else if (i8mf_supported(type, M, K, wd)) {
+    } else if (i8mf_supported(type, M, K, N, wd)) {
         const ActView A = ws_view(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));

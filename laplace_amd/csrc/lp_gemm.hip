@@ -1440,10 +1440,17 @@ gemv_b32_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
     }
 }
 
-bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w) {
+bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
     // LDS: per block and token the scale (Q4_K also the sum), at most 64 KiB
-    if (M < kMfMinM || M > kMfMaxM || K % 256 != 0) return false;
-    if (type == T_Q4_K) return (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    if (M > kMfMaxM || K % 256 != 0) return false;
+    if (type == T_Q4_K) {
+        // M = 3, 4 where the 16-row workgroups apply (measured at 4096 x 14336:
+        // M=3 31.1 -> 23.3 us, M=4 36.6 -> 23.8; at 14336 x 4096 the GEMV
+        // stays faster, 17.4 vs 19.8)
+        const int min_m = (N + 31) / 32 < device_cu_count() ? 3 : kMfMinM;
+        return M >= min_m && (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    }
+    if (M < kMfMinM) return false;
     // Q8_0 from 9 rows (measured at 14336 x 4096: M=8 64 us vs 54 on the GEMV,
     // M=16 70 vs 104, M=64 266 vs 392); Q4_0 was no faster than the GEMV
     const bool lds_ok = (size_t)(K / 32) * 16 * 4 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 2 == 0;
@@ -1455,7 +1462,7 @@ bool i8mf_supported(uint32_t type, int M, int K, const uint8_t* w) {
 hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
                             hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (!i8mf_supported(type, M, K, w)) return hipErrorInvalidValue;
+    if (!i8mf_supported(type, M, K, N, w)) return hipErrorInvalidValue;
     const dim3 grid((N + 16 * kMfTiles - 1) / (16 * kMfTiles));
     if (type == T_Q8_0) {
         const size_t shm = (size_t)(K / 32) * 16 * 4;

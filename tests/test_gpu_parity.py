@@ -294,6 +294,20 @@ def test_gemm_q4k_small_prefill_chunks(orc, K, N, M):
         assert np.array_equal(part.view(np.uint32), y[m0:m0 + 16].view(np.uint32))
 
 
+@pytest.mark.parametrize("N", [256, 8192])
+@pytest.mark.parametrize("M", [3, 4])
+def test_q4k_three_four_rows(orc, M, N):
+    """Q4_K at M = 3, 4: the int8 MFMA kernel when its 16-row workgroups
+    apply (few rows: N = 256), the dot4 GEMV on wide shapes (N = 8192 on a
+    256-CU part); both against the oracle's gemm_int."""
+    K = 512
+    _flush(f"Q4_K M={M} N={N} K={K}")
+    w = synth_weights(Q4_K, K, N, seed=M + N)
+    x = synth_x(M, K, seed=M + 3, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    assert normwise(y, orc.gemm_int(Q4_K, x, w, N)) <= TOL
+
+
 def test_gemm_matches_gemv_rows(orc):
     """The MFMA GEMM (M = 16) and the GEMV (M = 8, twice) agree per row."""
     _flush("gemm vs gemv")
