@@ -1444,10 +1444,11 @@ bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
     // LDS: per block and token the scale (Q4_K also the sum), at most 64 KiB
     if (M > kMfMaxM || K % 256 != 0) return false;
     if (type == T_Q4_K) {
-        // M = 3, 4 where the 16-row workgroups apply (measured at 4096 x 14336:
-        // M=3 31.1 -> 23.3 us, M=4 36.6 -> 23.8; at 14336 x 4096 the GEMV
-        // stays faster, 17.4 vs 19.8)
-        const int min_m = (N + 31) / 32 < device_cu_count() ? 3 : kMfMinM;
+        // M = 3, 4 at long K where the 16-row workgroups apply (measured at
+        // 4096 x 14336: M=3 31.1 -> 23.3 us, M=4 36.6 -> 23.8); the GEMV stays
+        // faster on wide shapes (14336 x 4096: 17.4 vs 19.8) and at shorter K
+        // (4096 x 8192, M=3: 12.2 vs 15.1)
+        const int min_m = ((N + 31) / 32 < device_cu_count() && K >= 14336) ? 3 : kMfMinM;
         return M >= min_m && (size_t)(K / 32) * 16 * 8 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
     }
     if (M < kMfMinM) return false;

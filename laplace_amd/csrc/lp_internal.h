@@ -76,7 +76,7 @@ hipError_t launch_gemv_fused_batch(const uint8_t* const* w, float* const* y, con
 // M <= 16 on the small-M MFMA kernel, larger M on the tiled GEMM.
 bool gemm_supported(uint32_t type, int M, int K);
 // Small M on int8 MFMA straight from the quantized blocks (no planes):
-// Q4_K and Q6_K for 5 <= M <= 16 (Q4_K from M = 3 when N < 32 x CUs),
+// Q4_K and Q6_K for 5 <= M <= 16 (Q4_K from M = 3 when N < 32 x CUs and K >= 14336),
 // Q8_0 for 9 <= M <= 16.
 bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
 hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,

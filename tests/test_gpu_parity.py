@@ -294,13 +294,12 @@ def test_gemm_q4k_small_prefill_chunks(orc, K, N, M):
         assert np.array_equal(part.view(np.uint32), y[m0:m0 + 16].view(np.uint32))
 
 
-@pytest.mark.parametrize("N", [256, 8192])
+@pytest.mark.parametrize("N,K", [(256, 14336), (8192, 512), (256, 512)])
 @pytest.mark.parametrize("M", [3, 4])
-def test_q4k_three_four_rows(orc, M, N):
+def test_q4k_three_four_rows(orc, M, N, K):
     """Q4_K at M = 3, 4: the int8 MFMA kernel when its 16-row workgroups
-    apply (few rows: N = 256), the dot4 GEMV on wide shapes (N = 8192 on a
-    256-CU part); both against the oracle's gemm_int."""
-    K = 512
+    apply and K is long (N = 256, K = 14336), the dot4 GEMV otherwise (a wide
+    shape on a 256-CU part, short K); all against the oracle's gemm_int."""
     _flush(f"Q4_K M={M} N={N} K={K}")
     w = synth_weights(Q4_K, K, N, seed=M + N)
     x = synth_x(M, K, seed=M + 3, outliers=0.01)
