@@ -44,6 +44,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 ROTATE_MIN_BYTES = 512 << 20
+KERNEL_MIN_LAUNCHES = 200
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
 F32, F16, Q5_0, Q2_K, Q3_K, Q5_K, BF16 = 0, 1, 6, 10, 11, 13, 30
 FACT_TYPES = (F32, F16, BF16, Q2_K, Q3_K, Q5_K)   # fp32-activation GEMV
@@ -174,12 +175,20 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
     with torch.cuda.graph(graph):
         for i in range(ncp):
             step(i)
+    # the headline window runs exactly `steps` steps: whole replays of the
+    # ncp-step graph plus one graph of the remaining steps
+    full, rest = divmod(steps, ncp)
+    grest = None
+    if rest:
+        grest = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(grest):
+            for i in range(rest):
+                step(i)
     gk = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gk):
         for i in range(ncp):
             gemv_only(i)
 
-    reps = max(1, -(-steps // ncp))
     wreps = max(1, -(-warmup // ncp))
     for _ in range(wreps):
         graph.replay()
@@ -191,24 +200,29 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
+    for _ in range(full):
         graph.replay()
+    if grest is not None:
+        grest.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    nsteps = reps * ncp
+    nsteps = steps
     ms_step = wall * 1e3 / nsteps
 
-    # GEMV kernel alone: HIP events on the launch stream around graph replays
+    # GEMV kernel alone: HIP events on the launch stream around graph
+    # replays, at least KERNEL_MIN_LAUNCHES back-to-back launches
+    kreps = max(1, -(-max(steps, KERNEL_MIN_LAUNCHES) // ncp))
     for _ in range(wreps):
         gk.replay()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
-    for _ in range(reps):
+    for _ in range(kreps):
         gk.replay()
     ev1.record()
     torch.cuda.synchronize()
-    us_kernel = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+    us_kernel = ev0.elapsed_time(ev1) * 1e3 / (kreps * ncp)
+    kernel_launches = kreps * ncp
 
     return {
         "type": TNAME[t], "N": N, "K": K, "M": M,
@@ -216,7 +230,7 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
         "copies": ncp, "rotation_bytes": int(w.nbytes) * ncp,
         "steps": nsteps, "ms_per_step": ms_step,
         "gbs_step": alg_bytes / (ms_step * 1e-3) / 1e9,
-        "us_gemv": us_kernel,
+        "us_gemv": us_kernel, "kernel_launches": kernel_launches,
         "gbs_gemv": alg_bytes / (us_kernel * 1e-6) / 1e9,
         "w_host": w, "x_host": x, "fused": fused,
     }
@@ -538,11 +552,29 @@ def measure_host_api(g: Gpu, w, x, t, N, K, reps=200):
             "note": "host x/y over PCIe, registered device weights, synchronous (lp_gemm)"}
 
 
+def host_cores():
+    """Threads for the CPU baseline: every core this process may run on.
+    The count is the CPU affinity set, lowered to the cgroup CPU quota when
+    one is set (cpu.max), since threads past the quota only time-slice."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, p = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(p)))
+    except (OSError, ValueError):
+        pass
+    n = min(aff, quota) if quota else aff
+    note = f"affinity set {aff} cores" + (f", cgroup quota {quota} cores" if quota else ", no cgroup quota")
+    return n, note
+
+
 def cpu_baseline(t, w, x, N, K, budget_s=12.0):
     """Scalar fp32 path of the reference on the host, whole matrix."""
     from oracle import oracle as orc
     orc.build()
-    threads = min(16, os.cpu_count() or 1)
+    threads, cores_note = host_cores()
     M = x.shape[0]
     alg = w.nbytes + 4 * M * K + 4 * M * N
     res = {}
@@ -557,11 +589,44 @@ def cpu_baseline(t, w, x, N, K, budget_s=12.0):
     med, runs = res[threads]
     med1, runs1 = res[1]
     return {
-        "value": alg / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "value": alg / med / 1e9, "unit": "GB/s", "cores": threads, "cores_note": cores_note,
+        "kind": "port",
         "sample": f"{TNAME[t]} {N}x{K} M={M} whole matrix, gemm_scalar (src/matmul.cpp:320-334) "
                   f"restated in oracle/lp_oracle.c, median of {runs} runs",
         "value_1thread": alg / med1 / 1e9, "runs_1thread": runs1,
     }
+
+
+def cpu_baseline_gemm(N, K, M, budget_s=15.0):
+    """Scalar fp32 path of the reference for the prefill GEMM
+    (gemm_scalar<dot_row_q4_k>, src/matmul.cpp:137-167, :320-353, as restated
+    in oracle/liboracle.so) on the host cores: all M tokens against a sample
+    of the weight rows, sized from a short calibration run to about
+    budget_s seconds; ops = 2*M*rows*K over the timed run."""
+    from oracle import oracle as orc
+    orc.build()
+    threads, cores_note = host_cores()
+    w_all = synth_weights(Q4_K, K, N, seed=N + K)
+    x = synth_x(M, K, seed=2, outliers=0.01)
+    rb = row_bytes(Q4_K, K)
+
+    def run(n):
+        w = np.ascontiguousarray(w_all[: n * rb])
+        t0 = time.perf_counter()
+        orc.gemm_scalar(Q4_K, x, w, n, nthreads=threads)
+        return time.perf_counter() - t0
+
+    n0 = max(threads, 8)
+    t0 = run(n0)
+    n = int(min(N, max(n0, n0 * budget_s / max(t0, 1e-3))))
+    n = max(threads, n - n % threads)
+    dt = run(n)
+    ops = 2.0 * M * n * K
+    return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": threads,
+            "cores_note": cores_note, "kind": "port",
+            "sample": f"Q4_K gemm_scalar (src/matmul.cpp:320-353) restated in oracle/lp_oracle.c: "
+                      f"all {M} tokens x K {K} against the first {n} of {N} weight rows, one run "
+                      f"of {dt:.1f} s"}
 
 
 def load_traffic(name):
@@ -623,6 +688,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(name),
+                     "kernel_launches_timed": r["kernel_launches"],
                      "kernel": "gemv_q4k_sb (quantize fused, one launch per step)" if r["fused"]
                      else "gemv_kernel<Q4_K,M=1>", "us_per_launch": round(r["us_gemv"], 3)},
     }
@@ -661,6 +727,8 @@ def main():
                                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                                     "frac": head["frac_int8_peak"], "traffic": None},
                        "all": gemms}
+        if not args.no_cpu:
+            out["gemm"]["cpu_baseline"] = cpu_baseline_gemm(14336, 4096, 2048)
     if not args.no_moe:
         out["moe"] = measure_moe(g)
         g.torch.cuda.empty_cache()

@@ -3,9 +3,14 @@
  *
  * The functions below are what the Laplace C++ engine binds to replace its
  * CPU matmul back-end. Plain pointers and sizes only; no HIP or torch types.
- * `type` is a GGMLType value (reference src/tensor.h:11-34): Q4_0 = 2,
- * Q8_0 = 8, Q4_K = 12, Q6_K = 14 are handled; every other type makes the
- * call return "not handled" so the caller falls back to its CPU path.
+ * `type` is a GGMLType value (reference src/tensor.h:11-34). The matmul
+ * entries (lp_gemm, lp_gemm_dev, lp_gemm_batch) handle F32 = 0, F16 = 1,
+ * Q4_0 = 2, Q5_0 = 6, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13,
+ * Q6_K = 14 and BF16 = 30; lp_gemm_q_dev takes the int8-activation types
+ * (Q4_0, Q5_0, Q8_0, Q4_K, Q6_K) and the grouped-MoE entries Q4_0, Q8_0,
+ * Q4_K and Q6_K. Any other type
+ * makes the call return "not handled" so the caller falls back to its CPU
+ * path.
  *
  * Two families:
  *   1. Host-pointer, synchronous entry points with the exact signatures of
@@ -79,6 +84,11 @@ lp_moe_gemv_fn lp_get_moe_gemv_multi(void);
 int lp_register_weights(const void* base, size_t size);
 /* Drops every registered region and cached weight copy of the current device. */
 void lp_release_weights(void);
+/* Drops the one region registered at `base` (other regions and cached copies
+ * stay). LP_EINVAL if no region starts there. No reference counterpart: the
+ * reference never unregisters; this is for a file that is closed while
+ * others stay open. */
+int lp_release_region(const void* base);
 
 /* Host-pointer quantizer, the ActQ8 fields as separate arrays (test hook):
  * d, sum, sum_lo, sum_hi hold M*K/32 values, qs M*K codes. K % 32 == 0. */

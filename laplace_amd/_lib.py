@@ -32,6 +32,7 @@ SIGNATURES = {
     "lp_get_moe_gemv_multi": (_vp, []),
     "lp_register_weights": (_i, [_vp, _sz]),
     "lp_release_weights": (None, []),
+    "lp_release_region": (_i, [_vp]),
     "lp_quantize_act": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "lp_act_workspace_bytes": (_sz, [_i, _i]),
     "lp_quantize_act_dev": (_i, [_vp, _i, _i, _vp, _sz, _vp]),

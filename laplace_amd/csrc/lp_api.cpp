@@ -197,7 +197,8 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
 struct Region {
     const uint8_t* host;
     size_t size;
-    uint8_t* dev;
+    uint8_t* dev;   // device address of host[0]
+    void* alloc;    // what hipMalloc returned (dev minus the alignment offset)
 };
 
 struct HostCtx {
@@ -265,7 +266,7 @@ static int resolve_weights(HostCtx& c, const uint8_t* w, size_t len, const uint8
         return LP_OK;
     }
     if (it != c.copies.end()) {
-        (void)hipFree(it->second.dev);
+        (void)hipFree(it->second.alloc);
         c.copies.erase(it);
     }
     uint8_t* d = nullptr;
@@ -275,7 +276,7 @@ static int resolve_weights(HostCtx& c, const uint8_t* w, size_t len, const uint8
         set_err("weight upload failed");
         return LP_EHIP;
     }
-    c.copies[w] = Region{w, len, d};
+    c.copies[w] = Region{w, len, d, d};
     *out = d;
     return LP_OK;
 }
@@ -486,15 +487,35 @@ int lp_register_weights(const void* base, size_t size) {
     std::lock_guard<std::mutex> lk(g_host_mtx);
     HostCtx* c = host_ctx();
     if (!c) return LP_ENODEV;
+    // The copy starts at the same offset modulo 256 as the host region, so
+    // a host weight pointer and the device address it resolves to have the
+    // same alignment (the kernels' 16-byte loads rely on it).
+    const size_t off = reinterpret_cast<uintptr_t>(base) & 255;
     uint8_t* d = nullptr;
-    LP_HIP(hipMalloc(reinterpret_cast<void**>(&d), size));
-    if (hipMemcpy(d, base, size, hipMemcpyHostToDevice) != hipSuccess) {
+    LP_HIP(hipMalloc(reinterpret_cast<void**>(&d), size + off));
+    if (hipMemcpy(d + off, base, size, hipMemcpyHostToDevice) != hipSuccess) {
         (void)hipFree(d);
         set_err("weight upload failed");
         return LP_EHIP;
     }
-    c->regions.push_back(Region{static_cast<const uint8_t*>(base), size, d});
+    c->regions.push_back(Region{static_cast<const uint8_t*>(base), size, d + off, d});
     return LP_OK;
+}
+
+int lp_release_region(const void* base) {
+    std::lock_guard<std::mutex> lk(g_host_mtx);
+    HostCtx* c = host_ctx();
+    if (!c) return LP_ENODEV;
+    for (size_t i = 0; i < c->regions.size(); i++) {
+        if (c->regions[i].host == base) {
+            (void)hipStreamSynchronize(c->stream);
+            (void)hipFree(c->regions[i].alloc);
+            c->regions.erase(c->regions.begin() + i);
+            return LP_OK;
+        }
+    }
+    set_err("no registered region starts at %p", base);
+    return LP_EINVAL;
 }
 
 void lp_release_weights(void) {
@@ -502,8 +523,8 @@ void lp_release_weights(void) {
     HostCtx* c = host_ctx();
     if (!c) return;
     (void)hipStreamSynchronize(c->stream);
-    for (Region& r : c->regions) (void)hipFree(r.dev);
-    for (auto& kv : c->copies) (void)hipFree(kv.second.dev);
+    for (Region& r : c->regions) (void)hipFree(r.alloc);
+    for (auto& kv : c->copies) (void)hipFree(kv.second.alloc);
     c->regions.clear();
     c->copies.clear();
 }
@@ -889,10 +910,31 @@ static int host_gemm_batch(const lp_batch_spec* specs, int n) {
     if ((rc = grow_pinned(c->x_pin, c->x_pin_cap, 4 * xt)) != LP_OK) return rc;
     if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, 4 * yt)) != LP_OK) return rc;
     std::vector<lp_batch_spec> ds(specs, specs + n);
+    // Each distinct weight pointer is resolved once, for the longest span any
+    // spec reads from it: resolving a later, longer span would replace the
+    // cached copy an earlier spec already points to.
+    std::vector<size_t> span(n);
     for (int i = 0; i < n; i++) {
         const lp_batch_spec& s = specs[i];
         const size_t rbytes = fact_type(s.type) ? fact_row_bytes(s.type, s.K) : row_bytes(s.type, s.K);
-        if (s.N > 0 && (rc = resolve_weights(*c, s.w, rbytes * (size_t)s.N, &ds[i].w)) != LP_OK) return rc;
+        span[i] = s.N > 0 ? rbytes * (size_t)s.N : 0;
+    }
+    for (int i = 0; i < n; i++) {
+        if (span[i] == 0) continue;
+        int first = i;
+        for (int k = 0; k < i; k++)
+            if (span[k] && specs[k].w == specs[i].w) { first = k; break; }
+        if (first != i) continue;
+        size_t len = span[i];
+        for (int k = i + 1; k < n; k++)
+            if (specs[k].w == specs[i].w && span[k] > len) len = span[k];
+        const uint8_t* d = nullptr;
+        if ((rc = resolve_weights(*c, specs[i].w, len, &d)) != LP_OK) return rc;
+        for (int k = i; k < n; k++)
+            if (span[k] && specs[k].w == specs[i].w) ds[k].w = d;
+    }
+    for (int i = 0; i < n; i++) {
+        const lp_batch_spec& s = specs[i];
         std::memcpy(c->x_pin + xo[i], s.x, sizeof(float) * (size_t)s.K);
         ds[i].x = c->xd + xo[i];
         ds[i].y = c->yd + yo[i];

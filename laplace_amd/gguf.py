@@ -167,11 +167,12 @@ class GGUFFile:
         region = self._buf[self.data_offset:]
         if region.size:
             check(lib().lp_register_weights(region.ctypes.data, region.nbytes), "lp_register_weights")
-            self._registered = True
+            self._registered = region.ctypes.data
 
     def close(self) -> None:
         if getattr(self, "_registered", False):
-            lib().lp_release_weights()
+            # only this file's region: other registered files stay resident
+            lib().lp_release_region(self._registered)
             self._registered = False
         self.tensors = {}
         self._buf = None

@@ -126,3 +126,41 @@ def test_batch_rejects_bad_spec():
     arr = (BatchSpec * 1)(BatchSpec(x.ctypes.data, w.ctypes.data, 3, x.ctypes.data, 256, 16))
     assert not L().lp_gemm_batch(arr, 1)
     assert L().lp_gemm_batch_dev(arr, 1, None, 0, None) == _lib.LP_UNSUPPORTED
+
+
+def test_host_batch_shared_weight_different_n(orc):
+    """Two specs read the same host weight pointer over different lengths
+    (the second spec's N is larger). The batch resolves the pointer once for
+    the longer span, so the first spec does not read a freed device copy."""
+    K, Nbig, Nsmall = 1024, 384, 128
+    w = synth_weights(Q4_K, K, Nbig, seed=71)
+    x = synth_x(1, K, 72)[0]
+    L().lp_release_weights()
+    specs = [(x, w, Q4_K, Nsmall), (x, w, Q4_K, Nbig)]
+    outs = _run_host(specs)
+    L().lp_release_weights()
+    ref = orc.gemm_int(Q4_K, x[None], w, Nbig)[0]
+    assert normwise(outs[1], ref) <= TOL
+    assert normwise(outs[0], ref[:Nsmall]) <= TOL
+    assert np.array_equal(outs[0].view(np.uint32), outs[1][:Nsmall].view(np.uint32))
+
+
+def test_registered_region_unaligned_base(orc):
+    """A region registered at a base that is not 256-byte aligned: its
+    device copy keeps the host alignment modulo 256, so a 16-byte-aligned
+    Q4_K tensor inside it runs on the aligned kernels and matches the
+    oracle; lp_release_region drops only that region."""
+    K, N = 1024, 256
+    w = synth_weights(Q4_K, K, N, seed=73)
+    x = synth_x(1, K, 74)
+    buf = np.zeros(w.nbytes + 512, np.uint8)
+    base = buf[48:]                      # base % 256 != 0 in general
+    pad = (-(base.ctypes.data + 16)) % 16
+    tensor = base[16 + pad:16 + pad + w.nbytes]
+    tensor[:] = w
+    _lib.check(L().lp_register_weights(base.ctypes.data, base.nbytes), "lp_register_weights")
+    y = np.zeros(N, np.float32)
+    assert L().lp_gemm(x.ctypes.data, tensor.ctypes.data, Q4_K, y.ctypes.data, 1, K, N), L().lp_last_error()
+    assert normwise(y, orc.gemm_int(Q4_K, x, w, N)[0]) <= TOL
+    assert L().lp_release_region(base.ctypes.data) == 0
+    assert L().lp_release_region(base.ctypes.data) != 0   # already dropped

@@ -293,8 +293,10 @@ def test_moe_equals_per_expert_gemm(orc, multi):
 @pytest.mark.parametrize("t", [Q5_0, Q2_K, Q3_K, Q5_K, F16, BF16, F32])
 def test_scalar_dot_matches_own_dequantize(orc, t):
     """Types outside quant_ref.h: the scalar dot and dequantize of the same
-    blocks agree (layout of these types is not pinned by a reference
-    fixture; the GPU path does not cover them yet)."""
+    blocks agree. This is a consistency check only; the field layouts are
+    pinned by the closed-form probes in test_oracle_probes.py, and the GPU
+    kernels for these types are checked against the oracle in
+    test_gpu_fact.py."""
     K, N = 512, 16
     rng = np.random.default_rng(200 + t)
     nbytes = orc.row_bytes(t, K) * N
