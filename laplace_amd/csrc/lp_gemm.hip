@@ -8,31 +8,21 @@
 // blocks (src/matmul_simd.cpp:348-410).
 //
 // Why not int8 MFMA: the activation scale xd_mb changes every 32 elements,
-// so an int8 MFMA per 32-K block must be followed by >= 3 VALU operations
-// per output (int->float, scale, accumulate). At M=2048, N=14336, K=4096
-// that is 3.8e9 element-blocks per op, ~96 us of VALU per op on 256 CUs,
-// which caps the int8 route far below the MFMA rate. Instead the block
-// scale is folded into the operands, exactly:
-//   A[m,k] = xd_mb * q_mk  (fp32 product) split as hi = fp16(A), lo = fp16(A - hi)
-//   V[n,k] = sc_nb * nib_nk   (an integer <= 945: exact in fp16)
-// so sum_k A*V over a super-block is two fp16 MFMA streams (hi, lo) with
-// fp32 accumulation, and the only per-output epilogue is per super-block
-// (x d_n). The min term sum_b mn_nb*xs_mb is a second, K = 8 per
-// super-block, fp16 MFMA (xs split hi/lo; the 6-bit mn exact). Every
-// activation row is pre-scaled by an exact power of two (undone in the
-// epilogue) so its values sit well inside fp16 range. The result equals the
-// reference's within fp32 rounding (relative error ~1e-6).
+// so an int8 MFMA per 32-K block must be followed by >= 2 VALU operations
+// per output (int->float, scaled accumulate; the scale product itself is a
+// third). One VALU operation per output and block already takes as long as
+// the int8 MFMA producing it (a 32x32x32 int8 MFMA is 32 cycles, its 16
+// outputs per lane 16 wave64 VALU operations of 4 cycles), so the int8
+// route is VALU-bound at no more than half the int8 rate (a third with the
+// scale product). The block scales are
+// instead folded into the operands: A = xd*q (an fp32 product) as an fp16
+// value plus its e4m3 residual, V = sc*nibble (exact in fp16), so the
+// per-output epilogue runs once per 256-element super-block. See
+// gemm_q4k_sp below for the operands, the error bound and the tiling.
 //
-// Tiling: workgroup = 8 waves, output tile 128 tokens x 256 weight rows,
-// K step 64 (a quarter super-block). Each wave owns 64 x 64 = 2 x 2 MFMA
-// tiles of 32 x 32 (v_mfma_f32_32x32x16_f16). Per K step, the activation
-// hi/lo planes (32 KB) and the raw 4-bit codes of the weight rows (8 KB)
-// are copied into LDS with buffer_load_dwordx4 ... lds (1 KiB per wave
-// instruction, scalar per-step offsets), three stages in flight; super-block
-// headers and activation sums are staged once per super-block. The 4-bit
-// codes become fp16 V in registers (v_bfi_b32 into the fp16 1024 + n pattern,
-// then one packed-fp16 FMA per pair), decoded between the MFMAs of the
-// previous K=16 sub-step.
+// Small M (<= 16 rows, K beyond the int8 kernel's LDS limit) keeps the
+// two-plane fp16 form (hi = fp16(xd*q), lo = fp16(xd*q - hi)) on
+// v_mfma_f32_16x16x32_f16 (gemv_q4k_mf).
 #include <hip/hip_runtime.h>
 
 #include "lp_chunks.h"
@@ -59,6 +49,43 @@ constexpr int kPlaneChunk = 1024;   // elements per workgroup in the plane kerne
 // fl(d*q): if the compiler fuses the product into the fp16 conversion of one
 // use (v_fma_mix) but not the other, hi + lo misses v by an fp16 ulp at
 // rounding ties. Contraction is off and v passes through an empty asm.
+// Split-precision planes (SP, for the prefill GEMM) replace lo by the e4m3
+// residual of hi = fp16(t * 2^9): lo8 = e4m3(t * 2^9 - hi), stored per
+// 64-element chunk in the [g][s][e] order the GEMM's fp8 MFMA reads.
+__device__ __forceinline__ uint32_t lo8_index(int k) {
+    const int p = k & 63;
+    return (uint32_t)((k & ~63) + 32 * ((p >> 3) & 1) + 8 * (p >> 4) + (p & 7));
+}
+
+// Four values of one group (in stored order k0 k2 k1 k3): hi and lo planes.
+template <bool SP>
+__device__ __forceinline__ void store_group(float t[4], _Float16* hi, _Float16* lo, size_t rowoff, int k) {
+#pragma clang fp contract(off)
+    h4 vh, vl;
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float v = SP ? t[c] * 512.0f : t[c];
+        asm volatile("" : "+v"(v));   // hi and lo both from fl32(v): no fused fp16 product
+        const _Float16 h = (_Float16)v;
+        vh[c] = h;
+        r[c] = v - (float)h;
+        vl[c] = (_Float16)r[c];
+    }
+    *reinterpret_cast<h4*>(hi + rowoff + k) = h4{vh[0], vh[2], vh[1], vh[3]};
+    if (SP) {
+        typedef short s2 __attribute__((ext_vector_type(2)));
+        s2 w = {0, 0};
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(w, h2{vl[0], vl[2]}, 1.0f, false);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(w, h2{vl[1], vl[3]}, 1.0f, true);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(lo) + rowoff + lo8_index(k)) =
+            __builtin_bit_cast(uint32_t, w);
+    } else {
+        *reinterpret_cast<h4*>(lo + rowoff + k) = h4{vl[0], vl[2], vl[1], vl[3]};
+    }
+}
+
+template <bool SP>
 __global__ void __launch_bounds__(256)
 gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restrict__ lo,
                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
@@ -87,18 +114,10 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
     if (k < K) {
         const uint32_t qq = *reinterpret_cast<const uint32_t*>(A.qs + (size_t)m * K + k);
         const float ds = d[k >> 5] * inv;
-        h4 vh, vl;
+        float t[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float v = ds * (float)(int8_t)(qq >> (8 * c));
-            asm volatile("" : "+v"(v));   // hi and lo both from fl32(v): no fused fp16 product
-            const _Float16 h = (_Float16)v;
-            vh[c] = h;
-            vl[c] = (_Float16)(v - (float)h);
-        }
-        // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
-        *reinterpret_cast<h4*>(hi + (size_t)m * K + k) = h4{vh[0], vh[2], vh[1], vh[3]};
-        *reinterpret_cast<h4*>(lo + (size_t)m * K + k) = h4{vl[0], vl[2], vl[1], vl[3]};
+        for (int c = 0; c < 4; c++) t[c] = ds * (float)(int8_t)(qq >> (8 * c));
+        store_group<SP>(t, hi, lo, (size_t)m * K, k);
         if ((k & 31) == 0) {
             const int b = k >> 5;
             float v = s[b] * inv;
@@ -109,18 +128,6 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
         }
     }
 }
-
-// ---------------------------------------------------------------------------
-
-constexpr int BM = 128, BN = 256, BK = 64;
-constexpr int A_PLANE = BM * BK * 2;          // 16 KB per plane per stage
-constexpr int B_TILE = BN * 32;               // 8 KB of codes per stage
-constexpr int STAGE = 2 * A_PLANE + B_TILE;   // 40 KB
-constexpr int HDR = BN * 16;                  // 4 KB super-block headers
-constexpr int XS = BM * 16;                   // 2 KB per xs plane
-constexpr int SB_STAGE = HDR + 2 * XS;        // 8 KB
-constexpr int NSTAGE = 3;                     // K-step buffers in flight
-constexpr int GEMM_LDS = NSTAGE * STAGE + 2 * SB_STAGE;   // 136 KB
 
 // Buffer-resource copies straight into LDS: the per-lane byte offset is fixed
 // for the whole tile and a K step only changes the scalar offset, so the copy
@@ -135,122 +142,6 @@ __device__ __forceinline__ void dma16(Rsrc r, uint32_t voff, uint32_t soff, uint
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
-struct GemmArgs {
-    const _Float16* hi;
-    const _Float16* lo;
-    const _Float16* shi;
-    const _Float16* slo;
-    const float* escale;
-    const uint8_t* w;
-    size_t rb;
-    float* y;
-    int M, N, K;
-    int ksplit;           // 2: two workgroups per tile, one per half of the super-blocks,
-                          // adding into a zeroed y (two fp32 adds onto 0 give the same
-                          // sum in either order)
-};
-
-// LDS layouts (per stage):
-//   activation plane: row r (token) at r*128, its eight 16-byte pieces
-//     stored at slot piece ^ ((r >> 1) & 7) - any 16 consecutive rows read
-//     the same piece from 16 distinct 16-byte bank groups;
-//   weight codes: 32-row groups of 1 KiB, [half 0: 32 x 16 B][half 1: 32 x 16 B].
-__device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 7; }
-
-// Per-lane source offsets of this wave's copies, fixed for the whole tile;
-// a K step only changes the scalar offset. Rows past M or N are clamped to
-// the last one (their results are not stored). A stage holds 32 activation
-// copies (16 per plane, 8 token rows x 128 B each), 8 weight-code copies (32
-// rows x 2 halves x 16 B) and, per super-block, 8 more (4 x 64 header rows,
-// 2 planes x 2 x 64 activation-sum rows); wave w takes an equal share of each.
-template <int NW>
-struct DmaPlan {
-    static constexpr int NA = 32 / NW, NB = 8 / NW, NS = 8 / NW;
-    Rsrc a_rs[2];           // hi, lo planes from the tile's first token row
-    uint32_t a_off[NA];     // byte offsets of the wave's activation copies
-    uint32_t a_plane[NA];   // plane of each copy (wave-uniform)
-    uint32_t a_lds[NA];     // LDS byte offset inside a stage
-    Rsrc w_rs;              // weight rows from the tile's first row
-    uint32_t b_off[NB];     // weight codes: row + 16 + 16 * half
-    uint32_t b_lds[NB];
-    Rsrc s_rs[NS];          // headers (w_rs) or an activation-sum plane
-    uint32_t s_off[NS];
-    uint32_t s_lds[NS];
-    uint32_t s_hdr[NS];     // 1: header copy (stride 144 per super-block), 0: sums (16)
-};
-
-template <int NW>
-__device__ __forceinline__ DmaPlan<NW> make_plan(const GemmArgs& g, int m0, int n0, int wave, int lane) {
-    using P = DmaPlan<NW>;
-    P d;
-    const int mt = g.M - m0 < BM ? g.M - m0 : BM;     // token rows in this tile
-    const int nt = g.N - n0 < BN ? g.N - n0 : BN;     // weight rows in this tile
-    const uint32_t kb = (uint32_t)g.K * 2;            // plane row bytes
-    d.a_rs[0] = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * kb);
-    d.a_rs[1] = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * kb);
-#pragma unroll
-    for (int i = 0; i < P::NA; i++) {
-        const int p = wave * P::NA + i;               // 0..31: 16 per plane
-        const int plane = p >> 4, pp = p & 15;
-        const int row = pp * 8 + (lane >> 3);
-        const int piece = (lane & 7) ^ a_swz(row);
-        const int r = row < mt ? row : mt - 1;
-        d.a_off[i] = (uint32_t)r * kb + (uint32_t)piece * 16;
-        d.a_plane[i] = plane;
-        d.a_lds[i] = plane * A_PLANE + pp * 1024;
-    }
-    d.w_rs = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
-#pragma unroll
-    for (int i = 0; i < P::NB; i++) {
-        const int c = wave * P::NB + i;               // 32-row group
-        int r = c * 32 + (lane & 31);
-        r = r < nt ? r : nt - 1;
-        d.b_off[i] = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
-        d.b_lds[i] = 2 * A_PLANE + c * 1024;
-    }
-    const int nbk = g.K >> 5;
-#pragma unroll
-    for (int i = 0; i < P::NS; i++) {
-        const int c = wave * P::NS + i;
-        if (c < 4) {
-            int r = c * 64 + lane;
-            r = r < nt ? r : nt - 1;
-            d.s_rs[i] = d.w_rs;
-            d.s_off[i] = (uint32_t)((size_t)r * g.rb);
-            d.s_lds[i] = c * 1024;
-            d.s_hdr[i] = 1;
-        } else {
-            const int plane = (c - 4) >> 1, part = (c - 4) & 1;
-            int r = part * 64 + lane;
-            r = r < mt ? r : mt - 1;
-            d.s_rs[i] = make_rsrc((plane ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
-            d.s_off[i] = (uint32_t)(r * nbk * 2);
-            d.s_lds[i] = HDR + plane * XS + part * 1024;
-            d.s_hdr[i] = 0;
-        }
-    }
-    return d;
-}
-
-// Copies of K step kt into stage `st` (+ super-block data into `sbb` when
-// kt starts a super-block). Returns the number of DMA instructions issued.
-template <int NW>
-__device__ __forceinline__ int issue_kstep(const DmaPlan<NW>& d, int kt, uint8_t* st, uint8_t* sbb) {
-    using P = DmaPlan<NW>;
-    const int sb = kt >> 2, jb = kt & 3;
-#pragma unroll
-    for (int i = 0; i < P::NA; i++)
-        dma16(d.a_plane[i] ? d.a_rs[1] : d.a_rs[0], d.a_off[i], (uint32_t)(kt * BK * 2), st + d.a_lds[i]);
-#pragma unroll
-    for (int i = 0; i < P::NB; i++) dma16(d.w_rs, d.b_off[i], (uint32_t)(sb * 144 + 32 * jb), st + d.b_lds[i]);
-    if (jb == 0) {
-#pragma unroll
-        for (int i = 0; i < P::NS; i++)
-            dma16(d.s_rs[i], d.s_off[i], (uint32_t)(d.s_hdr[i] ? sb * 144 : sb * 16), sbb + d.s_lds[i]);
-        return P::NA + P::NB + P::NS;
-    }
-    return P::NA + P::NB;
-}
 
 __device__ __forceinline__ void wait_dma(int outstanding) {
     // gfx9 s_waitcnt: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
@@ -309,68 +200,6 @@ __device__ __forceinline__ void lds_rd64(uint2& out, uint32_t a) {
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(out) : "v"(a), "n"(OFF));
 }
 
-// Activation hi/lo fragments of the wave's two token tiles for one K=16 sub-step.
-struct AFrag {
-    h8 hi[2], lo[2];
-};
-
-template <int S, int PLANE = A_PLANE>
-__device__ __forceinline__ void read_afrag(AFrag& o, uint32_t stage_off, const uint32_t a_base[2], const int a_x[2]) {
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        // piece (2S + lane/32) ^ swz: the lane/32 term is folded into a_x
-        const uint32_t a = a_base[tt] + stage_off + (uint32_t)(((2 * S) ^ a_x[tt]) * 16);
-        lds_rd128<0>(o.hi[tt], a);
-        lds_rd128<PLANE>(o.lo[tt], a);
-    }
-}
-
-// Wait until at most N LDS reads are outstanding (LDS reads complete in order).
-template <int N>
-__device__ __forceinline__ void wait_afrag(AFrag& o) {
-    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(o.hi[0]), "+v"(o.hi[1]), "+v"(o.lo[0]), "+v"(o.lo[1]) : "n"(N));
-}
-
-// Operands of one K=16 sub-step: activation hi/lo fragments of the wave's two
-// token tiles and the 4-bit codes of its two weight-row tiles.
-struct SubOps {
-    h8 ahi[2], alo[2];
-    uint2 u[2];
-};
-
-__device__ __forceinline__ void wait_sub(SubOps& o) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(o.ahi[0]), "+v"(o.ahi[1]), "+v"(o.alo[0]), "+v"(o.alo[1]), "+v"(o.u[0]), "+v"(o.u[1]));
-}
-
-// a_base[tt]: LDS address of token row (wm*64 + tt*32 + lane%32) in stage 0;
-// a_x: the row's swizzle; b_base: code address of (tile 0, half 0) in stage 0.
-template <int S>
-__device__ __forceinline__ void read_sub(SubOps& o, uint32_t stage_off, const uint32_t a_base[2], const int a_x[2],
-                                         uint32_t b_base) {
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        // piece (2S + lane/32) ^ swz: the lane/32 term is folded into a_x
-        const uint32_t a = a_base[tt] + stage_off + (uint32_t)(((2 * S) ^ a_x[tt]) * 16);
-        lds_rd128<0>(o.ahi[tt], a);
-        lds_rd128<A_PLANE>(o.alo[tt], a);
-    }
-    const uint32_t b = b_base + stage_off + (S & 1) * 512;
-    lds_rd64<0>(o.u[0], b);
-    lds_rd64<1024>(o.u[1], b);
-}
-
-__device__ __forceinline__ void scale_pair(uint32_t hy, uint32_t hw, int j, h2& mul, h2& add) {
-    uint32_t sc;
-    if (j < 4) sc = __builtin_amdgcn_ubfe(hy, 8 * j, 6);
-    else sc = __builtin_amdgcn_ubfe(hw, 8 * (j - 4), 4) | (__builtin_amdgcn_ubfe(hy, 8 * (j - 4) + 6, 2) << 4);
-    // even blocks use low nibbles (1024 + n), odd high (1024 + 16n)
-    const float s = (j & 1) ? (float)sc * 0.0625f : (float)sc;
-    const _Float16 h = (_Float16)s, a = (_Float16)(-1024.0f * s);
-    mul = h2{h, h};
-    add = h2{a, a};
-}
-
 __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
     h8 mm;
 #pragma unroll
@@ -383,343 +212,305 @@ __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
     return mm;
 }
 
-// NW waves as 2 (tokens) x NW/2 (weight rows); each wave computes 64 tokens x
-// 32*CT weight rows (2 x CT MFMA tiles of 32 x 32), NW * CT = 16.
-template <int NW, int CT>
-__global__ void __launch_bounds__(64 * NW)
-gemm_q4k_kernel(GemmArgs g, int ntn) {
-    static_assert(NW * CT == 16, "the workgroup tile is 128 x 256");
-    constexpr int WN = NW / 2;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    const int tile = blockIdx.x / g.ksplit, part = blockIdx.x % g.ksplit;
-    const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * BN;
-    // stage buffer i at smem + i * STAGE; super-block buffer i after them
-    auto stage = [&](int i) { return smem + i * STAGE; };
-    auto sbuf = [&](int i) { return smem + NSTAGE * STAGE + i * SB_STAGE; };
-    const int nsb_all = g.K >> 8;
-    const int sb_beg = part * nsb_all / g.ksplit, sb_end = (part + 1) * nsb_all / g.ksplit;
-    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;     // this workgroup's K steps [kt0, nk)
-    const DmaPlan<NW> plan = make_plan<NW>(g, m0, n0, wave, lane);
-
-    const uint32_t lds0 = lds_addr(smem);
-    uint32_t a_base[2];
-    int a_x[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        const int row = wm * 64 + tt * 32 + (lane & 31);
-        a_base[tt] = lds0 + row * 128;
-        a_x[tt] = (lane >> 5) ^ a_swz(row);
-    }
-    // weight tile ct of this wave: rows wn*32*CT + ct*32 + lane%32 (code group wn*CT + ct)
-    const uint32_t b_base = lds0 + 2 * A_PLANE + (wn * CT) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
-    const uint32_t hdr_base = lds0 + NSTAGE * STAGE + (wn * 32 * CT + (lane & 31)) * 16;
-    const uint32_t xs_base = lds0 + NSTAGE * STAGE + HDR + (wm * 64 + (lane & 31)) * 16;
-
-    f16v acc[2][CT], main_[2][CT];
-#pragma unroll
-    for (int a = 0; a < 2; a++)
-#pragma unroll
-        for (int b = 0; b < CT; b++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
-    const f16v zero = {};
-
-    // header words of the lane's weight rows for the current super-block
-    uint32_t hy[CT], hz[CT], hw[CT];
-    float dsc[CT], dmn[CT];
-
-    // steps kt+1 and kt+2 are in flight while step kt is computed
-    int cnt_next = 0;                                 // DMA count of step kt+1
-    (void)issue_kstep<NW>(plan, kt0, stage(0), sbuf(sb_beg & 1));
-    cnt_next = issue_kstep<NW>(plan, kt0 + 1, stage(1), sbuf(sb_beg & 1));
-    for (int sb = sb_beg; sb < sb_end; sb++) {
-        const uint32_t sb_off = (uint32_t)((sb & 1) * SB_STAGE);
-        // jb unrolled so every register-array index below is a constant
-#pragma unroll
-        for (int jb = 0; jb < 4; jb++) {
-            const int kt = 4 * sb + jb;
-            wait_dma(cnt_next);                       // step kt has landed
-            // after this barrier every wave has finished step kt-1, whose
-            // stage buffer is the one step kt+2 is copied into
-            __builtin_amdgcn_s_barrier();
-            cnt_next = 0;
-            if (kt + 2 < nk)
-                cnt_next = issue_kstep<NW>(plan, kt + 2, stage((kt + 2 - kt0) % NSTAGE), sbuf(((kt + 2) >> 2) & 1));
-            const uint32_t st_off = (uint32_t)(((kt - kt0) % NSTAGE) * STAGE);
-
-            if (jb == 0) {
-                u32x4 h[CT];
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) lds_rd128u<0>(h[ct], hdr_base + sb_off + 512 * ct);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    lds_wait_v(h[ct]);
-                    dsc[ct] = fp16_bits_to_f32(h[ct].x);
-                    dmn[ct] = fp16_bits_to_f32(h[ct].x >> 16);
-                    hy[ct] = h[ct].y;
-                    hz[ct] = h[ct].z;
-                    hw[ct] = h[ct].w;
-                }
-            }
-            h2 vmul[CT][2], vadd[CT][2];
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-                for (int i = 0; i < 2; i++) scale_pair(hy[ct], hw[ct], 2 * jb + i, vmul[ct][i], vadd[ct][i]);
-
-            // Four K=16 sub-steps. The step's weight codes are two 8-byte pairs per
-            // tile: pair s&1 holds sub-step s (low nibbles) and s+2 (high nibbles),
-            // read once. Activation fragments are read one sub-step ahead, and the
-            // weights of sub-step s+1 are decoded between the MFMAs of sub-step s.
-            uint2 u[2][CT];                             // [s & 1][tile]
-            AFrag af[2];                                // [s & 1]
-            h8 v[2][CT];                                // [s & 1][tile]
-            {
-                const uint32_t bq = b_base + st_off;
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    lds_rd64<0>(u[0][ct], bq + 1024 * ct);
-                    lds_rd64<512>(u[1][ct], bq + 1024 * ct);
-                }
-            }
-            read_afrag<0>(af[0], st_off, a_base, a_x);
-            read_afrag<1>(af[1], st_off, a_base, a_x);
-            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++) {
-                asm volatile("" : "+v"(u[0][ct]), "+v"(u[1][ct]));
-                v[0][ct] = decode_v(u[0][ct].x, u[0][ct].y, false, vmul[ct][0], vadd[ct][0]);
-            }
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                AFrag& o = af[s & 1];
-                if (s < 3) wait_afrag<4>(o);
-                else wait_afrag<0>(o);
-                __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_setprio(1);          // the MFMA burst issues ahead of the other waves
-                const h8 (&vs)[CT] = v[s & 1];
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            o.hi[tt], vs[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.lo[tt], vs[ct], main_[tt][ct], 0, 0, 0);
-                if (s < 3) {
-                    const int sn = s + 1;
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        v[sn & 1][ct] = decode_v(u[sn & 1][ct].x, u[sn & 1][ct].y, sn >= 2, vmul[ct][sn >> 1],
-                                                 vadd[ct][sn >> 1]);
-                }
-                // the MFMAs with the next sub-step's decode spread between them
-#pragma unroll
-                for (int i = 0; i < 4 * CT; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_setprio(0);
-                // the next-but-one activation fragments go into this sub-step's buffer
-                if (s == 0) read_afrag<2>(af[0], st_off, a_base, a_x);
-                if (s == 1) read_afrag<3>(af[1], st_off, a_base, a_x);
-            }
-
-            if (jb == 3) {
-                // min term of this super-block and the per-super-block epilogue
-                h8 shv[2], slv[2];
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
-                    lds_rd128<0>(shv[tt], xs_base + sb_off + tt * 512);
-                    lds_rd128<XS>(slv[tt], xs_base + sb_off + tt * 512);
-                }
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(shv[0]), "+v"(shv[1]), "+v"(slv[0]), "+v"(slv[1]));
-                h8 bmin[CT];
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
-                    const h8 mm = min_codes(hy[ct], hz[ct], hw[ct]);
-                    bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
-                    if (lane >= 32) { shv[tt] = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv[tt] = shv[tt]; }
-                    f16v mn[CT];
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin[ct], zero, 0, 0, 0);
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin[ct], mn[ct], 0, 0, 0);
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
-                            acc[tt][ct][r] = fmaf(-dmn[ct], mn[ct][r], acc[tt][ct][r]);
-                        }
-                }
-            }
-        }
-    }
-
-    // store: D[token][row] -> y[token * N + row] * 2^E_token
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-            const int n = n0 + wn * 32 * CT + ct * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * 64 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) {
-                    const float v = acc[tt][ct][r] * g.escale[m];
-                    if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = v;
-                    else atomicAdd(&g.y[(size_t)m * g.N + n], v);
-                }
-            }
-        }
-}
 
 // ---------------------------------------------------------------------------
-// 64-token tile variant: 4 waves (one 64 x 64 tile each, 64 tokens x 256
-// weight rows per workgroup) and 80 KB of LDS, so two workgroups share a CU
-// and their barriers do not keep the two waves of a SIMD in step.
-// LDS: 3 stages x (2 x 8 KB planes + 8 KB codes), one 4 KB header buffer (a
-// super-block's headers are read at its first K step; the next ones are
-// copied two K steps later, after a barrier every wave passed after reading
-// them), two 2 KB activation-sum buffers.
-constexpr int A_PLANE64 = 64 * BK * 2;              // 8 KB
-constexpr int STAGE64 = 2 * A_PLANE64 + B_TILE;     // 24 KB
-constexpr int HDR64_OFF = NSTAGE * STAGE64;         // 72 KB
-constexpr int XS64 = 64 * 16;                       // 1 KB per plane
-constexpr int XS64_BUF = 2 * XS64;
-constexpr int XS64_OFF = HDR64_OFF + HDR;           // 76 KB
-constexpr int GEMM64_LDS = XS64_OFF + 2 * XS64_BUF; // 80 KB
+// Split-precision prefill GEMM (Q4_K, M > 32).
+//
+// Operands (per 64-element K step):
+//   hi[m,k]  fp16(t),  t = xd_mb * q_mk * 2^(9 - E_m)  (|t| <= 65024)
+//   lo[m,k]  e4m3(t - hi)                  (the fp16 rounding residual)
+//   V[n,k]   sc_nb * nib_nk / 4            (<= 236.25: exact in fp16)
+//   V8[n,k]  e4m3(V)                       (converted in registers)
+// main = sum_k hi*V (v_mfma_f32_32x32x16_f16, exact products) + sum_k lo*V8
+// (v_mfma_f32_32x32x64_f8f6f4, one instruction per 64-K step and tile), so
+// main = 2^7 * sum_k xd*q*2^-E * sc*nib up to the residual term's error:
+// |lo| <= 2^-11 |t| and the two e4m3 roundings (relative 2^-4 each) leave a
+// per-product error below 2^-14 of |t*V| (2^-17 typical). The fp8 MFMA runs
+// at twice the fp16 rate, so a product costs 1.5 fp16-MFMA units, against 2
+// for an fp16 hi/lo pair of planes.
+// Per super-block: acc += d_n * 2^-7 * main - dmin_n * sum_b m_nb * xs_mb
+// (the min term: xs split into fp16 hi/lo against the exact 6-bit m).
+//
+// Workgroup = 8 waves, tile 32*TT tokens x 256 weight rows; wave w owns
+// every token of the tile and weight rows w*32 .. +32: TT MFMA tiles of
+// 32 x 32 (A = activations, B = weights; D lane = weight row, 16 tokens).
+// One decoded weight tile feeds TT token tiles, so the VALU work per MFMA
+// (nibble decode, e4m3 conversion, scales) shrinks as 1/TT; the VALU is
+// what bounds this kernel (fp16 and fp8 MFMAs of one wave co-issue with the
+// VALU of the other wave on its SIMD only in part).
+// Per K step the hi plane (128 B per token), the lo plane (64 B per token)
+// and the weight codes (32 B per row) are copied into LDS with
+// buffer_load_dwordx4 ... lds (1 KiB per wave instruction; scalar per-step
+// offsets), three stages in flight; headers and activation sums once per
+// super-block, double-buffered.
+//
+// LDS layouts (per stage):
+//   hi:    token row r at r*128; its eight 16-byte pieces (piece p holds the
+//          K=16 sub-step p/2, lane half p%2) at slot p ^ ((r >> 1) & 7);
+//   lo:    [lane half g][token row r][2 x 16 B] at g*BM*32 + r*32, the half
+//          h (sub-steps 2h, 2h+1) at slot h ^ ((r >> 3) & 1);
+//   codes: 32-row groups of 1 KiB, [half 0: 32 x 16 B][half 1: 32 x 16 B].
+// The swizzles make any 16 consecutive token rows read one piece from 16
+// distinct 16-byte bank groups.
+//
+// lo byte order: each 64-element chunk is stored as [g][s][e], byte
+// 32g + 8s + e holding the residual of the hi-plane position 16s + 8g + e,
+// so lane half g of the fp8 MFMA reads 32 contiguous bytes that pair with
+// the V values it decoded for the four fp16 sub-steps (V8 = their e4m3).
 
-struct DmaPlan64 {
-    Rsrc a_rs[2];
-    uint32_t a_off[4], a_plane[4], a_lds[4];
-    Rsrc w_rs;
-    uint32_t b_off[2], b_lds[2];
-    uint32_t h_off, h_lds;
-    Rsrc x_rs;                       // waves 0-1: one activation-sum plane
-    uint32_t x_off;
+constexpr int SP_BN = 256, SP_NW = 8;
+
+template <int TT>
+struct SpCfg {
+    static constexpr int BM = 32 * TT;
+    static constexpr int HI = BM * 128, LO = BM * 64, CODES = SP_BN * 32;
+    static constexpr int STAGE = HI + LO + CODES;
+    static constexpr int HDR = SP_BN * 16, XS = BM * 16;
+    static constexpr int SBUF = HDR + 2 * XS;
+    static constexpr int LDS = 3 * STAGE + 2 * SBUF;
+    static constexpr int N_HI = HI / 1024, N_LO = LO / 1024, N_CODES = CODES / 1024;
+    static constexpr int NX = 2 * XS / 1024;          // activation-sum copies per super-block
+    static_assert(N_HI % SP_NW == 0 && N_CODES == SP_NW && N_LO <= SP_NW && NX <= 4, "copy split");
 };
 
-__device__ __forceinline__ DmaPlan64 make_plan64(const GemmArgs& g, int m0, int n0, int wave, int lane) {
-    DmaPlan64 d;
-    const int mt = g.M - m0 < 64 ? g.M - m0 : 64;
-    const int nt = g.N - n0 < BN ? g.N - n0 : BN;
-    const uint32_t kb = (uint32_t)g.K * 2;
-    d.a_rs[0] = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * kb);
-    d.a_rs[1] = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * kb);
+struct SpArgs {
+    const _Float16* hi;
+    const uint8_t* lo;
+    const _Float16* shi;
+    const _Float16* slo;
+    const float* escale;
+    const uint8_t* w;
+    size_t rb;
+    float* y;
+    int M, N, K;
+    int ksplit;           // 2: two workgroups per tile, one per half of the super-blocks,
+                          // adding into a zeroed y (two fp32 adds onto 0 give the same
+                          // sum in either order)
+    int ntn, ntiles;      // weight-row tiles, tiles
+};
+
+// Per-lane copy sources of one wave, fixed for the whole tile; a K step
+// changes only the scalar offset. Every wave issues N_HI/8 hi copies and one
+// code copy per K step; waves below N_LO one lo copy; per super-block waves
+// 0..3 one header copy and waves 4.. one activation-sum copy. Rows past M
+// or N are clamped to the last one (their results are not stored).
+template <int TT>
+struct SpPlan {
+    using Cf = SpCfg<TT>;
+    static constexpr int H = Cf::N_HI / SP_NW;
+    Rsrc rs_hi, rs_lo, rs_w, rs_xs;
+    uint32_t hi_off[H], hi_lds[H], lo_off, lo_lds, c_off, c_lds, h_off, h_lds, x_off, x_lds;
+    int has_lo, has_h, has_x;         // wave-uniform
+};
+
+template <int TT>
+__device__ __forceinline__ SpPlan<TT> sp_plan(const SpArgs& g, int m0, int n0, int wave, int lane) {
+    using Cf = SpCfg<TT>;
+    using P = SpPlan<TT>;
+    P d;
+    const int mt = g.M - m0 < Cf::BM ? g.M - m0 : Cf::BM;
+    const int nt = g.N - n0 < SP_BN ? g.N - n0 : SP_BN;
+    const int nbk = g.K >> 5;
+    d.rs_hi = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * (uint32_t)g.K * 2);
+    d.rs_lo = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * (uint32_t)g.K);
+    d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int p = wave * 4 + i;                   // 0..15: 8 per plane
-        const int plane = p >> 3, pp = p & 7;
-        const int row = pp * 8 + (lane >> 3);
-        const int piece = (lane & 7) ^ a_swz(row);
+    for (int i = 0; i < P::H; i++) {
+        const int j = wave * P::H + i;
+        const int row = 8 * j + (lane >> 3);
+        const int piece = (lane & 7) ^ ((row >> 1) & 7);
         const int r = row < mt ? row : mt - 1;
-        d.a_off[i] = (uint32_t)r * kb + (uint32_t)piece * 16;
-        d.a_plane[i] = plane;
-        d.a_lds[i] = plane * A_PLANE64 + pp * 1024;
+        d.hi_off[i] = (uint32_t)r * (uint32_t)g.K * 2 + (uint32_t)piece * 16;
+        d.hi_lds[i] = (uint32_t)j * 1024;
     }
-    d.w_rs = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int c = wave * 2 + i;
-        int r = c * 32 + (lane & 31);
-        r = r < nt ? r : nt - 1;
-        d.b_off[i] = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
-        d.b_lds[i] = 2 * A_PLANE64 + c * 1024;
+    d.has_lo = wave < Cf::N_LO;
+    {
+        const int o = 1024 * (wave % Cf::N_LO) + 16 * lane;
+        const int gh = o / (Cf::BM * 32), rem = o % (Cf::BM * 32);
+        const int row = rem >> 5, slot = (rem >> 4) & 1;
+        const int h = slot ^ ((row >> 3) & 1);
+        const int r = row < mt ? row : mt - 1;
+        d.lo_off = (uint32_t)r * (uint32_t)g.K + (uint32_t)(32 * gh + 16 * h);
+        d.lo_lds = Cf::HI + (uint32_t)o;
     }
     {
-        int r = wave * 64 + lane;
+        int r = 32 * wave + (lane & 31);
+        r = r < nt ? r : nt - 1;
+        d.c_off = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
+        d.c_lds = Cf::HI + Cf::LO + (uint32_t)wave * 1024;
+    }
+    d.has_h = wave < 4;
+    {
+        int r = 64 * (wave & 3) + lane;
         r = r < nt ? r : nt - 1;
         d.h_off = (uint32_t)((size_t)r * g.rb);
-        d.h_lds = HDR64_OFF + wave * 1024;
+        d.h_lds = (uint32_t)(wave & 3) * 1024;
     }
+    const int xw = wave - 4;
+    d.has_x = xw >= 0 && xw < Cf::NX;
     {
-        const int nbk = g.K >> 5;
-        const int r = lane < mt ? lane : mt - 1;
-        d.x_rs = make_rsrc(((wave & 1) ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
+        const int q = xw < 0 ? 0 : xw;
+        const int per = Cf::XS / 1024 > 0 ? Cf::XS / 1024 : 1;
+        const int pl = q / per, part = q % per;
+        int r = 64 * part + lane;
+        r = r < mt ? r : mt - 1;
+        d.rs_xs = make_rsrc((pl ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
         d.x_off = (uint32_t)(r * nbk * 2);
+        d.x_lds = Cf::HDR + pl * Cf::XS + part * 1024;
     }
     return d;
 }
 
-__device__ __forceinline__ int issue_kstep64(const DmaPlan64& d, int wave, int kt, int kt0, uint8_t* smem) {
+// Copies of K step kt into stage `st` (+ super-block data into `sbb` when kt
+// starts a super-block). Returns the number of copies issued.
+template <int TT>
+__device__ __forceinline__ int sp_issue(const SpPlan<TT>& d, int kt, uint8_t* st, uint8_t* sbb) {
+    using P = SpPlan<TT>;
     const int sb = kt >> 2, jb = kt & 3;
-    uint8_t* st = smem + ((kt - kt0) % NSTAGE) * STAGE64;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        dma16(d.a_plane[i] ? d.a_rs[1] : d.a_rs[0], d.a_off[i], (uint32_t)(kt * BK * 2), st + d.a_lds[i]);
-#pragma unroll
-    for (int i = 0; i < 2; i++) dma16(d.w_rs, d.b_off[i], (uint32_t)(sb * 144 + 32 * jb), st + d.b_lds[i]);
-    if (jb != 0) return 6;
-    dma16(d.w_rs, d.h_off, (uint32_t)(sb * 144), smem + d.h_lds);
-    if (wave >= 2) return 7;
-    dma16(d.x_rs, d.x_off, (uint32_t)(sb * 16), smem + XS64_OFF + (sb & 1) * XS64_BUF + (wave & 1) * XS64);
-    return 8;
+    for (int i = 0; i < P::H; i++) dma16(d.rs_hi, d.hi_off[i], (uint32_t)(kt * 128), st + d.hi_lds[i]);
+    dma16(d.rs_w, d.c_off, (uint32_t)(sb * 144 + 32 * jb), st + d.c_lds);
+    int n = P::H + 1;
+    if (d.has_lo) {
+        dma16(d.rs_lo, d.lo_off, (uint32_t)(kt * 64), st + d.lo_lds);
+        n++;
+    }
+    if (jb == 0) {
+        if (d.has_h) {
+            dma16(d.rs_w, d.h_off, (uint32_t)(sb * 144), sbb + d.h_lds);
+            n++;
+        }
+        if (d.has_x) {
+            dma16(d.rs_xs, d.x_off, (uint32_t)(sb * 16), sbb + d.x_lds);
+            n++;
+        }
+    }
+    return n;
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-gemm_q4k_m64(GemmArgs g, int ntn) {
-    constexpr int CT = 2;
+typedef int i8x32 __attribute__((ext_vector_type(8)));   // 32 fp8 bytes
+
+template <int N, typename V, int T>
+__device__ __forceinline__ void lgkm_wait(V (&a)[T]) {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+    for (int i = 0; i < T; i++) asm volatile("" : "+v"(a[i]));
+}
+
+__device__ __forceinline__ uint32_t h4_to_e4m3(uint32_t h01, uint32_t h23) {
+    uint32_t w;
+    asm("v_cvt_scalef32_pk_fp8_f16 %0, %1, 1.0\n\tv_cvt_scalef32_pk_fp8_f16 %0, %2, 1.0 op_sel:[0,0,1]"
+        : "=&v"(w) : "v"(h01), "v"(h23));
+    return w;
+}
+__device__ __forceinline__ uint2 h8_to_e4m3(h8 v) {
+    const u32x4 q = __builtin_bit_cast(u32x4, v);
+    return make_uint2(h4_to_e4m3(q.x, q.y), h4_to_e4m3(q.z, q.w));
+}
+
+// Per-block decode constants for V = sc * nibble / 4: decode_v's packed fma
+// (h - 1024) * mul computes it exactly (h = 1024 + n for low nibbles, 1024 +
+// 16n for high ones, hence mul = sc/4 or sc/64).
+__device__ __forceinline__ void scale_pair4(uint32_t hy, uint32_t hw, int j, h2& mul, h2& add) {
+    uint32_t sc;
+    if (j < 4) sc = __builtin_amdgcn_ubfe(hy, 8 * j, 6);
+    else sc = __builtin_amdgcn_ubfe(hw, 8 * (j - 4), 4) | (__builtin_amdgcn_ubfe(hy, 8 * (j - 4) + 6, 2) << 4);
+    const float s = (j & 1) ? (float)sc * (0.0625f * 0.25f) : (float)sc * 0.25f;
+    const _Float16 h = (_Float16)s, a = (_Float16)(-1024.0f * s);
+    mul = h2{h, h};
+    add = h2{a, a};
+}
+
+template <int TT>
+__device__ __forceinline__ void rd_tiles(h8 (&o)[TT], uint32_t a) {
+    lds_rd128<0>(o[0], a);
+    if (TT > 1) lds_rd128<4096>(o[1 % TT], a);
+    if (TT > 2) lds_rd128<8192>(o[2 % TT], a);
+    if (TT > 3) lds_rd128<12288>(o[3 % TT], a);
+}
+template <int OFF>
+__device__ __forceinline__ void lds_rd_lo(i8x32& o, uint32_t a0, uint32_t a1) {
+    u32x4 p0, p1;
+    lds_rd128u<OFF>(p0, a0);
+    lds_rd128u<OFF>(p1, a1);
+    asm volatile("" : "+v"(p0), "+v"(p1));
+    o = i8x32{(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w, (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
+}
+template <int TT>
+__device__ __forceinline__ void rd_lo(i8x32 (&o)[TT], uint32_t a0, uint32_t a1) {
+    lds_rd_lo<0>(o[0], a0, a1);
+    if (TT > 1) lds_rd_lo<1024>(o[1 % TT], a0, a1);
+    if (TT > 2) lds_rd_lo<2048>(o[2 % TT], a0, a1);
+    if (TT > 3) lds_rd_lo<3072>(o[3 % TT], a0, a1);
+}
+
+// Tile of linear index `lin`: groups of kGroupM token tiles walk the weight
+// tiles together (consecutive tiles share a weight tile, the next kGroupM
+// share the next one), so the tiles in flight on one XCD reuse both operands
+// in its L2.
+constexpr int kGroupM = 8;
+__device__ __forceinline__ void sp_tile(int lin, int ntm, int ntn, int& tm, int& tn) {
+    const int per_group = kGroupM * ntn;
+    const int grp = lin / per_group, in = lin % per_group;
+    const int gm = ntm - grp * kGroupM < kGroupM ? ntm - grp * kGroupM : kGroupM;
+    tm = grp * kGroupM + in % gm;
+    tn = in / gm;
+}
+
+template <int TT>
+__global__ void __launch_bounds__(64 * SP_NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_q4k_sp(SpArgs g) {
+    using C = SpCfg<TT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave;
-    const int tile = blockIdx.x / g.ksplit, part = blockIdx.x % g.ksplit;
-    const int m0 = (tile / ntn) * 64, n0 = (tile % ntn) * BN;
+    // blocks are dealt to the 8 XCDs round-robin: give each XCD a contiguous
+    // run of linear tile indices
+    const int nblk = g.ntiles * g.ksplit;
+    const int bid = blockIdx.x;
+    const int lin = (nblk & 7) == 0 ? (bid & 7) * (nblk >> 3) + (bid >> 3) : bid;
+    const int tile = lin / g.ksplit, part = lin % g.ksplit;
+    int tm, tn;
+    sp_tile(tile, g.ntiles / g.ntn, g.ntn, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * SP_BN;
     const int nsb_all = g.K >> 8;
     const int sb_beg = part * nsb_all / g.ksplit, sb_end = (part + 1) * nsb_all / g.ksplit;
-    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;     // this workgroup's K steps [kt0, nk)
-    const DmaPlan64 plan = make_plan64(g, m0, n0, wave, lane);
+    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;
+    const SpPlan<TT> plan = sp_plan<TT>(g, m0, n0, wave, lane);
+    auto stage = [&](int i) { return smem + i * C::STAGE; };
+    auto sbuf = [&](int i) { return smem + 3 * C::STAGE + i * C::SBUF; };
 
     const uint32_t lds0 = lds_addr(smem);
-    uint32_t a_base[2];
-    int a_x[2];
+    const int gl = lane >> 5, r32 = lane & 31;
+    uint32_t a_s[4], lo_h[2];
+    {
+        const int a_x = gl ^ ((r32 >> 1) & 7);
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        const int row = tt * 32 + (lane & 31);
-        a_base[tt] = lds0 + row * 128;
-        a_x[tt] = (lane >> 5) ^ a_swz(row);
+        for (int s = 0; s < 4; s++) a_s[s] = lds0 + r32 * 128 + (uint32_t)(((2 * s) ^ a_x) * 16);
+        const int x = (r32 >> 3) & 1;
+        const uint32_t lb = lds0 + C::HI + gl * C::BM * 32 + r32 * 32;
+        lo_h[0] = lb + 16 * x;
+        lo_h[1] = lb + 16 * (x ^ 1);
     }
-    // weight tile ct of this wave: rows wn*32*CT + ct*32 + lane%32 (code group wn*CT + ct)
-    const uint32_t b_base = lds0 + 2 * A_PLANE64 + (wn * CT) * 1024 + (lane & 31) * 16 + 8 * (lane >> 5);
-    const uint32_t hdr_base = lds0 + HDR64_OFF + (wn * 32 * CT + (lane & 31)) * 16;
-    const uint32_t xs_base = lds0 + XS64_OFF + (lane & 31) * 16;
+    // this wave's weight rows: wave*32 + lane%32 (code group `wave`)
+    const uint32_t b_base = lds0 + C::HI + C::LO + wave * 1024 + (lane & 31) * 16 + 8 * gl;
+    const uint32_t hdr_base = lds0 + 3 * C::STAGE + (wave * 32 + (lane & 31)) * 16;
+    const uint32_t xs_base = lds0 + 3 * C::STAGE + C::HDR + (lane & 31) * 16;
 
-    f16v acc[2][CT], main_[2][CT];
+    f16v acc[TT], main_[TT];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < TT; a++)
 #pragma unroll
-        for (int b = 0; b < CT; b++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
-    const f16v zero = {};
+        for (int r = 0; r < 16; r++) acc[a][r] = 0.0f;
 
-    // header words of the lane's weight rows for the current super-block
-    uint32_t hy[CT], hz[CT], hw[CT];
-    float dsc[CT], dmn[CT];
+    uint32_t hy = 0, hz = 0, hw = 0;
+    float dsc = 0.0f, dmn = 0.0f;
 
-    // steps kt+1 and kt+2 are in flight while step kt is computed
-    int cnt_next = 0;                                 // DMA count of step kt+1
-    (void)issue_kstep64(plan, wave, kt0, kt0, smem);
-    cnt_next = issue_kstep64(plan, wave, kt0 + 1, kt0, smem);
+    int cnt_next = 0;                                 // copies of step kt+1
+    (void)sp_issue<TT>(plan, kt0, stage(0), sbuf(sb_beg & 1));
+    cnt_next = sp_issue<TT>(plan, kt0 + 1, stage(1), sbuf(sb_beg & 1));
     for (int sb = sb_beg; sb < sb_end; sb++) {
-        const uint32_t xs_off = (uint32_t)((sb & 1) * XS64_BUF);
-        // jb unrolled so every register-array index below is a constant
+        const uint32_t sb_off = (uint32_t)((sb & 1) * C::SBUF);
 #pragma unroll
         for (int jb = 0; jb < 4; jb++) {
             const int kt = 4 * sb + jb;
@@ -729,144 +520,112 @@ gemm_q4k_m64(GemmArgs g, int ntn) {
             __builtin_amdgcn_s_barrier();
             cnt_next = 0;
             if (kt + 2 < nk)
-                cnt_next = issue_kstep64(plan, wave, kt + 2, kt0, smem);
-            const uint32_t st_off = (uint32_t)(((kt - kt0) % NSTAGE) * STAGE64);
+                cnt_next = sp_issue<TT>(plan, kt + 2, stage((kt + 2 - kt0) % 3), sbuf(((kt + 2) >> 2) & 1));
+            const uint32_t st_off = (uint32_t)(((kt - kt0) % 3) * C::STAGE);
 
             if (jb == 0) {
-                u32x4 h[CT];
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) lds_rd128u<0>(h[ct], hdr_base + 512 * ct);
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    lds_wait_v(h[ct]);
-                    dsc[ct] = fp16_bits_to_f32(h[ct].x);
-                    dmn[ct] = fp16_bits_to_f32(h[ct].x >> 16);
-                    hy[ct] = h[ct].y;
-                    hz[ct] = h[ct].z;
-                    hw[ct] = h[ct].w;
-                }
+                u32x4 h;
+                lds_rd128u<0>(h, hdr_base + sb_off);
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(h));
+                dsc = fp16_bits_to_f32(h.x) * 0.0078125f;   // d * 2^-7 (main carries 2^7)
+                dmn = fp16_bits_to_f32(h.x >> 16);
+                hy = h.y;
+                hz = h.z;
+                hw = h.w;
             }
-            h2 vmul[CT][2], vadd[CT][2];
+            h2 vmul[2], vadd[2];
 #pragma unroll
-            for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-                for (int i = 0; i < 2; i++) scale_pair(hy[ct], hw[ct], 2 * jb + i, vmul[ct][i], vadd[ct][i]);
+            for (int i = 0; i < 2; i++) scale_pair4(hy, hw, 2 * jb + i, vmul[i], vadd[i]);
 
-            // Four K=16 sub-steps. The step's weight codes are two 8-byte pairs per
-            // tile: pair s&1 holds sub-step s (low nibbles) and s+2 (high nibbles),
-            // read once. Activation fragments are read one sub-step ahead, and the
-            // weights of sub-step s+1 are decoded between the MFMAs of sub-step s.
-            uint2 u[2][CT];                             // [s & 1][tile]
-            AFrag af[2];                                // [s & 1]
-            h8 v[2][CT];                                // [s & 1][tile]
-            {
-                const uint32_t bq = b_base + st_off;
+            // Four K=16 sub-steps on the hi plane; the weight codes are two 8-byte
+            // pairs (pair s&1: sub-step s low nibbles, s+2 high nibbles).
+            uint2 u[2];
+            h8 ah[2][TT];                               // [s & 1][token tile]
+            h8 v[2];                                    // [s & 1]
+            uint2 v8[4];                                // e4m3 V of the four sub-steps
+            const uint32_t bq = b_base + st_off;
+            lds_rd64<0>(u[0], bq);
+            lds_rd64<512>(u[1], bq);
+            uint32_t as[4];
 #pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    lds_rd64<0>(u[0][ct], bq + 1024 * ct);
-                    lds_rd64<512>(u[1][ct], bq + 1024 * ct);
-                }
-            }
-            read_afrag<0, A_PLANE64>(af[0], st_off, a_base, a_x);
-            read_afrag<1, A_PLANE64>(af[1], st_off, a_base, a_x);
-            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-#pragma unroll
-            for (int ct = 0; ct < CT; ct++) {
-                asm volatile("" : "+v"(u[0][ct]), "+v"(u[1][ct]));
-                v[0][ct] = decode_v(u[0][ct].x, u[0][ct].y, false, vmul[ct][0], vadd[ct][0]);
-            }
+            for (int q = 0; q < 4; q++) as[q] = a_s[q] + st_off;
+            rd_tiles<TT>(ah[0], as[0]);
+            rd_tiles<TT>(ah[1], as[1]);
+            lgkm_wait<2 * TT>(u);
+            v[0] = decode_v(u[0].x, u[0].y, false, vmul[0], vadd[0]);
+            i8x32 al[TT];
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                AFrag& o = af[s & 1];
-                if (s < 3) wait_afrag<4>(o);
-                else wait_afrag<0>(o);
+                // LDS reads in flight behind this sub-step's TT: s=0,1: the other
+                // buffer's TT; s=2: sub-step 3's TT and the 2TT residual reads;
+                // s=3: those 2TT
+                if (s < 2) lgkm_wait<TT>(ah[s & 1]);
+                else if (s == 2) lgkm_wait<3 * TT>(ah[s & 1]);
+                else lgkm_wait<2 * TT>(ah[s & 1]);
                 __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_setprio(1);          // the MFMA burst issues ahead of the other waves
-                const h8 (&vs)[CT] = v[s & 1];
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            o.hi[tt], vs[ct], (jb == 0 && s == 0) ? zero : main_[tt][ct], 0, 0, 0);
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        main_[tt][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.lo[tt], vs[ct], main_[tt][ct], 0, 0, 0);
+                for (int tt = 0; tt < TT; tt++)
+                    main_[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        ah[s & 1][tt], v[s & 1], (jb == 0 && s == 0) ? f16v{} : main_[tt], 0, 0, 0);
+                v8[s] = h8_to_e4m3(v[s & 1]);
                 if (s < 3) {
                     const int sn = s + 1;
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        v[sn & 1][ct] = decode_v(u[sn & 1][ct].x, u[sn & 1][ct].y, sn >= 2, vmul[ct][sn >> 1],
-                                                 vadd[ct][sn >> 1]);
-                }
-                // the MFMAs with the next sub-step's decode spread between them
-#pragma unroll
-                for (int i = 0; i < 4 * CT; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    v[sn & 1] = decode_v(u[sn & 1].x, u[sn & 1].y, sn >= 2, vmul[sn >> 1], vadd[sn >> 1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_s_setprio(0);
-                // the next-but-one activation fragments go into this sub-step's buffer
-                if (s == 0) read_afrag<2, A_PLANE64>(af[0], st_off, a_base, a_x);
-                if (s == 1) read_afrag<3, A_PLANE64>(af[1], st_off, a_base, a_x);
+                if (s < 2) rd_tiles<TT>(ah[s & 1], as[s + 2]);
+                if (s == 1) rd_lo<TT>(al, lo_h[0] + st_off, lo_h[1] + st_off);
             }
+            lgkm_wait<0>(al);
+            const i8x32 b8 = {(int)v8[0].x, (int)v8[0].y, (int)v8[1].x, (int)v8[1].y,
+                              (int)v8[2].x, (int)v8[2].y, (int)v8[3].x, (int)v8[3].y};
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+                main_[tt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[tt], b8, main_[tt], 0, 0, 0, 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
 
             if (jb == 3) {
-                // min term of this super-block and the per-super-block epilogue
-                h8 shv[2], slv[2];
+                // min term and the super-block's scale: sum_b m * xs as a K = 16
+                // product (lanes 32..63 supply k = 8..15: zero)
+                h8 shv[TT], slv[TT];
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
-                    lds_rd128<0>(shv[tt], xs_base + xs_off + tt * 512);
-                    lds_rd128<XS64>(slv[tt], xs_base + xs_off + tt * 512);
+                for (int tt = 0; tt < TT; tt++) {
+                    lds_rd128<0>(shv[tt], xs_base + sb_off + tt * 512);
+                    lds_rd128<C::XS>(slv[tt], xs_base + sb_off + tt * 512);
                 }
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(shv[0]), "+v"(shv[1]), "+v"(slv[0]), "+v"(slv[1]));
-                h8 bmin[CT];
+                const h8 mm = min_codes(hy, hz, hw);
+                const h8 bmin = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
+                lgkm_wait<0>(shv);
+                lgkm_wait<0>(slv);
 #pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    // lanes 32..63 supply k = 8..15 of the K=16 min MFMA: zero
-                    const h8 mm = min_codes(hy[ct], hz[ct], hw[ct]);
-                    bmin[ct] = lane < 32 ? mm : h8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
+                for (int tt = 0; tt < TT; tt++) {
                     if (lane >= 32) { shv[tt] = h8{0, 0, 0, 0, 0, 0, 0, 0}; slv[tt] = shv[tt]; }
-                    f16v mn[CT];
+                    f16v mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin, f16v{}, 0, 0, 0);
+                    mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin, mn, 0, 0, 0);
 #pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(shv[tt], bmin[ct], zero, 0, 0, 0);
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-                        mn[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(slv[tt], bmin[ct], mn[ct], 0, 0, 0);
-#pragma unroll
-                    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            acc[tt][ct][r] = fmaf(dsc[ct], main_[tt][ct][r], acc[tt][ct][r]);
-                            acc[tt][ct][r] = fmaf(-dmn[ct], mn[ct][r], acc[tt][ct][r]);
-                        }
+                    for (int r = 0; r < 16; r++) {
+                        acc[tt][r] = fmaf(dsc, main_[tt][r], acc[tt][r]);
+                        acc[tt][r] = fmaf(-dmn, mn[r], acc[tt][r]);
+                    }
                 }
             }
         }
     }
 
     // store: D[token][row] -> y[token * N + row] * 2^E_token
+    const int n = n0 + wave * 32 + (lane & 31);
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++)
+    for (int tt = 0; tt < TT; tt++)
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-            const int n = n0 + wn * 32 * CT + ct * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + tt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) {
-                    const float v = acc[tt][ct][r] * g.escale[m];
-                    if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = v;
-                    else atomicAdd(&g.y[(size_t)m * g.N + n], v);
-                }
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + tt * 32 + 8 * (r >> 2) + 4 * gl + (r & 3);
+            if (m < g.M && n < g.N) {
+                const float val = acc[tt][r] * g.escale[m];
+                if (g.ksplit == 1) g.y[(size_t)m * g.N + n] = val;
+                else atomicAdd(&g.y[(size_t)m * g.N + n], val);
             }
         }
 }
@@ -904,7 +663,7 @@ static Planes carve_planes(void* base, int M, int K) {
 // registers (NF float4 per thread, 8 consecutive threads per 32-element
 // block). Pass 1: block scales and their row maximum (the exponent E); pass
 // 2: codes, hi/lo and shi/slo from the registers.
-template <int NF>
+template <int NF, bool SP>
 __global__ void __launch_bounds__(1024)
 quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
 #pragma clang fp contract(off)
@@ -947,33 +706,23 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0) P.escale[m] = ldexpf(1.0f, e);
     // pass 2
-    _Float16* hi = P.hi + (size_t)m * K;
-    _Float16* lo = P.lo + (size_t)m * K;
 #pragma unroll
     for (int j = 0; j < NF; j++) {
         const int i = threadIdx.x + j * nt;
         const Q8Group q = quant_group8(v[j]);
         if (i < n4) {
             const float ds = q.d * inv;
-            h4 vh, vl;
+            float t[4];
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                float t = ds * (float)(int8_t)(q.packed >> (8 * c));
-                asm volatile("" : "+v"(t));   // hi and lo both from fl32(t): no fused fp16 product
-                const _Float16 h = (_Float16)t;
-                vh[c] = h;
-                vl[c] = (_Float16)(t - (float)h);
-            }
-            // stored as k0 k2 k1 k3 (the order decode_v produces weights in)
-            *reinterpret_cast<h4*>(hi + 4 * i) = h4{vh[0], vh[2], vh[1], vh[3]};
-            *reinterpret_cast<h4*>(lo + 4 * i) = h4{vl[0], vl[2], vl[1], vl[3]};
+            for (int c = 0; c < 4; c++) t[c] = ds * (float)(int8_t)(q.packed >> (8 * c));
+            store_group<SP>(t, P.hi, P.lo, (size_t)m * K, 4 * i);
             if ((i & 7) == 0) {
                 const int b = i >> 3;
-                float t = q.sum * inv;
-                asm volatile("" : "+v"(t));
-                const _Float16 h = (_Float16)t;
+                float xs = q.sum * inv;
+                asm volatile("" : "+v"(xs));
+                const _Float16 h = (_Float16)xs;
                 P.shi[(size_t)m * nb + b] = h;
-                P.slo[(size_t)m * nb + b] = (_Float16)(t - (float)h);
+                P.slo[(size_t)m * nb + b] = (_Float16)(xs - (float)h);
             }
         }
     }
@@ -1522,6 +1271,10 @@ bool gemm_supported(uint32_t type, int M, int K) {
     return type == T_Q4_K && M >= kMfMinM && K % 256 == 0;
 }
 
+// Planes for M rows: the fp16 hi/lo pair for the small-M MFMA kernel
+// (M <= kMfMaxM), the split-precision pair for the GEMM otherwise.
+static bool planes_sp(int M) { return M > kMfMaxM; }
+
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     // NF float4 per thread, at most 1024 threads (K <= 32768); 8 | K/4/NF since 32 | K
@@ -1530,19 +1283,37 @@ hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipS
     const int threads = n4 / nf;
     if (threads % 8 != 0) return hipErrorInvalidValue;     // 8-thread groups must not straddle blocks
     const Planes P = carve_planes(planes, M, K);
+    const bool sp = planes_sp(M);
+#define LP_QP(NF)                                                                                   \
+    if (sp) hipLaunchKernelGGL((quant_planes_kernel<NF, true>), dim3(M), dim3(threads), 0, st, x, K, P); \
+    else hipLaunchKernelGGL((quant_planes_kernel<NF, false>), dim3(M), dim3(threads), 0, st, x, K, P);
     switch (nf) {
-        case 1: hipLaunchKernelGGL(quant_planes_kernel<1>, dim3(M), dim3(threads), 0, st, x, K, P); break;
-        case 2: hipLaunchKernelGGL(quant_planes_kernel<2>, dim3(M), dim3(threads), 0, st, x, K, P); break;
-        case 4: hipLaunchKernelGGL(quant_planes_kernel<4>, dim3(M), dim3(threads), 0, st, x, K, P); break;
-        default: hipLaunchKernelGGL(quant_planes_kernel<8>, dim3(M), dim3(threads), 0, st, x, K, P); break;
+        case 1: LP_QP(1) break;
+        case 2: LP_QP(2) break;
+        case 4: LP_QP(4) break;
+        default: LP_QP(8) break;
     }
+#undef LP_QP
     return hipGetLastError();
 }
 
 static hipError_t launch_planes_from_act(const ActView& A, void* planes, int M, int K, hipStream_t st) {
     const Planes P = carve_planes(planes, M, K);
-    hipLaunchKernelGGL(gemm_prep_kernel, dim3((K + kPlaneChunk - 1) / kPlaneChunk, M), dim3(kPlaneChunk / 4), 0, st,
-                       A, K, P.hi, P.lo, P.shi, P.slo, P.escale);
+    const dim3 grid((K + kPlaneChunk - 1) / kPlaneChunk, M);
+    if (planes_sp(M))
+        hipLaunchKernelGGL(gemm_prep_kernel<true>, grid, dim3(kPlaneChunk / 4), 0, st, A, K, P.hi, P.lo, P.shi,
+                           P.slo, P.escale);
+    else
+        hipLaunchKernelGGL(gemm_prep_kernel<false>, grid, dim3(kPlaneChunk / 4), 0, st, A, K, P.hi, P.lo, P.shi,
+                           P.slo, P.escale);
+    return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_sp(SpArgs g, hipStream_t st) {
+    g.ntiles = g.ntn * ((g.M + SpCfg<TT>::BM - 1) / SpCfg<TT>::BM);
+    const long nblk = (long)g.ntiles * g.ksplit;
+    hipLaunchKernelGGL((gemm_q4k_sp<TT>), dim3((unsigned)nblk), dim3(64 * SP_NW), SpCfg<TT>::LDS, st, g);
     return hipGetLastError();
 }
 
@@ -1557,27 +1328,22 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
                            0, st, a);
         return hipGetLastError();
     }
-    const int ntn = (N + BN - 1) / BN, ntm = (M + BM - 1) / BM;
+    const int ntn = (N + SP_BN - 1) / SP_BN;
     const long cus = device_cu_count();
-    GemmArgs g{P.hi, P.lo, P.shi, P.slo, P.escale, w, row_bytes(type, K), y, M, N, K, 1};
-    if ((long)ntn * ntm < cus || N >= 8192) {
-        // fewer 128-token tiles than CUs, or wide weights: 64-token tiles (two
-        // workgroups per CU), and when even those leave CUs idle, K split over
-        // two workgroups that add into a zeroed y (two fp32 additions onto 0
-        // give the same sum in either order). Measured: Q4_K 4096 x 4096, M 512:
-        // 130 -> 80 us; 14336 x 4096, M 2048: 615 -> 598 us (4096 x 4096, M 2048:
-        // no difference).
-        const long t64 = (long)ntn * ((M + 63) / 64);
-        g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
-        if (g.ksplit == 2) {
-            const size_t n4 = (size_t)M * N;
-            hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
-        }
-        hipLaunchKernelGGL(gemm_q4k_m64, dim3((unsigned)(t64 * g.ksplit)), dim3(256), GEMM64_LDS, st, g, ntn);
-        return hipGetLastError();
+    SpArgs g{P.hi, reinterpret_cast<const uint8_t*>(P.lo), P.shi, P.slo, P.escale, w, row_bytes(type, K), y,
+             M, N, K, 1, ntn, 0};
+    // 128-token tiles; 64-token ones when those leave CUs idle, and then K
+    // split over two workgroups that add into a zeroed y (two fp32
+    // additions onto 0 give the same sum in either order)
+    const long t128 = (long)ntn * ((M + 127) / 128);
+    if (t128 >= cus) return launch_sp<4>(g, st);
+    const long t64 = (long)ntn * ((M + 63) / 64);
+    g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
+    if (g.ksplit == 2) {
+        const size_t n4 = (size_t)M * N;
+        hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
     }
-    hipLaunchKernelGGL((gemm_q4k_kernel<8, 2>), dim3((unsigned)(ntn * ntm)), dim3(512), GEMM_LDS, st, g, ntn);
-    return hipGetLastError();
+    return launch_sp<2>(g, st);
 }
 
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
