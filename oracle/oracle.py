@@ -116,8 +116,80 @@ def ref():
         R.ref_dequant.argtypes = [C.c_int, _u8p, C.c_long, _f32p]
         R.ref_xorshift_u32.argtypes = [C.c_uint32, C.c_long, _u32p]
         R.ref_xorshift_float.argtypes = [C.c_uint32, C.c_long, _f32p]
+        vp, cp = C.c_void_p, C.c_char_p
+        R.ref_gguf_new.restype = vp
+        R.ref_gguf_free.argtypes = [vp]
+        R.ref_gguf_kv_u32.argtypes = [vp, cp, C.c_uint32]
+        R.ref_gguf_kv_i32.argtypes = [vp, cp, C.c_int32]
+        R.ref_gguf_kv_f32.argtypes = [vp, cp, C.c_float]
+        R.ref_gguf_kv_bool.argtypes = [vp, cp, C.c_int]
+        R.ref_gguf_kv_str.argtypes = [vp, cp, cp]
+        R.ref_gguf_kv_arr_str.argtypes = [vp, cp, C.POINTER(cp), C.c_long]
+        R.ref_gguf_kv_arr_u8.argtypes = [vp, cp, _u8p, C.c_long]
+        R.ref_gguf_kv_arr_i16.argtypes = [vp, cp, _i16p, C.c_long]
+        R.ref_gguf_kv_arr_bool.argtypes = [vp, cp, _u8p, C.c_long]
+        R.ref_gguf_kv_arr_i32.argtypes = [vp, cp, _i32p, C.c_long]
+        R.ref_gguf_add_tensor.argtypes = [vp, cp, C.POINTER(C.c_uint64), C.c_int, C.c_uint32, _u8p, C.c_long]
+        R.ref_gguf_write.restype = C.c_int
+        R.ref_gguf_write.argtypes = [vp, cp, C.c_long]
         _ref = R
     return _ref
+
+
+class RefGGUFWriter:
+    """The reference's GGUF test-file writer (tests/gguf_writer.h, compiled
+    into oracle/_ref): metadata and tensors are handed to it one by one, and
+    it writes the file exactly as the reference's tests do (GGUF v3, tensor
+    data 32-byte aligned)."""
+
+    def __init__(self):
+        self.R = ref()
+        self.h = self.R.ref_gguf_new()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.R.ref_gguf_free(self.h)
+            self.h = None
+
+    def kv(self, kind: str, key: str, value):
+        k = key.encode()
+        R, h = self.R, self.h
+        if kind == "u32":
+            R.ref_gguf_kv_u32(h, k, value)
+        elif kind == "i32":
+            R.ref_gguf_kv_i32(h, k, value)
+        elif kind == "f32":
+            R.ref_gguf_kv_f32(h, k, value)
+        elif kind == "bool":
+            R.ref_gguf_kv_bool(h, k, 1 if value else 0)
+        elif kind == "str":
+            R.ref_gguf_kv_str(h, k, value.encode())
+        elif kind == "arr_str":
+            arr = (C.c_char_p * len(value))(*[v.encode() for v in value])
+            R.ref_gguf_kv_arr_str(h, k, arr, len(value))
+        elif kind == "arr_u8":
+            a = np.ascontiguousarray(value, np.uint8)
+            R.ref_gguf_kv_arr_u8(h, k, a, a.size)
+        elif kind == "arr_i16":
+            a = np.ascontiguousarray(value, np.int16)
+            R.ref_gguf_kv_arr_i16(h, k, a, a.size)
+        elif kind == "arr_bool":
+            a = np.ascontiguousarray(value, np.uint8)
+            R.ref_gguf_kv_arr_bool(h, k, a, a.size)
+        elif kind == "arr_i32":
+            a = np.ascontiguousarray(value, np.int32)
+            R.ref_gguf_kv_arr_i32(h, k, a, a.size)
+        else:
+            raise ValueError(kind)
+
+    def tensor(self, name: str, dims, type_: int, data: np.ndarray):
+        d = (C.c_uint64 * len(dims))(*dims)
+        a = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        self.R.ref_gguf_add_tensor(self.h, name.encode(), d, len(dims), type_, a, a.size)
+
+    def write(self, path: str, truncate: int = 0):
+        if self.R.ref_gguf_write(self.h, path.encode(), truncate):
+            raise OSError(f"reference writer failed on {path}")
 
 
 # --------------------------------------------------------------------------

@@ -80,23 +80,46 @@ def test_version_2_and_default_alignment(tmp_path):
         assert g.version == 2 and g.alignment == 32 and "general.alignment" not in g.metadata
 
 
-@pytest.mark.gpu
-def test_registered_file_matmul(tmp_path, orc):
-    """The reference's flow: mmap the GGUF, register the data region once,
-    then call the back-end with host weight pointers into the mapping."""
-    from hip_util import synth_weights, synth_x
-    from laplace_amd._lib import lib
+REF_FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_writer_weights.gguf")
+
+
+def _own_writer_file(tmp_path):
+    from hip_util import synth_weights
     K, N = 1024, 96
     ws = [("q4k", Q4_K, synth_weights(Q4_K, K, N, seed=1)), ("q6k", Q6_K, synth_weights(Q6_K, K, N, seed=2)),
           ("q80", Q8_0, synth_weights(Q8_0, K, N, seed=3))]
     p = str(tmp_path / "w.gguf")
     write_gguf(p, [(n, t, (K, N), w) for n, t, w in ws], {"general.architecture": "test"})
-    x = synth_x(3, K, seed=4)
+    return p
+
+
+def test_reference_fixture_reads():
+    """The committed fixture written by the reference's writer
+    (tests/golden/make_gguf_fixture.py) parses: three K 1024 x N 32 tensors."""
+    with GGUFFile(REF_FIXTURE) as g:
+        assert g.version == 3 and g.metadata["general.architecture"] == "laplace-test"
+        assert {n: (t.type, t.dims) for n, t in g.tensors.items()} == {
+            "w.q4k": (Q4_K, (1024, 32)), "w.q6k": (Q6_K, (1024, 32)), "w.q80": (Q8_0, (1024, 32))}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["own_writer", "reference_writer"])
+def test_registered_file_matmul(tmp_path, orc, which):
+    """The reference's flow: mmap the GGUF, register the data region once,
+    then call the back-end with host weight pointers into the mapping. Run
+    on a file from write_gguf and on the committed fixture written by the
+    reference's own writer (tests/gguf_writer.h)."""
+    from hip_util import synth_x
+    from laplace_amd._lib import lib
+    p = _own_writer_file(tmp_path) if which == "own_writer" else REF_FIXTURE
     with GGUFFile(p) as g:
+        K = next(iter(g.tensors.values())).dims[0]
+        x = synth_x(3, K, seed=4)
         g.register()
-        for name, t, w in ws:
-            wt = g.tensors[name].data
+        for name, gt in g.tensors.items():
+            t, N = gt.type, gt.dims[1]
+            wt = gt.data
             y = np.zeros((3, N), np.float32)
             assert lib().lp_gemm(x.ctypes.data, wt.ctypes.data, t, y.ctypes.data, 3, K, N), lib().lp_last_error()
-            ref = orc.gemm_int(t, x, w, N)
-            assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
+            ref = orc.gemm_int(t, x, np.array(wt), N)
+            assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max(), name
