@@ -126,6 +126,16 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
 int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
                   void* stream);
 
+/* lp_gemm_dev without a workspace argument: the workspace is a static
+ * device array of the library (8 MiB per device), so the call allocates
+ * nothing, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. Shapes whose workspace (lp_act_workspace_bytes(M, K))
+ * exceeds 8 MiB return LP_EINVAL. Calls that overlap on one device race on
+ * the shared array; serialise them (one stream, or events). */
+int lp_gemm_dev_noalloc(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                        void* stream);
+
 /* Per-sub-block int32 dots through the GEMV decoders (test hook):
  * out[(m*N + j)*S + s], S = K/32 (K/16 for Q6_K). */
 int lp_block_sums_dev(const void* ws, const uint8_t* w, uint32_t type, int32_t* out, int M,

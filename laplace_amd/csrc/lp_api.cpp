@@ -1003,6 +1003,55 @@ int lp_dequantize(const uint8_t* w, uint32_t type, float* dst, long n) {
     return LP_OK;
 }
 
+// ---- the entry point that allocates nothing -------------------------------
+// lp_gemm_dev with its workspace in a file-scope device array instead of a
+// caller buffer. Each device holds its own copy of the array; its device
+// address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and kept. In host code `scratch` only names the symbol:
+// kernels get the looked-up address. Nothing in the scratch needs to start
+// at zero (the quantizer writes every activation block and plane the
+// products read), and calls that overlap on one device race on it.
+constexpr size_t kNoAllocScratch = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratch];
+static std::mutex g_scratch_mtx;
+static void* g_scratch_dev[64];
+
+static int scratch_ptr(void** out) {
+    int dev = 0;
+    LP_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) {
+        set_err("device ordinal %d out of range", dev);
+        return LP_ENODEV;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mtx);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_err("hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return LP_EHIP;
+        }
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return LP_OK;
+}
+
+int lp_gemm_dev_noalloc(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
+                        void* stream) {
+    int rc = check_shape(type, w, M, K, N);
+    if (rc != LP_OK) return rc;
+    const size_t need = fact_type(type) ? 0 : ws_bytes(M, K);
+    if (need > kNoAllocScratch) {
+        set_err("M=%d K=%d needs %zu bytes of workspace; the no-alloc scratch holds %zu (use lp_gemm_dev)",
+                M, K, need, kNoAllocScratch);
+        return LP_EINVAL;
+    }
+    void* ws = nullptr;
+    if ((rc = scratch_ptr(&ws)) != LP_OK) return rc;
+    return lp_gemm_dev(x, w, type, y, M, K, N, ws, kNoAllocScratch, stream);
+}
+
 const char* lp_last_error(void) { return g_err; }
 
 int lp_device_ok(void) { return dev_info().ok ? 1 : 0; }
