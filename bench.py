@@ -129,7 +129,58 @@ class Gpu:
         return out
 
 
-def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
+# (grid, block, loads in flight per thread); (224, 1024, 9) is the GEMV's own
+# shape at 14336 x 4096 (224 workgroups of 16 waves, 9 x 16 B per lane)
+READ_PROBE_SHAPES = [(224, 1024, 9), (256, 1024, 9), (512, 1024, 4), (1024, 512, 4), (2048, 256, 4),
+                     (2048, 1024, 1), (4096, 512, 1), (8192, 256, 1), (16384, 128, 1), (32768, 64, 1)]
+
+
+def measure_read_ceiling(g: Gpu, bufs, nbytes, reps, wreps):
+    """The part's streaming-read ceiling for this byte count: the
+    lp_read_probe_dev kernel over the same rotating weight copies, graph-
+    timed like the GEMV kernel, best of READ_PROBE_SHAPES (grid, block,
+    loads in flight per thread)."""
+    torch = g.torch
+    sink = torch.zeros(4, dtype=torch.int32, device=g.dev)
+    ncp = len(bufs)
+    nb = nbytes - nbytes % 16
+    res = []
+    for (grid, block, unroll) in READ_PROBE_SHAPES:
+        def launch(i):
+            g.check(g.L.lp_read_probe_dev(bufs[i % ncp].data_ptr(), nb, grid, block, unroll, sink.data_ptr(),
+                                          g.stream()), "lp_read_probe_dev")
+        launch(0)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            launch(1)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(ncp):
+                launch(i)
+        for _ in range(wreps):
+            gr.replay()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(reps):
+            gr.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / (reps * ncp)
+        res.append((us, grid, block, unroll))
+    us, grid, block, unroll = min(res)
+    return {"us": round(us, 3), "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "best_shape": {"grid": grid, "block": block, "loads_in_flight_per_thread": unroll},
+            "shapes_tried": len(res), "bytes": nb,
+            "all_us": {f"{gr}x{bl}x{un}": round(u, 3) for (u, gr, bl, un) in res}}
+
+
+def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False):
     """Time quantize+GEMV steps over rotating weight copies; time the GEMV
     kernel alone with HIP events. Returns a dict of figures."""
     torch = g.torch
@@ -224,7 +275,12 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0):
     us_kernel = ev0.elapsed_time(ev1) * 1e3 / (kreps * ncp)
     kernel_launches = kreps * ncp
 
+    ceiling = None
+    if read_ceiling:
+        ceiling = measure_read_ceiling(g, ws_list, int(w.nbytes), kreps, wreps)
+
     return {
+        "read_ceiling": ceiling,
         "type": TNAME[t], "N": N, "K": K, "M": M,
         "alg_bytes": alg_bytes, "weight_bytes": int(w.nbytes),
         "copies": ncp, "rotation_bytes": int(w.nbytes) * ncp,
@@ -664,7 +720,7 @@ def main():
         g.torch.cuda.synchronize()
         del a, b
     t, N, K, M = Q4_K, 14336, 4096, 1
-    r = measure_gemv(g, t, N, K, M, args.steps, args.warmup)
+    r = measure_gemv(g, t, N, K, M, args.steps, args.warmup, read_ceiling=True)
     name = "q4k_gemv_14336x4096_m1"
     achieved = r["gbs_gemv"]
     out = {
@@ -689,6 +745,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(name),
                      "kernel_launches_timed": r["kernel_launches"],
+                     "read_ceiling": r["read_ceiling"],
+                     "frac_of_read_ceiling": round(r["read_ceiling"]["us"] / r["us_gemv"], 4),
                      "kernel": "gemv_q4k_sb (quantize fused, one launch per step)" if r["fused"]
                      else "gemv_kernel<Q4_K,M=1>", "us_per_launch": round(r["us_gemv"], 3)},
     }

@@ -221,6 +221,15 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
 
 /* ---- diagnostics ----------------------------------------------------------- */
 
+/* Measurement hook, no reference counterpart: streams `bytes` (a multiple
+ * of 16) from device memory with `grid` x `block` threads and `unroll`
+ * (1, 4 or 9) independent 16-byte non-temporal loads in flight per thread,
+ * the GEMV's load form; `sink` (4 bytes of device memory) is written only on
+ * an impossible checksum. Its time per launch is the read ceiling the
+ * weight-streaming kernels are compared with (bench.py's roofline field). */
+int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
+                      void* stream);
+
 /* Text of the last error on this thread ("" if none). */
 const char* lp_last_error(void);
 /* 1 if the current device is usable (gfx950), 0 otherwise. */

@@ -52,6 +52,7 @@ SIGNATURES = {
     "lp_gemm_batch": (_b, [C.POINTER(BatchSpec), _i]),
     "lp_gemm_batch_workspace_bytes": (_sz, [C.POINTER(BatchSpec), _i]),
     "lp_gemm_batch_dev": (_i, [C.POINTER(BatchSpec), _i, _vp, _sz, _vp]),
+    "lp_read_probe_dev": (_i, [_vp, _sz, _i, _i, _i, _vp, _vp]),
     "lp_last_error": (C.c_char_p, []),
     "lp_device_ok": (_i, []),
 }

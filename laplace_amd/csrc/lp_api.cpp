@@ -1052,6 +1052,16 @@ int lp_gemm_dev_noalloc(const float* x, const uint8_t* w, uint32_t type, float* 
     return lp_gemm_dev(x, w, type, y, M, K, N, ws, kNoAllocScratch, stream);
 }
 
+int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
+                      void* stream) {
+    if (!buf || !sink) {
+        set_err("null pointer");
+        return LP_EINVAL;
+    }
+    LP_HIP(launch_read_probe(buf, bytes, grid, block, unroll, sink, static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
 const char* lp_last_error(void) { return g_err; }
 
 int lp_device_ok(void) { return dev_info().ok ? 1 : 0; }

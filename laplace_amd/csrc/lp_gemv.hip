@@ -1546,3 +1546,45 @@ hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, 
 }
 
 }  // namespace lp
+
+namespace lp {
+
+// ---------------------------------------------------------------------------
+// Streaming-read probe: reads `n16` 16-byte pieces with U independent
+// non-temporal loads in flight per thread (the GEMV's load form) and keeps
+// them live with a checksum that is stored only on an impossible value. It
+// measures what the part delivers for a given byte count and launch shape,
+// the ceiling the weight-streaming kernels are compared with.
+template <int U>
+__global__ void __launch_bounds__(1024) read_probe_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                          uint32_t* __restrict__ sink) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4 acc = {0, 0, 0, 0};
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) v[k] = ld_nt16(p + i + k * stride);
+#pragma unroll
+        for (int k = 0; k < U; k++) acc ^= v[k];
+    }
+    for (; i < n16; i += stride) acc ^= ld_nt16(p + i);
+    const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (r == 0x9E3779B9u && threadIdx.x == 0x3ff) sink[0] = r;
+}
+
+hipError_t launch_read_probe(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
+                             hipStream_t st) {
+    if (grid < 1 || block < 64 || block > 1024 || block % 64 || bytes % 16) return hipErrorInvalidValue;
+    const size_t n16 = bytes / 16;
+    const u32x4* p = static_cast<const u32x4*>(buf);
+    switch (unroll) {
+        case 1: hipLaunchKernelGGL(read_probe_kernel<1>, dim3(grid), dim3(block), 0, st, p, n16, sink); break;
+        case 4: hipLaunchKernelGGL(read_probe_kernel<4>, dim3(grid), dim3(block), 0, st, p, n16, sink); break;
+        case 9: hipLaunchKernelGGL(read_probe_kernel<9>, dim3(grid), dim3(block), 0, st, p, n16, sink); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lp

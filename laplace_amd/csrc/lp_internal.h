@@ -117,6 +117,9 @@ hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActV
 int dequant_block_elems(uint32_t type);
 size_t dequant_src_bytes(uint32_t type, long n);
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, hipStream_t st);
+// streaming-read probe (measurement): unroll in {1, 4, 9}
+hipError_t launch_read_probe(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
+                             hipStream_t st);
 hipError_t launch_block_sums(uint32_t type, const uint8_t* w, const ActView& A, int32_t* out,
                              int M, int K, int N, hipStream_t st);
 
