@@ -231,7 +231,7 @@ __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
 // Per super-block: acc += d_n * 2^-7 * main - dmin_n * sum_b m_nb * xs_mb
 // (the min term: xs split into fp16 hi/lo against the exact 6-bit m).
 //
-// Workgroup = 8 waves, tile 32*TT tokens x 256 weight rows; wave w owns
+// Workgroup = NW waves, tile 32*TT tokens x 32*NW weight rows; wave w owns
 // every token of the tile and weight rows w*32 .. +32: TT MFMA tiles of
 // 32 x 32 (A = activations, B = weights; D lane = weight row, 16 tokens).
 // One decoded weight tile feeds TT token tiles, so the VALU work per MFMA
@@ -241,8 +241,11 @@ __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
 // Per K step the hi plane (128 B per token), the lo plane (64 B per token)
 // and the weight codes (32 B per row) are copied into LDS with
 // buffer_load_dwordx4 ... lds (1 KiB per wave instruction; scalar per-step
-// offsets), three stages in flight; headers and activation sums once per
-// super-block, double-buffered.
+// offsets), NS stages in flight; headers and activation sums once per
+// super-block, double-buffered. Large shapes run 4-wave workgroups of 128 x
+// 128 with two stages, two workgroups per CU: each waits at its own barrier,
+// so one workgroup's MFMAs fill the other's copy and barrier stalls (8 % faster
+// than one 8-wave workgroup of 128 x 256 with three stages).
 //
 // LDS layouts (per stage):
 //   hi:    token row r at r*128; its eight 16-byte pieces (piece p holds the
@@ -258,19 +261,22 @@ __device__ __forceinline__ h8 min_codes(uint32_t hy, uint32_t hz, uint32_t hw) {
 // so lane half g of the fp8 MFMA reads 32 contiguous bytes that pair with
 // the V values it decoded for the four fp16 sub-steps (V8 = their e4m3).
 
-constexpr int SP_BN = 256, SP_NW = 8;
-
-template <int TT>
+// TT: 32-token tiles per wave (the workgroup's tokens); NW: waves (32 weight
+// rows each); NS: copy stages in flight.
+template <int TT, int NW, int NS>
 struct SpCfg {
-    static constexpr int BM = 32 * TT;
-    static constexpr int HI = BM * 128, LO = BM * 64, CODES = SP_BN * 32;
+    static constexpr int BM = 32 * TT, BN = 32 * NW;
+    static constexpr int HI = BM * 128, LO = BM * 64, CODES = BN * 32;
     static constexpr int STAGE = HI + LO + CODES;
-    static constexpr int HDR = SP_BN * 16, XS = BM * 16;
+    static constexpr int HDR = BN * 16, XS = BM * 16;
     static constexpr int SBUF = HDR + 2 * XS;
-    static constexpr int LDS = 3 * STAGE + 2 * SBUF;
+    static constexpr int LDS = NS * STAGE + 2 * SBUF;
     static constexpr int N_HI = HI / 1024, N_LO = LO / 1024, N_CODES = CODES / 1024;
-    static constexpr int NX = 2 * XS / 1024;          // activation-sum copies per super-block
-    static_assert(N_HI % SP_NW == 0 && N_CODES == SP_NW && N_LO <= SP_NW && NX <= 4, "copy split");
+    static constexpr int N_HDR = HDR / 1024, N_SB = N_HDR + 2 * XS / 1024;   // per super-block
+    static constexpr int H = N_HI / NW;                                      // hi copies per wave
+    static constexpr int LW = (N_LO + NW - 1) / NW, SBW = (N_SB + NW - 1) / NW;
+    static_assert(N_HI % NW == 0 && N_CODES == NW && N_HDR >= 1 && XS % 1024 == 0, "copy split");
+    static_assert(NS == 2 || NS == 3, "two or three stages");
 };
 
 struct SpArgs {
@@ -290,48 +296,50 @@ struct SpArgs {
 };
 
 // Per-lane copy sources of one wave, fixed for the whole tile; a K step
-// changes only the scalar offset. Every wave issues N_HI/8 hi copies and one
-// code copy per K step; waves below N_LO one lo copy; per super-block waves
-// 0..3 one header copy and waves 4.. one activation-sum copy. Rows past M
-// or N are clamped to the last one (their results are not stored).
-template <int TT>
+// changes only the scalar offset. Every wave issues H hi copies and one code
+// copy per K step; lo copies and the per-super-block copies (headers, then
+// the two activation-sum planes) are dealt round-robin over the waves, with
+// wave-uniform flags. Rows past M or N are clamped to the last one (their
+// results are not stored).
+template <int TT, int NW, int NS>
 struct SpPlan {
-    using Cf = SpCfg<TT>;
-    static constexpr int H = Cf::N_HI / SP_NW;
-    Rsrc rs_hi, rs_lo, rs_w, rs_xs;
-    uint32_t hi_off[H], hi_lds[H], lo_off, lo_lds, c_off, c_lds, h_off, h_lds, x_off, x_lds;
-    int has_lo, has_h, has_x;         // wave-uniform
+    using Cf = SpCfg<TT, NW, NS>;
+    Rsrc rs_hi, rs_lo, rs_w, rs_sb[Cf::SBW];
+    uint32_t hi_off[Cf::H], hi_lds[Cf::H], lo_off[Cf::LW], lo_lds[Cf::LW], c_off, c_lds;
+    uint32_t sb_off[Cf::SBW], sb_lds[Cf::SBW];
+    int has_lo[Cf::LW], sb_kind[Cf::SBW];   // sb_kind: 0 header, 1 activation sums, -1 none
 };
 
-template <int TT>
-__device__ __forceinline__ SpPlan<TT> sp_plan(const SpArgs& g, int m0, int n0, int wave, int lane) {
-    using Cf = SpCfg<TT>;
-    using P = SpPlan<TT>;
-    P d;
+template <int TT, int NW, int NS>
+__device__ __forceinline__ SpPlan<TT, NW, NS> sp_plan(const SpArgs& g, int m0, int n0, int wave, int lane) {
+    using Cf = SpCfg<TT, NW, NS>;
+    SpPlan<TT, NW, NS> d;
     const int mt = g.M - m0 < Cf::BM ? g.M - m0 : Cf::BM;
-    const int nt = g.N - n0 < SP_BN ? g.N - n0 : SP_BN;
+    const int nt = g.N - n0 < Cf::BN ? g.N - n0 : Cf::BN;
     const int nbk = g.K >> 5;
     d.rs_hi = make_rsrc(g.hi + (size_t)m0 * g.K, (uint32_t)mt * (uint32_t)g.K * 2);
     d.rs_lo = make_rsrc(g.lo + (size_t)m0 * g.K, (uint32_t)mt * (uint32_t)g.K);
     d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
 #pragma unroll
-    for (int i = 0; i < P::H; i++) {
-        const int j = wave * P::H + i;
+    for (int i = 0; i < Cf::H; i++) {
+        const int j = wave * Cf::H + i;
         const int row = 8 * j + (lane >> 3);
         const int piece = (lane & 7) ^ ((row >> 1) & 7);
         const int r = row < mt ? row : mt - 1;
         d.hi_off[i] = (uint32_t)r * (uint32_t)g.K * 2 + (uint32_t)piece * 16;
         d.hi_lds[i] = (uint32_t)j * 1024;
     }
-    d.has_lo = wave < Cf::N_LO;
-    {
-        const int o = 1024 * (wave % Cf::N_LO) + 16 * lane;
+#pragma unroll
+    for (int i = 0; i < Cf::LW; i++) {
+        const int j = i * NW + wave;
+        d.has_lo[i] = j < Cf::N_LO;
+        const int o = 1024 * (j < Cf::N_LO ? j : 0) + 16 * lane;
         const int gh = o / (Cf::BM * 32), rem = o % (Cf::BM * 32);
         const int row = rem >> 5, slot = (rem >> 4) & 1;
         const int h = slot ^ ((row >> 3) & 1);
         const int r = row < mt ? row : mt - 1;
-        d.lo_off = (uint32_t)r * (uint32_t)g.K + (uint32_t)(32 * gh + 16 * h);
-        d.lo_lds = Cf::HI + (uint32_t)o;
+        d.lo_off[i] = (uint32_t)r * (uint32_t)g.K + (uint32_t)(32 * gh + 16 * h);
+        d.lo_lds[i] = Cf::HI + (uint32_t)o;
     }
     {
         int r = 32 * wave + (lane & 31);
@@ -339,50 +347,60 @@ __device__ __forceinline__ SpPlan<TT> sp_plan(const SpArgs& g, int m0, int n0, i
         d.c_off = (uint32_t)((size_t)r * g.rb) + 16 + 16 * (lane >> 5);
         d.c_lds = Cf::HI + Cf::LO + (uint32_t)wave * 1024;
     }
-    d.has_h = wave < 4;
-    {
-        int r = 64 * (wave & 3) + lane;
-        r = r < nt ? r : nt - 1;
-        d.h_off = (uint32_t)((size_t)r * g.rb);
-        d.h_lds = (uint32_t)(wave & 3) * 1024;
-    }
-    const int xw = wave - 4;
-    d.has_x = xw >= 0 && xw < Cf::NX;
-    {
-        const int q = xw < 0 ? 0 : xw;
-        const int per = Cf::XS / 1024 > 0 ? Cf::XS / 1024 : 1;
-        const int pl = q / per, part = q % per;
-        int r = 64 * part + lane;
-        r = r < mt ? r : mt - 1;
-        d.rs_xs = make_rsrc((pl ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
-        d.x_off = (uint32_t)(r * nbk * 2);
-        d.x_lds = Cf::HDR + pl * Cf::XS + part * 1024;
+#pragma unroll
+    for (int i = 0; i < Cf::SBW; i++) {
+        const int j = i * NW + wave;
+        d.sb_kind[i] = -1;
+        d.rs_sb[i] = d.rs_w;
+        d.sb_off[i] = 0;
+        d.sb_lds[i] = 0;
+        if (j < Cf::N_HDR) {
+            int r = 64 * j + lane;
+            r = r < nt ? r : nt - 1;
+            d.sb_kind[i] = 0;
+            d.sb_off[i] = (uint32_t)((size_t)r * g.rb);
+            d.sb_lds[i] = (uint32_t)j * 1024;
+        } else if (j < Cf::N_SB) {
+            const int q = j - Cf::N_HDR, per = Cf::XS / 1024;
+            const int pl = q / per, part = q % per;
+            int r = 64 * part + lane;
+            r = r < mt ? r : mt - 1;
+            d.sb_kind[i] = 1;
+            d.rs_sb[i] = make_rsrc((pl ? g.slo : g.shi) + (size_t)m0 * nbk, (uint32_t)(mt * nbk * 2));
+            d.sb_off[i] = (uint32_t)(r * nbk * 2);
+            d.sb_lds[i] = Cf::HDR + pl * Cf::XS + part * 1024;
+        }
     }
     return d;
 }
 
 // Copies of K step kt into stage `st` (+ super-block data into `sbb` when kt
 // starts a super-block). Returns the number of copies issued.
-template <int TT>
-__device__ __forceinline__ int sp_issue(const SpPlan<TT>& d, int kt, uint8_t* st, uint8_t* sbb) {
-    using P = SpPlan<TT>;
+template <int TT, int NW, int NS>
+__device__ __forceinline__ int sp_issue(const SpPlan<TT, NW, NS>& d, int kt, uint8_t* st, uint8_t* sbb) {
+    using Cf = SpCfg<TT, NW, NS>;
     const int sb = kt >> 2, jb = kt & 3;
 #pragma unroll
-    for (int i = 0; i < P::H; i++) dma16(d.rs_hi, d.hi_off[i], (uint32_t)(kt * 128), st + d.hi_lds[i]);
+    for (int i = 0; i < Cf::H; i++) dma16(d.rs_hi, d.hi_off[i], (uint32_t)(kt * 128), st + d.hi_lds[i]);
     dma16(d.rs_w, d.c_off, (uint32_t)(sb * 144 + 32 * jb), st + d.c_lds);
-    int n = P::H + 1;
-    if (d.has_lo) {
-        dma16(d.rs_lo, d.lo_off, (uint32_t)(kt * 64), st + d.lo_lds);
-        n++;
-    }
-    if (jb == 0) {
-        if (d.has_h) {
-            dma16(d.rs_w, d.h_off, (uint32_t)(sb * 144), sbb + d.h_lds);
+    int n = Cf::H + 1;
+#pragma unroll
+    for (int i = 0; i < Cf::LW; i++) {
+        if (d.has_lo[i]) {
+            dma16(d.rs_lo, d.lo_off[i], (uint32_t)(kt * 64), st + d.lo_lds[i]);
             n++;
         }
-        if (d.has_x) {
-            dma16(d.rs_xs, d.x_off, (uint32_t)(sb * 16), sbb + d.x_lds);
-            n++;
+    }
+    if (jb == 0) {
+#pragma unroll
+        for (int i = 0; i < Cf::SBW; i++) {
+            if (d.sb_kind[i] == 0) {
+                dma16(d.rs_sb[i], d.sb_off[i], (uint32_t)(sb * 144), sbb + d.sb_lds[i]);
+                n++;
+            } else if (d.sb_kind[i] == 1) {
+                dma16(d.rs_sb[i], d.sb_off[i], (uint32_t)(sb * 16), sbb + d.sb_lds[i]);
+                n++;
+            }
         }
     }
     return n;
@@ -457,10 +475,10 @@ __device__ __forceinline__ void sp_tile(int lin, int ntm, int ntn, int& tm, int&
     tn = in / gm;
 }
 
-template <int TT>
-__global__ void __launch_bounds__(64 * SP_NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int TT, int NW, int NS>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_q4k_sp(SpArgs g) {
-    using C = SpCfg<TT>;
+    using C = SpCfg<TT, NW, NS>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -472,13 +490,13 @@ gemm_q4k_sp(SpArgs g) {
     const int tile = lin / g.ksplit, part = lin % g.ksplit;
     int tm, tn;
     sp_tile(tile, g.ntiles / g.ntn, g.ntn, tm, tn);
-    const int m0 = tm * C::BM, n0 = tn * SP_BN;
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int nsb_all = g.K >> 8;
     const int sb_beg = part * nsb_all / g.ksplit, sb_end = (part + 1) * nsb_all / g.ksplit;
     const int kt0 = 4 * sb_beg, nk = 4 * sb_end;
-    const SpPlan<TT> plan = sp_plan<TT>(g, m0, n0, wave, lane);
+    const SpPlan<TT, NW, NS> plan = sp_plan<TT, NW, NS>(g, m0, n0, wave, lane);
     auto stage = [&](int i) { return smem + i * C::STAGE; };
-    auto sbuf = [&](int i) { return smem + 3 * C::STAGE + i * C::SBUF; };
+    auto sbuf = [&](int i) { return smem + NS * C::STAGE + i * C::SBUF; };
 
     const uint32_t lds0 = lds_addr(smem);
     const int gl = lane >> 5, r32 = lane & 31;
@@ -494,8 +512,8 @@ gemm_q4k_sp(SpArgs g) {
     }
     // this wave's weight rows: wave*32 + lane%32 (code group `wave`)
     const uint32_t b_base = lds0 + C::HI + C::LO + wave * 1024 + (lane & 31) * 16 + 8 * gl;
-    const uint32_t hdr_base = lds0 + 3 * C::STAGE + (wave * 32 + (lane & 31)) * 16;
-    const uint32_t xs_base = lds0 + 3 * C::STAGE + C::HDR + (lane & 31) * 16;
+    const uint32_t hdr_base = lds0 + NS * C::STAGE + (wave * 32 + (lane & 31)) * 16;
+    const uint32_t xs_base = lds0 + NS * C::STAGE + C::HDR + (lane & 31) * 16;
 
     f16v acc[TT], main_[TT];
 #pragma unroll
@@ -506,22 +524,25 @@ gemm_q4k_sp(SpArgs g) {
     uint32_t hy = 0, hz = 0, hw = 0;
     float dsc = 0.0f, dmn = 0.0f;
 
-    int cnt_next = 0;                                 // copies of step kt+1
-    (void)sp_issue<TT>(plan, kt0, stage(0), sbuf(sb_beg & 1));
-    cnt_next = sp_issue<TT>(plan, kt0 + 1, stage(1), sbuf(sb_beg & 1));
+    // NS stages: steps kt+1 .. kt+NS-2 are in flight while step kt is
+    // computed; cnt_next counts the copies of step kt+1 (three stages)
+    int cnt_next = 0;
+    (void)sp_issue<TT, NW, NS>(plan, kt0, stage(0), sbuf(sb_beg & 1));
+    if (NS == 3 && kt0 + 1 < nk) cnt_next = sp_issue<TT, NW, NS>(plan, kt0 + 1, stage(1), sbuf(sb_beg & 1));
     for (int sb = sb_beg; sb < sb_end; sb++) {
         const uint32_t sb_off = (uint32_t)((sb & 1) * C::SBUF);
 #pragma unroll
         for (int jb = 0; jb < 4; jb++) {
             const int kt = 4 * sb + jb;
-            wait_dma(cnt_next);                       // step kt has landed
+            wait_dma(NS == 3 ? cnt_next : 0);         // step kt has landed
             // after this barrier every wave has finished step kt-1, whose
-            // stage buffer is the one step kt+2 is copied into
+            // stage buffer is the one step kt+NS-1 is copied into
             __builtin_amdgcn_s_barrier();
             cnt_next = 0;
-            if (kt + 2 < nk)
-                cnt_next = sp_issue<TT>(plan, kt + 2, stage((kt + 2 - kt0) % 3), sbuf(((kt + 2) >> 2) & 1));
-            const uint32_t st_off = (uint32_t)(((kt - kt0) % 3) * C::STAGE);
+            if (kt + NS - 1 < nk)
+                cnt_next = sp_issue<TT, NW, NS>(plan, kt + NS - 1, stage((kt + NS - 1 - kt0) % NS),
+                                                sbuf(((kt + NS - 1) >> 2) & 1));
+            const uint32_t st_off = (uint32_t)(((kt - kt0) % NS) * C::STAGE);
 
             if (jb == 0) {
                 u32x4 h;
@@ -616,7 +637,7 @@ gemm_q4k_sp(SpArgs g) {
     }
 
     // store: D[token][row] -> y[token * N + row] * 2^E_token
-    const int n = n0 + wave * 32 + (lane & 31);
+    const int n = n0 + wave * 32 + (lane & 31);   // D lane = weight row
 #pragma unroll
     for (int tt = 0; tt < TT; tt++)
 #pragma unroll
@@ -1309,11 +1330,13 @@ static hipError_t launch_planes_from_act(const ActView& A, void* planes, int M, 
     return hipGetLastError();
 }
 
-template <int TT>
+template <int TT, int NW, int NS>
 static hipError_t launch_sp(SpArgs g, hipStream_t st) {
-    g.ntiles = g.ntn * ((g.M + SpCfg<TT>::BM - 1) / SpCfg<TT>::BM);
+    using C = SpCfg<TT, NW, NS>;
+    g.ntn = (g.N + C::BN - 1) / C::BN;
+    g.ntiles = g.ntn * ((g.M + C::BM - 1) / C::BM);
     const long nblk = (long)g.ntiles * g.ksplit;
-    hipLaunchKernelGGL((gemm_q4k_sp<TT>), dim3((unsigned)nblk), dim3(64 * SP_NW), SpCfg<TT>::LDS, st, g);
+    hipLaunchKernelGGL((gemm_q4k_sp<TT, NW, NS>), dim3((unsigned)nblk), dim3(64 * NW), C::LDS, st, g);
     return hipGetLastError();
 }
 
@@ -1328,22 +1351,21 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
                            0, st, a);
         return hipGetLastError();
     }
-    const int ntn = (N + SP_BN - 1) / SP_BN;
     const long cus = device_cu_count();
     SpArgs g{P.hi, reinterpret_cast<const uint8_t*>(P.lo), P.shi, P.slo, P.escale, w, row_bytes(type, K), y,
-             M, N, K, 1, ntn, 0};
+             M, N, K, 1, 0, 0};
     // 128-token tiles; 64-token ones when those leave CUs idle, and then K
     // split over two workgroups that add into a zeroed y (two fp32
     // additions onto 0 give the same sum in either order)
-    const long t128 = (long)ntn * ((M + 127) / 128);
-    if (t128 >= cus) return launch_sp<4>(g, st);
-    const long t64 = (long)ntn * ((M + 63) / 64);
+    const long t128 = (long)((N + 255) / 256) * ((M + 127) / 128);
+    if (t128 >= cus) return launch_sp<4, 4, 2>(g, st);
+    const long t64 = (long)((N + 255) / 256) * ((M + 63) / 64);
     g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
     if (g.ksplit == 2) {
         const size_t n4 = (size_t)M * N;
         hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
     }
-    return launch_sp<2>(g, st);
+    return launch_sp<2, 4, 2>(g, st);
 }
 
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
