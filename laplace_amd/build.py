@@ -24,7 +24,7 @@ OBJ = os.path.join(ROOT, "_build", "obj")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_api.cpp"]
+SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_rq.hip", "lp_api.cpp"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
@@ -34,10 +34,15 @@ CFLAGS = [
 ]
 
 
+# Per-source additions. lp_rq.hip: MFMA results in VGPRs (its int8 block sums
+# feed VALU at once; the AGPR form costs a v_accvgpr_read per value).
+SRC_FLAGS = {"lp_rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(OBJ, src.rsplit(".", 1)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-x", "hip", "-c", path, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *SRC_FLAGS.get(src, []), "-x", "hip", "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -129,33 +129,6 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
     }
 }
 
-// Buffer-resource copies straight into LDS: the per-lane byte offset is fixed
-// for the whole tile and a K step only changes the scalar offset, so the copy
-// addresses cost no vector instructions. LDS destination: the wave-uniform
-// base plus 16 bytes per lane.
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
-    // 0x00020000: the raw-buffer configuration word of the gfx9 family
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ void dma16(Rsrc r, uint32_t voff, uint32_t soff, uint8_t* lds) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
-
-
-__device__ __forceinline__ void wait_dma(int outstanding) {
-    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14
-    switch (outstanding) {
-#define LP_W(i) case i: __builtin_amdgcn_s_waitcnt(((i) & 15) | (7 << 4) | (15 << 8) | (((i) >> 4) << 14)); break;
-        LP_W(1) LP_W(2) LP_W(3) LP_W(4) LP_W(5) LP_W(6) LP_W(7) LP_W(8) LP_W(9) LP_W(10) LP_W(11) LP_W(12)
-        LP_W(13) LP_W(14) LP_W(15) LP_W(16) LP_W(17) LP_W(18) LP_W(19) LP_W(20) LP_W(21) LP_W(22) LP_W(23)
-        LP_W(24) LP_W(25) LP_W(26) LP_W(27) LP_W(28) LP_W(29) LP_W(30) LP_W(31) LP_W(32) LP_W(33) LP_W(34)
-        LP_W(35) LP_W(36) LP_W(37) LP_W(38) LP_W(39) LP_W(40)
-#undef LP_W
-        default: __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); break;
-    }
-}
-
 // 8 codes (bytes b0..b7 in u0,u1; nibble half `hi`) -> 8 fp16 V = sc * nibble,
 // in the order b0 b2 b1 b3 b4 b6 b5 b7: masking a dword's nibbles into fp16
 // 1024 + n (or 1024 + 16n) yields bytes 0 and 2 in one step and, after a
@@ -1234,6 +1207,7 @@ hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, f
                             hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
     if (!i8mf_supported(type, M, K, N, w)) return hipErrorInvalidValue;
+    if (rq_preferred(type, M, K, N, w)) return launch_gemv_rq(w, A, y, M, K, N, st);
     const dim3 grid((N + 16 * kMfTiles - 1) / (16 * kMfTiles));
     if (type == T_Q8_0) {
         const size_t shm = (size_t)(K / 32) * 16 * 4;

@@ -1260,6 +1260,9 @@ hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, const float* x, fl
 template <uint32_t T>
 static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y, int M, int K,
                                    int N, hipStream_t st) {
+    if constexpr (T == T_Q4_K) {
+        if (rq_preferred(T, M, K, N, w)) return launch_gemv_rq(w, A, y, M, K, N, st);
+    }
     if constexpr (T == T_Q6_K) {
         if (q6k_sbm_supported(K, M, w)) return launch_q6k_sbm(w, A, y, M, K, N, st);
     }

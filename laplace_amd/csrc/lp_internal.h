@@ -81,6 +81,12 @@ bool gemm_supported(uint32_t type, int M, int K);
 bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
 hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
                             hipStream_t st);
+// Q4_K for 1 <= M <= 8 on 4x4 int8 MFMA blocks, a row quad per wave
+// (lp_rq.hip); K <= 4096. rq_preferred: the shapes where it is the fastest
+// kernel.
+bool rq_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
+bool rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w);
+hipError_t launch_gemv_rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
 size_t gemm_planes_bytes(int M, int K);
 // planes from fp32 x (quantize + planes in one pass)
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st);
