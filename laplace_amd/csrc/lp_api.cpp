@@ -9,6 +9,7 @@
 // by host pointer on first use (after get_weight_buf, src/metal.mm:601-621).
 // Calls are serialised by one mutex, as the Metal back-end does
 // (src/metal.mm:646).
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -364,6 +365,15 @@ static int check_moe(uint32_t type, const void* w, int T, int topk, int E, int K
     return LP_OK;
 }
 
+// Pairs per routed group below the 16-pair MFMA groups: 8 on the row-quad
+// kernel once experts average more than 2 pairs (groups of 4 would split
+// many experts into groups that each read the expert again; measured at 128
+// experts, 64 tokens, top-8: 133 vs 147 us), else 4 on the GEMV kernels
+// (one or two pairs per expert: 39 vs 41 us at one token, 52 vs 58 at four).
+static int moe_group_size(uint32_t type, int K, int P, int E) {
+    return rq_moe_supported(type, K) && P > 2 * E ? kRqMoeGroup : 4;
+}
+
 static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, uint32_t type,
                  float* y, int T, int topk, int E, int K, int N, void* ws, hipStream_t st) {
     const int P = T * topk, rows = multi ? P : T;
@@ -375,7 +385,8 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
     // 236 us); decode-sized batches stay on the GEMV kernels
     const bool mf = moe_mf_supported(type, K) && P > 8 * E;
     LP_HIP(launch_quantize(x, rows, K, A, st));
-    LP_HIP(launch_moe_grouped(type, w, A, mf, rows, idx, P, E, multi, topk, route, y, K, N, st));
+    LP_HIP(launch_moe_grouped(type, w, A, mf ? 16 : moe_group_size(type, K, P, E), rows, idx, P, E, multi, topk,
+                              route, y, K, N, st));
     return LP_OK;
 }
 
@@ -784,11 +795,14 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
         return rc;
     LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
     if (fused) {
-        LP_HIP(launch_moe_route(idx, P, n_exp, f.route, false, st));
-        LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, false, T, P, n_exp, 0, top_k, f.route,
+        // one route table for both products: groups of 8 only if both run on
+        // the row-quad kernel
+        const int gs = std::min(moe_group_size(gate_up_type, H, P, n_exp), moe_group_size(down_type, inter, P, n_exp));
+        LP_HIP(launch_moe_route(idx, P, n_exp, f.route, gs, st));
+        LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, gs, T, P, n_exp, 0, top_k, f.route,
                                          f.gu, H, 2 * inter, st));
         LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, f.hq, st));
-        LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, false, P, P, n_exp, 1, top_k, f.route, f.eo,
+        LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, gs, P, P, n_exp, 1, top_k, f.route, f.eo,
                                          inter, H, st));
     } else {
         if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,

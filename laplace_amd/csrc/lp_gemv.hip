@@ -1452,34 +1452,40 @@ moe_gemv_kernel(const uint8_t* __restrict__ w, size_t rb, ActView A, const uint8
     }
 }
 
-hipError_t launch_moe_route(const int* idx, int P, int E, void* route, bool mf_groups, hipStream_t st) {
+hipError_t launch_moe_route(const int* idx, int P, int E, void* route, int gsize, hipStream_t st) {
     if (P <= 0) return hipSuccess;
-    if (E <= 0 || E > kMoeMaxExperts) return hipErrorInvalidValue;
+    if (E <= 0 || E > kMoeMaxExperts || gsize < kMoeGroup) return hipErrorInvalidValue;
     const int mg = moe_max_groups(P, E);
     const size_t rshm = sizeof(int) * (3 * (size_t)E + 2 * kRouteThreads);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), rshm, st, idx, P, E,
-                       static_cast<uint8_t*>(route), mg, mf_groups ? kMoeGroupMf : kMoeGroup);
+                       static_cast<uint8_t*>(route), mg, gsize);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                               int rows, const int* idx, int P, int E, int multi, int topk, void* route,
                               float* y, int K, int N, hipStream_t st) {
     if (P <= 0 || N <= 0) return hipSuccess;
     if (E <= 0 || E > kMoeMaxExperts || topk <= 0) return hipErrorInvalidValue;
-    const bool mf = mf_groups && moe_mf_supported(type, K);
-    hipError_t e = launch_moe_route(idx, P, E, route, mf, st);
+    hipError_t e = launch_moe_route(idx, P, E, route, gsize, st);
     if (e != hipSuccess) return e;
-    return launch_moe_grouped_routed(type, w, A, mf, rows, P, E, multi, topk, route, y, K, N, st);
+    return launch_moe_grouped_routed(type, w, A, gsize, rows, P, E, multi, topk, route, y, K, N, st);
 }
 
-hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
+hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
                                      int K, int N, hipStream_t st) {
     if (P <= 0 || N <= 0) return hipSuccess;
-    const bool mf = mf_groups && moe_mf_supported(type, K);
     const int mg = moe_max_groups(P, E);
-    if (mf) return launch_moe_i8mf(w, A, route, mg, multi, topk, y, K, N, st);
+    if (gsize == kMoeGroupMf) {
+        if (!moe_mf_supported(type, K)) return hipErrorInvalidValue;
+        return launch_moe_i8mf(w, A, route, mg, multi, topk, y, K, N, st);
+    }
+    if (gsize == kRqMoeGroup) {
+        if (!rq_moe_supported(type, K)) return hipErrorInvalidValue;
+        return launch_moe_rq(w, A, route, mg, gsize, multi, topk, y, K, N, st);
+    }
+    if (gsize != kMoeGroup) return hipErrorInvalidValue;
     if (type == T_Q4_K && sbm_supported(K, w)) {
         SbmArgs args{w, (long)row_bytes(type, K) * N, A, y, K, N, 0, static_cast<const uint8_t*>(route), mg, multi,
                      topk};

@@ -103,21 +103,28 @@ hipError_t launch_moe_i8mf(const uint8_t* w, const ActView& A, const void* route
                            int topk, float* y, int K, int N, hipStream_t st);
 // Grouped MoE dispatch (lp_gemv.hip). P = T * topk pairs, E experts stacked
 // in w (E x N rows). `route` is scratch of moe_route_bytes(P, E) bytes.
-// mf_groups: Q4_K runs on the int8 small-M MFMA kernel in groups of <= 16
-// pairs; otherwise the GEMV kernels read A in groups of <= 4.
+// gsize: pairs per group (the group is the activation-row count of one
+// workgroup): 16 for the 16x16 int8 MFMA kernel (Q4_K), 8 for the row-quad
+// kernel (Q4_K, rq_moe_supported), 4 for the GEMV kernels (any type; Q4_K on
+// the row-quad kernel where supported).
 constexpr int kMoeMaxExperts = 8192;
+constexpr int kRqMoeGroup = 8;
 int moe_max_groups(int P, int E);
 size_t moe_route_bytes(int P, int E);
-hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
+hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                               int rows, const int* idx, int P, int E, int multi, int topk, void* route,
                               float* y, int K, int N, hipStream_t st);
 // The two halves of launch_moe_grouped: the route table of the pairs (groups
-// of <= 16 pairs for the MFMA kernel, mf_groups, else <= 4), and the grouped
-// products on a route table built for the same pairs and group size.
-hipError_t launch_moe_route(const int* idx, int P, int E, void* route, bool mf_groups, hipStream_t st);
-hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, bool mf_groups,
+// of <= gsize pairs), and the grouped products on a route table built for the
+// same pairs and group size.
+hipError_t launch_moe_route(const int* idx, int P, int E, void* route, int gsize, hipStream_t st);
+hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
                                      int K, int N, hipStream_t st);
+// Q4_K MoE groups of <= 8 pairs on the row-quad kernel (lp_rq.hip)
+bool rq_moe_supported(uint32_t type, int K);
+hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, int max_groups, int gsize,
+                         int multi, int topk, float* y, int K, int N, hipStream_t st);
 // dequantize (lp_dequant.hip): elements per block (0 = type not handled)
 // and source bytes of n elements.
 int dequant_block_elems(uint32_t type);

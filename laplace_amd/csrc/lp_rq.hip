@@ -6,11 +6,11 @@
 //   y[m, n] += (d_n * sc_nb) * xd_mb * P  -  (dmin_n * m_nb) * xs_mb
 // with xd / xs the token's block scale and scaled block sum.
 //
-// Layout: a wave owns a row quad (4 consecutive weight rows) at a time, with
-// all of K (K <= 4096: at most 16 super-blocks). Lane l = 4q + j: weight row
-// j of the quad, super-block q. Each lane loads its super-block (144 bytes:
-// header + codes) with nine 16-byte loads; for a fixed row the 16 lanes read
-// 2.3 KB of one row, so an instruction touches 4 row spans.
+// Layout: a wave owns G = 16 / S row quads (4 consecutive weight rows each)
+// at a time, with all of K (K <= 4096: at most 16 super-blocks; S = the
+// super-block count rounded up to a power of two). Lane l = 4q + j: weight
+// row j of row quad q / S, super-block q % S. Each lane loads its
+// super-block (144 bytes: header + codes) with nine 16-byte loads.
 //
 // v_mfma_i32_4x4x4_16b_i8 is 16 independent 4x4x4 products; block q of the
 // instruction is lane quad q (lanes 4q..4q+3): A row i = lane 4q+i, B column
@@ -27,10 +27,14 @@
 // super-block.
 // TG groups of 4 tokens (M <= 4 TG); unused token rows are zero.
 //
-// The partial sums of the 16 super-block lanes of a row are added with
-// cross-lane shuffles (fixed order) when the row quad is done. Each wave
-// handles `per_wave` consecutive row quads; the next quad's loads are issued
-// before the current one is computed.
+// The partial sums of the S super-block lanes of a row are added with
+// cross-lane shuffles (fixed order) when the row quads are done. Each wave
+// handles `per_wave` consecutive units of G row quads; the next unit's loads
+// are issued before the current one is computed.
+// MOE: blockIdx.y is a routed group (expert, first pair, n <= 8 pairs, from
+// the route table of the grouped dispatch): the group's activation rows
+// (token, or pair in the multi form) and output rows (pairs) replace rows
+// 0..M-1, and the weights are the group's expert.
 //
 // LDS (per workgroup): the tokens' codes, token stride = 272 bytes per
 // super-block rounded to 64 mod 256 (lanes 4q+j of a 16-lane read phase then
@@ -53,10 +57,14 @@ struct RqArgs {
     ActView A;
     float* y;
     int M, K, N;
-    long nrq;            // row quads
-    int per_wave;        // row quads per wave
+    long nunits;         // units of G row quads
+    int per_wave;        // units per wave
     int tok_stride;      // LDS bytes per token's codes
     int sc_stride;       // LDS floats per super-block of scales (8 blocks x 4 TG tokens, padded)
+    // MOE
+    const uint8_t* route;
+    long ebytes;         // bytes per expert
+    int max_groups, multi, topk;
 };
 
 struct RqTile {
@@ -64,35 +72,59 @@ struct RqTile {
     u32x4 c[8];          // codes: bytes 16 i .. 16 i + 15
 };
 
-template <int TG>
+template <int TG, int S, bool MOE>
 __global__ void __launch_bounds__(64 * kRqWaves)
 gemv_q4k_rq(RqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int MP = 4 * TG;
-    const int K = a.K, N = a.N, M = a.M;
+    constexpr int G = 16 / S;                 // row quads per wave unit
+    constexpr int L = S == 1 ? 0 : S == 2 ? 1 : S == 4 ? 2 : S == 8 ? 3 : 4;
+    const int K = a.K, N = a.N;
+    int M = a.M;
+    const uint8_t* w = a.w;
+    const int* pairs = nullptr;
+    int first = 0;
+    if constexpr (MOE) {
+        if ((int)blockIdx.y >= *reinterpret_cast<const int*>(a.route)) return;
+        const int4 gd = reinterpret_cast<const int4*>(a.route + 16)[blockIdx.y];
+        pairs = reinterpret_cast<const int*>(a.route + 16 + (size_t)a.max_groups * 16);
+        first = gd.y;
+        M = gd.z;
+        w += (size_t)gd.x * a.ebytes;
+    }
+    auto act_row = [&](int m) -> size_t {
+        if constexpr (MOE) {
+            const int p = pairs[first + m];
+            return (size_t)(a.multi ? p : p / a.topk);
+        } else {
+            return (size_t)m;
+        }
+    };
     const int nsb = K >> 8, nb = K >> 5;
     uint8_t* sq = smem;                                                   // [MP][tok_stride]
     float* sxd = reinterpret_cast<float*>(smem + (size_t)MP * a.tok_stride);   // [nsb][sc_stride]
     float* sxs = sxd + (size_t)nsb * a.sc_stride;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane >> 2, j = lane & 3;
-    const bool qv = q < nsb;
-    const int sbq = qv ? q : nsb - 1;
+    const int sub = q / S, sq_raw = q % S;
+    const bool qv = sq_raw < nsb;
+    const int sbq = qv ? sq_raw : nsb - 1;
+    const int tga = (M + 3) >> 2;             // token groups in use
 
     const long gw = (long)blockIdx.x * kRqWaves + __builtin_amdgcn_readfirstlane(wave);
-    const long rq0 = gw * a.per_wave;
-    const long rq1 = rq0 + a.per_wave < a.nrq ? rq0 + a.per_wave : a.nrq;
-    const uint32_t lane_off = (uint32_t)(j * a.rb + sbq * 144);
+    const long u0 = gw * a.per_wave;
+    const long u1 = u0 + a.per_wave < a.nunits ? u0 + a.per_wave : a.nunits;
+    const uint32_t lane_off = (uint32_t)((4 * sub + j) * a.rb + sbq * 144);
 
-    auto load = [&](long rq, RqTile& t) {
-        // wave-uniform row-quad base; the last quad clamps rows past N
+    auto load = [&](long u, RqTile& t) {
+        // wave-uniform unit base; the last unit clamps rows past N
         const uint8_t* p;
-        if (rq * 4 + 4 <= N) {
-            p = a.w + rq * 4 * a.rb + lane_off;
+        if ((u + 1) * 4 * G <= N) {
+            p = w + u * 4 * G * a.rb + lane_off;
         } else {
-            long row = rq * 4 + j;
+            long row = (u * G + sub) * 4 + j;
             row = row < N ? row : N - 1;
-            p = a.w + row * a.rb + (long)sbq * 144;
+            p = w + row * a.rb + (long)sbq * 144;
         }
         // plain loads: each 128-byte line is read by several of the nine
         // instructions (nontemporal loads measured 1.9x slower)
@@ -102,20 +134,22 @@ gemv_q4k_rq(RqArgs a) {
     };
 
     RqTile ta, tb;
-    if (rq0 < rq1) load(rq0, ta);
+    if (u0 < u1) load(u0, ta);
 
     // stage the tokens' codes and block scales (zero for padding tokens)
-    for (int i = threadIdx.x; i < MP * (K >> 4); i += blockDim.x) {
-        const int m = i / (K >> 4), c = i % (K >> 4);        // 16-byte piece c of token m
+    const int kp = K >> 4;                    // 16-byte pieces per token
+    for (int i = threadIdx.x; i < MP * kp; i += blockDim.x) {
+        const int m = i / kp, c = i - m * kp;
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (m < M) v = reinterpret_cast<const u32x4*>(a.A.qs + (size_t)m * K)[c];
+        if (m < M) v = reinterpret_cast<const u32x4*>(a.A.qs + act_row(m) * K)[c];
         *reinterpret_cast<u32x4*>(sq + (size_t)m * a.tok_stride + (c >> 4) * 272 + (c & 15) * 16) = v;
     }
     for (int i = threadIdx.x; i < MP * nb; i += blockDim.x) {
-        const int m = i / nb, b = i % nb;
+        const int m = i / nb, b = i - m * nb;
         const int o = (b >> 3) * a.sc_stride + (b & 7) * MP + m;
-        sxd[o] = m < M ? a.A.d[(size_t)m * nb + b] : 0.0f;
-        sxs[o] = m < M ? a.A.sum[(size_t)m * nb + b] : 0.0f;
+        const size_t r = m < M ? act_row(m) : 0;
+        sxd[o] = m < M ? a.A.d[r * nb + b] : 0.0f;
+        sxs[o] = m < M ? a.A.sum[r * nb + b] : 0.0f;
     }
     __syncthreads();
 
@@ -125,8 +159,8 @@ gemv_q4k_rq(RqArgs a) {
     const i4v zi = {0, 0, 0, 0};
     const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    // one row quad from its loaded tile
-    auto compute = [&](long rq, const RqTile& T) {
+    // one unit of G row quads from its loaded tile
+    auto compute = [&](long u, const RqTile& T) {
         const u32x4 h = T.h;
         const float d = qv ? fp16_bits_to_f32(h.x) : 0.0f;
         const float dmin = qv ? fp16_bits_to_f32(h.x >> 16) : 0.0f;
@@ -159,64 +193,87 @@ gemv_q4k_rq(RqArgs a) {
             }
 #pragma unroll
             for (int t = 0; t < TG; t++) {
-                const uint8_t* at = aq + (size_t)4 * t * a.tok_stride + 64 * jb;
-                const u32x4 l0 = *reinterpret_cast<const u32x4*>(at);
-                const u32x4 l1 = *reinterpret_cast<const u32x4*>(at + 16);
-                const u32x4 g0 = *reinterpret_cast<const u32x4*>(at + 32);
-                const u32x4 g1 = *reinterpret_cast<const u32x4*>(at + 48);
-                const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-                const uint32_t ah[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-                i4v p0 = zi, p1 = zi;
+                if (t < tga) {
+                    const uint8_t* at = aq + (size_t)4 * t * a.tok_stride + 64 * jb;
+                    const u32x4 l0 = *reinterpret_cast<const u32x4*>(at);
+                    const u32x4 l1 = *reinterpret_cast<const u32x4*>(at + 16);
+                    const u32x4 g0 = *reinterpret_cast<const u32x4*>(at + 32);
+                    const u32x4 g1 = *reinterpret_cast<const u32x4*>(at + 48);
+                    const uint32_t al[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                    const uint32_t ah[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                    i4v p0 = zi, p1 = zi;
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    p0 = __builtin_amdgcn_mfma_i32_4x4x4i8((int)al[i], (int)bl[i], p0, 0, 0, 0);
-                    p1 = __builtin_amdgcn_mfma_i32_4x4x4i8((int)ah[i], (int)bh[i], p1, 0, 0, 0);
-                }
-                const f4v xd0 = *reinterpret_cast<const f4v*>(xdq + (2 * jb) * MP + 4 * t);
-                const f4v xd1 = *reinterpret_cast<const f4v*>(xdq + (2 * jb + 1) * MP + 4 * t);
-                const float xs0 = xsq[(2 * jb) * MP + 4 * t + j];
-                const float xs1 = xsq[(2 * jb + 1) * MP + 4 * t + j];
+                    for (int i = 0; i < 8; i++) {
+                        p0 = __builtin_amdgcn_mfma_i32_4x4x4i8((int)al[i], (int)bl[i], p0, 0, 0, 0);
+                        p1 = __builtin_amdgcn_mfma_i32_4x4x4i8((int)ah[i], (int)bh[i], p1, 0, 0, 0);
+                    }
+                    const f4v xd0 = *reinterpret_cast<const f4v*>(xdq + (2 * jb) * MP + 4 * t);
+                    const f4v xd1 = *reinterpret_cast<const f4v*>(xdq + (2 * jb + 1) * MP + 4 * t);
+                    const float xs0 = xsq[(2 * jb) * MP + 4 * t + j];
+                    const float xs1 = xsq[(2 * jb + 1) * MP + 4 * t + j];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    acc[t][r] = fmaf((float)p0[r] * xd0[r], ds0, acc[t][r]);
-                    acc[t][r] = fmaf((float)p1[r] * xd1[r], ds1, acc[t][r]);
+                    for (int r = 0; r < 4; r++) {
+                        acc[t][r] = fmaf((float)p0[r] * xd0[r], ds0, acc[t][r]);
+                        acc[t][r] = fmaf((float)p1[r] * xd1[r], ds1, acc[t][r]);
+                    }
+                    mn[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(xs0, fm0, mn[t], 0, 0, 0);
+                    mn[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(xs1, fm1, mn[t], 0, 0, 0);
                 }
-                mn[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(xs0, fm0, mn[t], 0, 0, 0);
-                mn[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(xs1, fm1, mn[t], 0, 0, 0);
                 // keep the next step's LDS reads behind this one (without it:
                 // 219 / 372 registers, 10-40 % slower)
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        // Sum over the 16 super-block lanes of each row (lanes j + 4q) while
-        // spreading the 4 tokens over the lanes: after the xor-32 and xor-16
-        // exchanges lane bits 5..4 select the token, and the xor-8 and xor-4
-        // sums finish; lanes with bits 3..2 clear store.
-        const bool b5 = (lane & 32) != 0, b4 = (lane & 16) != 0;
-        const long row = rq * 4 + j;
+        // Sum over the S super-block lanes of each row (lane bits 2 .. L+1).
+        // With two or more levels the 4 tokens are spread over the lanes on
+        // the way: the exchanges over the top two levels leave token
+        // 2*b(L+1) + b(L) in each lane, the lower levels are plain sums, and
+        // the lanes with those lower bits clear store.
+        const long row = (u * G + sub) * 4 + j;
 #pragma unroll
         for (int t = 0; t < TG; t++) {
-            float v[4];
+            if (t < tga) {
+                float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = fmaf(-dmin, mn[t][r], acc[t][r]);
-            const float k0 = b5 ? v[2] : v[0], k1 = b5 ? v[3] : v[1];
-            const float s0 = b5 ? v[0] : v[2], s1 = b5 ? v[1] : v[3];
-            const float w0 = k0 + __shfl_xor(s0, 32), w1 = k1 + __shfl_xor(s1, 32);
-            float u = (b4 ? w1 : w0) + __shfl_xor(b4 ? w0 : w1, 16);
-            u += __shfl_xor(u, 8);
-            u += __shfl_xor(u, 4);
-            const int m = 4 * t + (lane >> 4);
-            if ((lane & 12) == 0 && m < M && row < N) a.y[(size_t)m * N + row] = u;
+                for (int r = 0; r < 4; r++) v[r] = fmaf(-dmin, mn[t][r], acc[t][r]);
+                if constexpr (L >= 2) {
+                    const bool bh = (lane >> (L + 1)) & 1, bl = (lane >> L) & 1;
+                    const float k0 = bh ? v[2] : v[0], k1 = bh ? v[3] : v[1];
+                    const float s0 = bh ? v[0] : v[2], s1 = bh ? v[1] : v[3];
+                    const float w0 = k0 + __shfl_xor(s0, 2 << L), w1 = k1 + __shfl_xor(s1, 2 << L);
+                    float uu = (bl ? w1 : w0) + __shfl_xor(bl ? w0 : w1, 1 << L);
+#pragma unroll
+                    for (int b = L - 1; b >= 2; b--) uu += __shfl_xor(uu, 1 << b);
+                    const int m = 4 * t + 2 * bh + bl;
+                    const bool st = ((lane >> 2) & ((1 << (L - 2)) - 1)) == 0;
+                    if (st && m < M && row < N) {
+                        size_t yr = (size_t)m;
+                        if constexpr (MOE) yr = (size_t)pairs[first + m];
+                        a.y[yr * N + row] = uu;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if constexpr (L == 1) v[r] += __shfl_xor(v[r], 4);
+                        const int m = 4 * t + r;
+                        if ((L == 0 || (q & 1) == 0) && m < M && row < N) {
+                            size_t yr = (size_t)m;
+                            if constexpr (MOE) yr = (size_t)pairs[first + m];
+                            a.y[yr * N + row] = v[r];
+                        }
+                    }
+                }
+            }
         }
     };
 
-    // row quads in pairs: each tile buffer is loaded while the other is computed
-    for (long rq = rq0; rq < rq1; rq += 2) {
-        if (rq + 1 < rq1) load(rq + 1, tb);
-        compute(rq, ta);
-        if (rq + 1 >= rq1) break;
-        if (rq + 2 < rq1) load(rq + 2, ta);
-        compute(rq + 1, tb);
+    // units in pairs: each tile buffer is loaded while the other is computed
+    for (long u = u0; u < u1; u += 2) {
+        if (u + 1 < u1) load(u + 1, tb);
+        compute(u, ta);
+        if (u + 1 >= u1) break;
+        if (u + 2 < u1) load(u + 2, ta);
+        compute(u + 1, tb);
     }
 }
 
@@ -251,6 +308,54 @@ bool rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w) {
     return M == 4 || (M == 3 && N >= 12288) || (M >= 5 && N >= 2048);
 }
 
+static int rq_span(int K) {
+    const int nsb = K / 256;
+    int S = 1;
+    while (S < nsb) S <<= 1;
+    return S;
+}
+
+template <bool MOE>
+static hipError_t launch_rq(const RqArgs& a0, int TG, int groups, hipStream_t st) {
+    RqArgs a = a0;
+    const int S = rq_span(a.K);
+    const int G = 16 / S;
+    a.nunits = ((long)a.N + 4 * G - 1) / (4 * G);
+    a.tok_stride = (int)rq_tok_stride(a.K);
+    a.sc_stride = 8 * 4 * TG + 4;
+    if (MOE) {
+        // four units per wave: the group's activation staging then serves
+        // four units' weights (measured at 128 experts, 64 tokens, top-8:
+        // 135 / 123 / 122 / 125 / 148 us at 1 / 2 / 4 / 8 / 16)
+        a.per_wave = 4;
+    } else {
+        // whole units per wave, as few per wave as lets every workgroup be
+        // resident at once (register-limited: 12 waves per CU at TG 1, 8 at TG 2)
+        const long target = (long)device_cu_count() * (TG == 1 ? 12 : 8);
+        a.per_wave = (int)((a.nunits + target - 1) / target);
+    }
+    const long waves = (a.nunits + a.per_wave - 1) / a.per_wave;
+    const dim3 grid((unsigned)((waves + kRqWaves - 1) / kRqWaves), (unsigned)groups);
+    const size_t shm = rq_lds(4 * TG, a.K);
+#define LP_RQ(TGV, SV) hipLaunchKernelGGL((gemv_q4k_rq<TGV, SV, MOE>), grid, dim3(64 * kRqWaves), shm, st, a)
+#define LP_RQS(TGV)                     \
+    switch (S) {                        \
+        case 1: LP_RQ(TGV, 1); break;   \
+        case 2: LP_RQ(TGV, 2); break;   \
+        case 4: LP_RQ(TGV, 4); break;   \
+        case 8: LP_RQ(TGV, 8); break;   \
+        default: LP_RQ(TGV, 16); break; \
+    }
+    if (TG == 1) {
+        LP_RQS(1)
+    } else {
+        LP_RQS(2)
+    }
+#undef LP_RQS
+#undef LP_RQ
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
     if (!rq_supported(T_Q4_K, M, K, N, w)) return hipErrorInvalidValue;
@@ -262,20 +367,30 @@ hipError_t launch_gemv_rq(const uint8_t* w, const ActView& A, float* y, int M, i
     a.M = M;
     a.K = K;
     a.N = N;
-    a.nrq = ((long)N + 3) / 4;
-    const int TG = rq_tg(M);
-    a.tok_stride = (int)rq_tok_stride(K);
-    a.sc_stride = 8 * 4 * TG + 4;
-    // whole row quads per wave, as few per wave as lets every workgroup be
-    // resident at once (register-limited: 12 waves per CU at TG 1, 8 at TG 2)
-    const long target = (long)device_cu_count() * (TG == 1 ? 12 : 8);
-    a.per_wave = (int)((a.nrq + target - 1) / target);
-    const long waves = (a.nrq + a.per_wave - 1) / a.per_wave;
-    const unsigned grid = (unsigned)((waves + kRqWaves - 1) / kRqWaves);
-    const size_t shm = rq_lds(M, K);
-    if (TG == 1) hipLaunchKernelGGL(gemv_q4k_rq<1>, dim3(grid), dim3(64 * kRqWaves), shm, st, a);
-    else hipLaunchKernelGGL(gemv_q4k_rq<2>, dim3(grid), dim3(64 * kRqWaves), shm, st, a);
-    return hipGetLastError();
+    return launch_rq<false>(a, rq_tg(M), 1, st);
+}
+
+bool rq_moe_supported(uint32_t type, int K) { return rq_supported(type, kRqMoeGroup, K, 1, nullptr); }
+
+hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, int max_groups, int gsize,
+                         int multi, int topk, float* y, int K, int N, hipStream_t st) {
+    if (N <= 0 || max_groups <= 0) return hipSuccess;
+    if (!rq_supported(T_Q4_K, kRqMoeGroup, K, N, w)) return hipErrorInvalidValue;
+    RqArgs a{};
+    a.w = w;
+    a.rb = (long)row_bytes(T_Q4_K, K);
+    a.A = A;
+    a.y = y;
+    a.M = kRqMoeGroup;
+    a.K = K;
+    a.N = N;
+    a.route = static_cast<const uint8_t*>(route);
+    a.ebytes = a.rb * N;
+    a.max_groups = max_groups;
+    a.multi = multi;
+    a.topk = topk;
+    if (gsize != kRqMoeGroup) return hipErrorInvalidValue;
+    return launch_rq<true>(a, 2, max_groups, st);
 }
 
 }  // namespace lp

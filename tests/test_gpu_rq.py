@@ -19,7 +19,7 @@ TOL = 1e-4
 CASES = [(4, 1), (4, 6), (4, 333), (4, 5000), (3, 12290), (5, 2048), (6, 2051), (7, 3001), (8, 4999)]
 
 
-@pytest.mark.parametrize("K", [256, 768, 2048, 3584, 4096])
+@pytest.mark.parametrize("K", [256, 512, 768, 1280, 2048, 3584, 4096])
 @pytest.mark.parametrize("M,N", CASES)
 def test_rq_q4k(orc, K, N, M):
     print(f"rq Q4_K M={M} K={K} N={N}", flush=True)
