@@ -221,6 +221,15 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
 
 /* ---- diagnostics ----------------------------------------------------------- */
 
+/* Routing probe, no reference counterpart: the name of the kernel family
+ * lp_gemm_q_dev runs for these operands (with a workspace of
+ * lp_act_workspace_bytes(M, K) bytes; the first chunk's kernel when M rows
+ * are split into chunks): "sb", "b32_sb", "sbm", "q6k_sbm", "rq", "i8mf",
+ * "gemm", "tile", "fact" (fp32-activation types); "" when the shape or
+ * type is rejected. The choice depends on the device (CU count): tests use
+ * it to show which kernel a parity case exercised. */
+const char* lp_gemm_route(uint32_t type, int M, int K, int N, const void* w);
+
 /* Measurement hook, no reference counterpart: streams `bytes` (a multiple
  * of 16) from device memory with `grid` x `block` threads and `unroll`
  * (1, 4 or 9) independent 16-byte non-temporal loads in flight per thread,

@@ -192,6 +192,17 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
     return LP_OK;
 }
 
+// The kernel gemm_q runs for these operands (first chunk when rows are
+// chunked), for the routing probe lp_gemm_route.
+static const char* gemm_q_route(uint32_t type, int M, int K, int N, const uint8_t* w) {
+    if (i8mf_supported(type, M, K, N, w)) return rq_preferred(type, M, K, N, w) ? "rq" : "i8mf";
+    if (use_gemm(type, M, K, N, w)) return "gemm";
+    const int chunk = i8mf_supported(type, 16, K, N, w) ? 16 : 8;
+    const int mt = M < chunk ? M : chunk;
+    if (i8mf_supported(type, mt, K, N, w)) return rq_preferred(type, mt, K, N, w) ? "rq" : "i8mf";
+    return gemv_route_name(type, mt, K, N, w);
+}
+
 // ---------------------------------------------------------------------------
 // Host-pointer machinery.
 
@@ -607,6 +618,13 @@ int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int
     if (rc != LP_OK) return rc;
     return gemm_q(ws_view(const_cast<void*>(ws), M, K), ws_planes(const_cast<void*>(ws), M, K), w,
                   type, y, M, K, N, static_cast<hipStream_t>(stream));
+}
+
+const char* lp_gemm_route(uint32_t type, int M, int K, int N, const void* w) {
+    if (fact_type(type)) return "fact";
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    if (check_shape(type, wb, M, K, N) != LP_OK || M <= 0 || N <= 0) return "";
+    return gemm_q_route(type, M, K, N, wb);
 }
 
 int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,

@@ -1293,6 +1293,19 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
     }
 }
 
+const char* gemv_route_name(uint32_t type, int M, int K, int N, const uint8_t* w) {
+    // the decisions of launch_gemv_type, in its order
+    if (type == T_Q6_K && q6k_sbm_supported(K, M, w)) return "q6k_sbm";
+    if (type == T_Q4_K && rq_preferred(type, M, K, N, w)) return "rq";
+    if (M == 1) {
+        if (type == T_Q4_K && sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0) return "sb";
+        if ((type == T_Q4_0 || type == T_Q8_0) && b32_sb_supported(type, K, w)) return "b32_sb";
+        return "tile";
+    }
+    if (M <= 4 && type == T_Q4_K && sbm_supported(K, w)) return "sbm";
+    return "tile";
+}
+
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
                        int N, hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;

@@ -51,6 +51,8 @@ hipError_t launch_gemv_fact(uint32_t type, const uint8_t* w, const float* x, flo
 hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st);
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K,
                        int N, hipStream_t st);
+// The kernel launch_gemv picks for these operands (routing probe).
+const char* gemv_route_name(uint32_t type, int M, int K, int N, const uint8_t* w);
 // Single-launch quantize + GEMV from fp32 x (M == 1, Q4_K): the workgroups
 // quantize x themselves, bit-identically to launch_quantize.
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w);

@@ -294,14 +294,26 @@ def test_gemm_q4k_small_prefill_chunks(orc, K, N, M):
         assert np.array_equal(part.view(np.uint32), y[m0:m0 + 16].view(np.uint32))
 
 
-@pytest.mark.parametrize("N,K", [(256, 14336), (8192, 512), (256, 512)])
+# (N, K) -> kernel at M = 3 and M = 4 on a 256-CU part (lp_gemm_route)
+THREE_FOUR = {(256, 14336): ("i8mf", "i8mf"), (256, 16384): ("i8mf", "i8mf"),
+              (8192, 512): ("sbm", "rq"), (256, 512): ("sbm", "rq"), (12288, 1024): ("rq", "rq")}
+
+
+@pytest.mark.parametrize("N,K", list(THREE_FOUR), ids=[f"{n}x{k}" for n, k in THREE_FOUR])
 @pytest.mark.parametrize("M", [3, 4])
 def test_q4k_three_four_rows(orc, M, N, K):
-    """Q4_K at M = 3, 4: the int8 MFMA kernel when its 16-row workgroups
-    apply and K is long (N = 256, K = 14336), the dot4 GEMV otherwise (a wide
-    shape on a 256-CU part, short K); all against the oracle's gemm_int."""
+    """Q4_K at M = 3, 4, each case on the kernel named in THREE_FOUR (checked
+    through the routing probe): the 16x16 int8 MFMA kernel when its 16-row
+    workgroups apply and K is long (N = 256, K = 14336, and K = 16384, the
+    last K whose block scales fit its LDS), the dot4 GEMV or the row-quad
+    kernel otherwise; all against the oracle's gemm_int."""
+    import torch
+    from hip_util import L, to_dev
     _flush(f"Q4_K M={M} N={N} K={K}")
     w = synth_weights(Q4_K, K, N, seed=M + N)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        route = L().lp_gemm_route(Q4_K, M, K, N, to_dev(w).data_ptr()).decode()
+        assert route == THREE_FOUR[(N, K)][M - 3]
     x = synth_x(M, K, seed=M + 3, outliers=0.01)
     y = gemm_dev(Q4_K, x, w, N)
     assert normwise(y, orc.gemm_int(Q4_K, x, w, N)) <= TOL

@@ -23,7 +23,11 @@ CASES = [(4, 1), (4, 6), (4, 333), (4, 5000), (3, 12290), (5, 2048), (6, 2051), 
 @pytest.mark.parametrize("M,N", CASES)
 def test_rq_q4k(orc, K, N, M):
     print(f"rq Q4_K M={M} K={K} N={N}", flush=True)
+    import torch
+    from hip_util import L, to_dev
     w = synth_weights(Q4_K, K, N, seed=K + 3 * N + M)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert L().lp_gemm_route(Q4_K, M, K, N, to_dev(w).data_ptr()).decode() == "rq"
     x = synth_x(M, K, seed=M * 5 + 1, outliers=0.01)
     y = gemm_dev(Q4_K, x, w, N)
     ref = orc.gemm_int(Q4_K, x, w, N)
