@@ -135,7 +135,7 @@ READ_PROBE_SHAPES = [(224, 1024, 9), (256, 1024, 9), (512, 1024, 4), (1024, 512,
                      (2048, 1024, 1), (4096, 512, 1), (8192, 256, 1), (16384, 128, 1), (32768, 64, 1)]
 
 
-def measure_read_ceiling(g: Gpu, bufs, nbytes, reps, wreps):
+def measure_read_ceiling(g: Gpu, bufs, nbytes, reps, wreps, shapes=None):
     """The part's streaming-read ceiling for this byte count: the
     lp_read_probe_dev kernel over the same rotating weight copies, graph-
     timed like the GEMV kernel, best of READ_PROBE_SHAPES (grid, block,
@@ -145,7 +145,7 @@ def measure_read_ceiling(g: Gpu, bufs, nbytes, reps, wreps):
     ncp = len(bufs)
     nb = nbytes - nbytes % 16
     res = []
-    for (grid, block, unroll) in READ_PROBE_SHAPES:
+    for (grid, block, unroll) in (shapes or READ_PROBE_SHAPES):
         def launch(i):
             g.check(g.L.lp_read_probe_dev(bufs[i % ncp].data_ptr(), nb, grid, block, unroll, sink.data_ptr(),
                                           g.stream()), "lp_read_probe_dev")
@@ -180,7 +180,7 @@ def measure_read_ceiling(g: Gpu, bufs, nbytes, reps, wreps):
             "all_us": {f"{gr}x{bl}x{un}": round(u, 3) for (u, gr, bl, un) in res}}
 
 
-def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False):
+def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False, ceiling_shapes=None):
     """Time quantize+GEMV steps over rotating weight copies; time the GEMV
     kernel alone with HIP events. Returns a dict of figures."""
     torch = g.torch
@@ -277,7 +277,7 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False):
 
     ceiling = None
     if read_ceiling:
-        ceiling = measure_read_ceiling(g, ws_list, int(w.nbytes), kreps, wreps)
+        ceiling = measure_read_ceiling(g, ws_list, int(w.nbytes), kreps, wreps, ceiling_shapes)
 
     return {
         "read_ceiling": ceiling,
@@ -764,12 +764,20 @@ def main():
                 (F32, 128, 2816, 1), (Q5_K, 14336, 4096, 1), (Q2_K, 14336, 4096, 1),
                 (BF16, 4096, 4096, 1)]
         for (tt, n, k, m) in cfgs:
-            e = measure_gemv(g, tt, n, k, m, max(64, args.steps // 4), 16)
-            extra.append({"workload": f"{TNAME[tt]} GEMV {n}x{k} M={m}",
-                          "gbs_step": round(e["gbs_step"], 1),
-                          "gbs_gemv": round(e["gbs_gemv"], 1),
-                          "hbm_frac_gemv": round(e["gbs_gemv"] / HBM_PEAK_GBS, 4),
-                          "us_gemv": round(e["us_gemv"], 3)})
+            # weight streams of 16 MB and more: the part's read ceiling for the
+            # same bytes in the probe's best shape at these sizes
+            big = row_bytes(tt, k) * n >= (16 << 20) if tt in (Q4_0, Q8_0, Q4_K, Q6_K) else False
+            e = measure_gemv(g, tt, n, k, m, max(64, args.steps // 4), 16, read_ceiling=big,
+                             ceiling_shapes=[(4096, 512, 1)])
+            line = {"workload": f"{TNAME[tt]} GEMV {n}x{k} M={m}",
+                    "gbs_step": round(e["gbs_step"], 1),
+                    "gbs_gemv": round(e["gbs_gemv"], 1),
+                    "hbm_frac_gemv": round(e["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                    "us_gemv": round(e["us_gemv"], 3)}
+            if e["read_ceiling"]:
+                line["read_ceiling_us"] = e["read_ceiling"]["us"]
+                line["frac_of_read_ceiling"] = round(e["read_ceiling"]["us"] / e["us_gemv"], 4)
+            extra.append(line)
             g.torch.cuda.empty_cache()
     out["extra"] = extra
     gemms = []
