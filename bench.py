@@ -608,6 +608,24 @@ def measure_host_api(g: Gpu, w, x, t, N, K, reps=200):
             "note": "host x/y over PCIe, registered device weights, synchronous (lp_gemm)"}
 
 
+def device_info(g: Gpu):
+    """The box's own figures next to the published peaks the roofline uses:
+    CU count, peak shader and memory clocks, memory bus width, and the
+    peaks they imply (HBM3E: 4 transfers per reported memory clock over the
+    bus, which gives the published 8 TB/s at 2000 MHz x 8192 bits; int8
+    MFMA: 4 SIMDs x 2048 int8 ops per clock per CU on gfx950)."""
+    v = [C.c_int(0) for _ in range(4)]
+    g.L.lp_device_info(*[C.byref(x) for x in v])
+    cus, clk, mclk, bus = (x.value for x in v)
+    torch = g.torch
+    return {"name": torch.cuda.get_device_properties(0).name, "cus": cus,
+            "shader_clock_mhz": round(clk / 1e3, 1), "memory_clock_mhz": round(mclk / 1e3, 1),
+            "memory_bus_bits": bus,
+            "hbm_peak_from_clocks_gbs": round(4 * mclk * 1e3 * bus / 8 / 1e9, 1),
+            "int8_peak_from_clock_tops": round(cus * 4 * 2048 * clk * 1e3 / 1e12, 1),
+            "peaks_used": {"hbm_gbs": HBM_PEAK_GBS, "int8_tops": INT8_PEAK_TOPS}}
+
+
 def host_cores():
     """Threads for the CPU baseline: every core this process may run on.
     The count is the CPU affinity set, lowered to the cgroup CPU quota when
@@ -750,6 +768,7 @@ def main():
                      "kernel": "gemv_q4k_sb (quantize fused, one launch per step)" if r["fused"]
                      else "gemv_kernel<Q4_K,M=1>", "us_per_launch": round(r["us_gemv"], 3)},
     }
+    out["device"] = device_info(g)
     out["host_api"] = measure_host_api(g, r["w_host"], r["x_host"], t, N, K)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(t, r["w_host"], r["x_host"], N, K)

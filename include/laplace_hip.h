@@ -243,6 +243,12 @@ int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int un
 const char* lp_last_error(void);
 /* 1 if the current device is usable (gfx950), 0 otherwise. */
 int lp_device_ok(void);
+/* Measurement aid, no reference counterpart: the current device's compute
+ * unit count, peak shader clock (kHz), memory clock (kHz) and memory bus
+ * width (bits), as the runtime reports them (0 where it reports nothing);
+ * bench.py records them next to the peaks it divides by. Null pointers are
+ * skipped. */
+int lp_device_info(int* cus, int* clock_khz, int* mem_clock_khz, int* mem_bus_bits);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,7 @@ SIGNATURES = {
     "lp_read_probe_dev": (_i, [_vp, _sz, _i, _i, _i, _vp, _vp]),
     "lp_last_error": (C.c_char_p, []),
     "lp_device_ok": (_i, []),
+    "lp_device_info": (_i, [_vp, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -1098,4 +1098,22 @@ const char* lp_last_error(void) { return g_err; }
 
 int lp_device_ok(void) { return dev_info().ok ? 1 : 0; }
 
+int lp_device_info(int* cus, int* clock_khz, int* mem_clock_khz, int* mem_bus_bits) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_err("no device");
+        return LP_EINVAL;
+    }
+    int v[4] = {0, 0, 0, 0};
+    const hipDeviceAttribute_t at[4] = {hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeClockRate,
+                                        hipDeviceAttributeMemoryClockRate, hipDeviceAttributeMemoryBusWidth};
+    for (int i = 0; i < 4; i++)
+        if (hipDeviceGetAttribute(&v[i], at[i], dev) != hipSuccess) v[i] = 0;
+    if (cus) *cus = v[0];
+    if (clock_khz) *clock_khz = v[1];
+    if (mem_clock_khz) *mem_clock_khz = v[2];
+    if (mem_bus_bits) *mem_bus_bits = v[3];
+    return LP_OK;
+}
+
 }  // extern "C"
