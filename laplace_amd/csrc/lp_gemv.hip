@@ -680,7 +680,10 @@ static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t s
 // (2-byte aligned): its fields are cut out of the loaded dwords with
 // v_alignbyte at compile-time offsets. Per block the reference's int dot
 // and fp32 terms (dot_row_q4_0_int_neon / dot_row_q8_0_int_neon,
-// src/matmul_simd.cpp:143-182).
+// src/matmul_simd.cpp:143-182). A group's 16-byte loads are all requested
+// before any is stored (Q8_0 in chunks of 6 KiB), and with the quantization
+// fused the second half of the workgroup's waves requests its first group
+// while the first half quantizes x.
 
 template <uint32_t T> struct B32Geom;
 template <> struct B32Geom<T_Q4_0> { static constexpr int BPB = 18; };
@@ -762,15 +765,43 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
     uint8_t* wbuf = smem + xbuf_off + (size_t)(threadIdx.x >> 6) * wbuf_bytes;
     const uint32_t act_l = lds_addr_of(smem) + sb * 272;
 
+    // the wave's row group: RPW rows of nsb blocks-of-8 (contiguous bytes),
+    // fully coalesced 16-byte loads (lane l: bytes 16 l of each KiB)
+    constexpr int NLD = (64 * SBB + 1023) / 1024;          // KiB per group when nsb == L
+    // KiB requested together: a Q4_0 group at once (9), a Q8_0 group (17)
+    // in chunks of 6, which keep the 69-dword span of the compute unspilled
+    constexpr int CH = NLD <= 9 ? NLD : 6;
+    auto load_chunk = [&](long g, int c0, u32x4 (&v)[CH]) {
+        const long gbeg = g * RPW * rb;
+        const long gend_full = gbeg + RPW * rb;
+        const long gend = gend_full < total ? gend_full : total;
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            long a = gbeg + 1024 * (c0 + k) + 16 * lane;
+            a = a + 16 <= gend ? a : gend - 16;
+            v[k] = ld_nt16(w + a);
+        }
+    };
+    const long nwaves0 = ((long)gridDim.x * blockDim.x) >> 6;
+    long g0 = (long)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    u32x4 v[CH];
+
     float xd[8], xs[8];
     if constexpr (FUSEQ) {
-        for (int i = threadIdx.x; i < (K >> 2); i += blockDim.x) {
-            const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
-            const int b = i >> 3, gq = i & 7;
-            *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
-            if (gq == 0) {
-                dl[b] = q.d;
-                sl_[b] = q.sum;
+        // as in gemv_q4k_sb: in a 16-wave workgroup the second half of the
+        // waves request their weights while the first half quantizes x
+        const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
+        const bool early = (int)threadIdx.x >= nq;
+        if (early && g0 * RPW < N) load_chunk(g0, 0, v);
+        if (!early) {
+            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
+                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
+                const int b = i >> 3, gq = i & 7;
+                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+                if (gq == 0) {
+                    dl[b] = q.d;
+                    sl_[b] = q.sum;
+                }
             }
         }
         __syncthreads();
@@ -779,10 +810,11 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
             xd[k] = dl[8 * sb + k];
             xs[k] = sl_[8 * sb + k];
         }
+        if (!early && g0 * RPW < N) load_chunk(g0, 0, v);
     } else {
         for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
-            const u32x4 v = reinterpret_cast<const u32x4*>(A.qs)[i];
-            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
+            const u32x4 a = reinterpret_cast<const u32x4*>(A.qs)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = a;
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
@@ -790,26 +822,25 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
             xs[k] = A.sum[8 * sb + k];
         }
         __syncthreads();
+        if (g0 * RPW < N) load_chunk(g0, 0, v);
     }
 
-    const long nwaves = ((long)gridDim.x * blockDim.x) >> 6;
-    for (long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6; g * RPW < N; g += nwaves) {
-        const long gbeg = g * RPW * rb;
-        const long gend_full = gbeg + RPW * rb;
-        const long gend = gend_full < total ? gend_full : total;
-        const int nld = (int)((gend - gbeg + 1023) / 1024);
-        for (int k = 0; k < nld; k++) {
-            long a = gbeg + 1024 * k + 16 * lane;
-            a = a + 16 <= gend ? a : gend - 16;
-            const u32x4 v = ld_nt16(w + a);
-            *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v;
+    // groups strided over the grid; all of a group's loads issue together
+    for (long g = g0; g * RPW < N; g += nwaves0) {
+        const int nld = (int)((((g * RPW + RPW < N ? RPW : N - g * RPW) * rb) + 1023) / 1024);
+#pragma unroll
+        for (int c0 = 0; c0 < NLD; c0 += CH) {
+            if (g != g0 || c0 != 0) load_chunk(g, c0, v);
+#pragma unroll
+            for (int k = 0; k < CH; k++)
+                if (c0 + k < NLD && c0 + k < nld) *reinterpret_cast<u32x4*>(wbuf + 1024 * (c0 + k) + 16 * lane) = v[k];
         }
         const u32x4* mine = reinterpret_cast<const u32x4*>(wbuf + (size_t)(rsub * nsb + sb) * SBB);
         uint32_t wd[4 * NV + 1];
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            const u32x4 v = mine[k];
-            wd[4 * k] = v.x; wd[4 * k + 1] = v.y; wd[4 * k + 2] = v.z; wd[4 * k + 3] = v.w;
+            const u32x4 m = mine[k];
+            wd[4 * k] = m.x; wd[4 * k + 1] = m.y; wd[4 * k + 2] = m.z; wd[4 * k + 3] = m.w;
         }
         wd[4 * NV] = 0;                           // alignbyte partner past the span end (unused bytes)
         float t = b32_span<T>(wd, act_l, xd, xs, 0.0f);
