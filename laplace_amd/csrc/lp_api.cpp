@@ -195,11 +195,13 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
 // The kernel gemm_q runs for these operands (first chunk when rows are
 // chunked), for the routing probe lp_gemm_route.
 static const char* gemm_q_route(uint32_t type, int M, int K, int N, const uint8_t* w) {
-    if (i8mf_supported(type, M, K, N, w)) return rq_preferred(type, M, K, N, w) ? "rq" : "i8mf";
+    if (i8mf_supported(type, M, K, N, w))
+        return rq_preferred(type, M, K, N, w) ? "rq" : q6rq_preferred(type, M, K, N, w) ? "q6rq" : "i8mf";
     if (use_gemm(type, M, K, N, w)) return "gemm";
     const int chunk = i8mf_supported(type, 16, K, N, w) ? 16 : 8;
     const int mt = M < chunk ? M : chunk;
-    if (i8mf_supported(type, mt, K, N, w)) return rq_preferred(type, mt, K, N, w) ? "rq" : "i8mf";
+    if (i8mf_supported(type, mt, K, N, w))
+        return rq_preferred(type, mt, K, N, w) ? "rq" : q6rq_preferred(type, mt, K, N, w) ? "q6rq" : "i8mf";
     return gemv_route_name(type, mt, K, N, w);
 }
 

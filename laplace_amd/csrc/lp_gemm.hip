@@ -1208,6 +1208,7 @@ hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, f
     if (M <= 0 || N <= 0) return hipSuccess;
     if (!i8mf_supported(type, M, K, N, w)) return hipErrorInvalidValue;
     if (rq_preferred(type, M, K, N, w)) return launch_gemv_rq(w, A, y, M, K, N, st);
+    if (q6rq_preferred(type, M, K, N, w)) return launch_gemv_q6rq(w, A, y, M, K, N, st);
     const dim3 grid((N + 16 * kMfTiles - 1) / (16 * kMfTiles));
     if (type == T_Q8_0) {
         const size_t shm = (size_t)(K / 32) * 16 * 4;

@@ -1295,6 +1295,7 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
         if (rq_preferred(T, M, K, N, w)) return launch_gemv_rq(w, A, y, M, K, N, st);
     }
     if constexpr (T == T_Q6_K) {
+        if (q6rq_preferred(T, M, K, N, w)) return launch_gemv_q6rq(w, A, y, M, K, N, st);
         if (q6k_sbm_supported(K, M, w)) return launch_q6k_sbm(w, A, y, M, K, N, st);
     }
     switch (M) {
@@ -1326,6 +1327,7 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
 
 const char* gemv_route_name(uint32_t type, int M, int K, int N, const uint8_t* w) {
     // the decisions of launch_gemv_type, in its order
+    if (type == T_Q6_K && q6rq_preferred(type, M, K, N, w)) return "q6rq";
     if (type == T_Q6_K && q6k_sbm_supported(K, M, w)) return "q6k_sbm";
     if (type == T_Q4_K && rq_preferred(type, M, K, N, w)) return "rq";
     if (M == 1) {

@@ -89,6 +89,11 @@ hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, f
 bool rq_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
 bool rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w);
 hipError_t launch_gemv_rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
+
+// Q6_K GEMV for 1 <= M <= 8 on 4x4x4 int8 MFMA blocks (lp_q6rq.hip), any K.
+bool q6rq_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
+bool q6rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w);
+hipError_t launch_gemv_q6rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
 size_t gemm_planes_bytes(int M, int K);
 // planes from fp32 x (quantize + planes in one pass)
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st);
