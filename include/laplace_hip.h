@@ -105,7 +105,9 @@ int lp_dequantize(const uint8_t* w, uint32_t type, float* dst, long n);
 
 /* ---- 2. device-pointer, stream-ordered API ------------------------------- */
 
-/* Bytes of workspace holding M rows of quantized activations of length K. */
+/* Bytes of workspace holding M rows of quantized activations of length K,
+ * plus the scratch of the kernels that run on them (fp16 planes of the
+ * prefill GEMM for M >= 5, 2 MiB of partial sums for 3 <= M <= 8). */
 size_t lp_act_workspace_bytes(int M, int K);
 
 /* Quantize x[M,K] (device) into the workspace (codes, scales, sums). */

@@ -84,9 +84,16 @@ static size_t act_bytes(int M, int K) {
     return up256((size_t)M * K) + 3 * up256(nbk * 4);
 }
 
-// Activation blocks, plus the fp16 planes of the MFMA products when M >= 5.
+// Scratch for the partial sums of the K-split Q6_K row-quad GEMV (3 <= M <= 8).
+constexpr size_t kPartReserve = size_t(2) << 20;
+static size_t part_reserve(int M) { return M >= 3 && M <= 8 ? kPartReserve : 0; }
+
+static size_t planes_reserve(int M, int K) { return M >= 5 ? gemm_planes_bytes(M, K) : 0; }
+
+// Activation blocks, plus the fp16 planes of the MFMA products when M >= 5,
+// plus the partial-sum scratch when 3 <= M <= 8.
 static size_t ws_bytes(int M, int K) {
-    return act_bytes(M, K) + (M >= 5 ? gemm_planes_bytes(M, K) : 0);
+    return act_bytes(M, K) + planes_reserve(M, K) + part_reserve(M);
 }
 
 static void* ws_planes(void* ws, int M, int K) {
@@ -104,6 +111,16 @@ static ActView ws_view(void* ws, int M, int K) {
     a.sum = reinterpret_cast<float*>(p);
     p += up256(nbk * 4);
     a.s16 = reinterpret_cast<int32_t*>(p);
+    return a;
+}
+
+// ws_view of a workspace of ws_bytes(M, K) bytes, with its partial-sum scratch.
+static ActView ws_view_full(void* ws, int M, int K) {
+    ActView a = ws_view(ws, M, K);
+    if (part_reserve(M)) {
+        a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + act_bytes(M, K) + planes_reserve(M, K));
+        a.part_bytes = part_reserve(M);
+    }
     return a;
 }
 
@@ -181,7 +198,7 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
     const int chunk = i8mf_supported(type, 16, K, N, w) ? 16 : 8;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mt = M - m0 < chunk ? M - m0 : chunk;
-        ActView sub;
+        ActView sub = A;                 // the partial-sum scratch is shared (stream-ordered)
         sub.qs = A.qs + (size_t)m0 * K;
         sub.d = A.d + (size_t)m0 * (K / 32);
         sub.sum = A.sum + (size_t)m0 * (K / 32);
@@ -329,7 +346,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     } else if (gemv_fused_supported(type, M, K, wd)) {
         LP_HIP(launch_gemv_fused(type, wd, c->xd, c->yd, M, K, N, c->stream));
     } else if (i8mf_supported(type, M, K, N, wd)) {
-        const ActView A = ws_view(c->ws, M, K);
+        const ActView A = ws_view_full(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
     } else if (use_gemm(type, M, K, N, wd)) {
@@ -337,7 +354,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));
         LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
     } else {
-        const ActView A = ws_view(c->ws, M, K);
+        const ActView A = ws_view_full(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
         if ((rc = gemm_q(A, ws_planes(c->ws, M, K), wd, type, c->yd, M, K, N, c->stream)) != LP_OK)
             return rc;
@@ -594,7 +611,7 @@ int lp_quantize_act_dev(const float* x, int M, int K, void* ws, size_t wsb, void
         set_err("x must be 16-byte aligned");
         return LP_EINVAL;
     }
-    LP_HIP(launch_quantize(x, M, K, ws_view(ws, M, K), static_cast<hipStream_t>(stream)));
+    LP_HIP(launch_quantize(x, M, K, ws_view_full(ws, M, K), static_cast<hipStream_t>(stream)));
     return LP_OK;
 }
 
@@ -618,7 +635,7 @@ int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int
     }
     int rc = check_shape(type, w, M, K, N);
     if (rc != LP_OK) return rc;
-    return gemm_q(ws_view(const_cast<void*>(ws), M, K), ws_planes(const_cast<void*>(ws), M, K), w,
+    return gemm_q(ws_view_full(const_cast<void*>(ws), M, K), ws_planes(const_cast<void*>(ws), M, K), w,
                   type, y, M, K, N, static_cast<hipStream_t>(stream));
 }
 

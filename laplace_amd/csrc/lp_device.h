@@ -31,6 +31,10 @@ struct ActView {
     float*   d;
     float*   sum;
     int32_t* s16;
+    // scratch of the caller's workspace for partial sums of K-split kernels
+    // (none when null; kernels then run unsplit)
+    float*   part = nullptr;
+    size_t   part_bytes = 0;
 };
 
 __device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {

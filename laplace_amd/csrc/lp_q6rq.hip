@@ -54,12 +54,14 @@ struct Q6rqArgs {
     int M, K, N;
     int nchunk;          // chunks of 16 super-blocks
     int buf_bytes;       // LDS bytes per chunk buffer
+    float* part;         // K split: per chunk (blockIdx.y) partial sums [nchunk][M][N]; else null
 };
 
 struct Q6Tile {
     u32x4 r[13];         // dwords 0..51 from the dword at or below the block start
     uint32_t tail;       // dword 52 (block bytes 206..209) when the block starts at byte 2 of a dword
     uint32_t dh;         // d (fp16 bits)
+    uint32_t sh;         // byte offset of the block start in dword 0 (0 or 2)
 };
 
 template <int TG, bool COAL>
@@ -73,16 +75,16 @@ gemv_q6k_rq(Q6rqArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane >> 2, j = lane & 3;
     const int tga = (M + 3) >> 2;
-    const long quad = (long)blockIdx.x * kQ6rqWaves + wave;
-    long row = quad * 4 + j;
-    const bool row_ok = row < N;
-    row = row_ok ? row : (long)N - 1;
-    const uint8_t* wrow = a.w + row * a.rb;
+    // row j of row quad qd (clamped to the last row)
+    auto lane_row = [&](long qd) {
+        const long r = qd * 4 + j;
+        return r < N ? r : (long)N - 1;
+    };
 
-    auto load = [&](int c, Q6Tile& t) {
+    auto load = [&](int c, long qd, Q6Tile& t) {
         int sb = 16 * c + q;
         sb = sb < nsb ? sb : nsb - 1;
-        const uint8_t* blk = wrow + (long)sb * 210;
+        const uint8_t* blk = a.w + lane_row(qd) * a.rb + (long)sb * 210;
         const uintptr_t ab = reinterpret_cast<uintptr_t>(blk);
         const uint8_t* base = reinterpret_cast<const uint8_t*>(ab & ~uintptr_t(3));
 #pragma unroll
@@ -94,6 +96,7 @@ gemv_q6k_rq(Q6rqArgs a) {
         // 51 again, so no load passes the block's end
         t.tail = *reinterpret_cast<const uint32_t*>(base + ((ab & 3) ? 208 : 204));
         t.dh = *reinterpret_cast<const uint16_t*>(blk + 208);
+        t.sh = (uint32_t)(ab & 3);
     };
 
     // chunk staging: tokens' codes (16-byte pieces) and per block xd, c0, c1
@@ -154,18 +157,15 @@ gemv_q6k_rq(Q6rqArgs a) {
     for (int t = 0; t < TG; t++) tot[t] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     // the lane's super-block as dwords 0..51 (ql, qh, scales) and its d
-    auto tile_words = [&](int c, const Q6Tile& T, uint32_t (&wd)[52], uint32_t& dh) {
+    auto tile_words = [&](const Q6Tile& T, uint32_t (&wd)[52], uint32_t& dh) {
         uint32_t raw[53];
 #pragma unroll
         for (int k = 0; k < 13; k++) {
             raw[4 * k] = T.r[k].x; raw[4 * k + 1] = T.r[k].y; raw[4 * k + 2] = T.r[k].z; raw[4 * k + 3] = T.r[k].w;
         }
         raw[52] = T.tail;
-        int sb = 16 * c + q;
-        sb = sb < nsb ? sb : nsb - 1;
-        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(wrow + (long)sb * 210) & 3);
 #pragma unroll
-        for (int k = 0; k < 52; k++) wd[k] = alignb(raw[k + 1], raw[k], sh);
+        for (int k = 0; k < 52; k++) wd[k] = alignb(raw[k + 1], raw[k], T.sh);
         dh = T.dh;
     };
 
@@ -228,7 +228,32 @@ gemv_q6k_rq(Q6rqArgs a) {
     };
 
     const int nc = a.nchunk;
+
+    // Sum over the 16 super-block lanes of each row (lane bits 2..5) and
+    // store row quad qd's outputs. The exchanges over bits 5 and 4 leave
+    // token 2*b5 + b4 of the group in each lane, bits 3 and 2 are plain sums,
+    // and the lanes with those clear store.
+    auto emit = [&](long qd, float* out) {
+        const long row = qd * 4 + j;
+#pragma unroll
+        for (int t = 0; t < TG; t++) {
+            if (t < tga) {
+                const f4v v = tot[t];
+                const bool bh = (lane >> 5) & 1, bl = (lane >> 4) & 1;
+                const float k0 = bh ? v[2] : v[0], k1 = bh ? v[3] : v[1];
+                const float s0 = bh ? v[0] : v[2], s1 = bh ? v[1] : v[3];
+                const float w0 = k0 + __shfl_xor(s0, 32), w1 = k1 + __shfl_xor(s1, 32);
+                float uu = (bl ? w1 : w0) + __shfl_xor(bl ? w0 : w1, 16);
+                uu += __shfl_xor(uu, 8);
+                uu += __shfl_xor(uu, 4);
+                const int m = 4 * t + 2 * bh + bl;
+                if ((lane & 12) == 0 && m < M && row < N) out[(size_t)m * N + row] = uu;
+            }
+        }
+    };
+
     if constexpr (COAL) {
+    const long quad = (long)blockIdx.x * kQ6rqWaves + wave;
     // Coalesced weight path: the wave copies its quad's chunk (4 rows x up
     // to 3360 bytes) into its own LDS region, row stride RS, as 16-byte
     // pieces at consecutive 16-byte aligned addresses (piece P = lane + 64 k:
@@ -299,36 +324,36 @@ gemv_q6k_rq(Q6rqArgs a) {
             __syncthreads();
         }
     }
+    emit(quad, a.y);
     } else {
-        // one chunk (K <= 4096): the lane's super-block loaded directly
+        // one row quad per wave and one chunk per workgroup (blockIdx.y;
+        // K <= 4096, or K split with the chunks' partial sums into a.part):
+        // many short-lived workgroups, whose loads and compute overlap
+        // across the resident ones (row quads in sequence per wave with the
+        // next one's super-blocks requested early measured slower: fewer
+        // resident waves at 183 VGPRs)
+        const int c = blockIdx.y;
+        const long qd = (long)blockIdx.x * kQ6rqWaves + wave;
         Q6Tile t0;
-        load(0, t0);
-        stage_load(0);
+        load(c, qd, t0);
+        stage_load(c);
         stage_store(0);
         __syncthreads();
         uint32_t wd[52], dh;
-        tile_words(0, t0, wd, dh);
-        compute(0, wd, dh, 0);
+        tile_words(t0, wd, dh);
+        compute(c, wd, dh, 0);
+        emit(qd, a.part ? a.part + (size_t)c * M * N : a.y);
     }
+}
 
-    // Sum over the 16 super-block lanes of each row (lane bits 2..5). The
-    // exchanges over bits 5 and 4 leave token 2*b5 + b4 of the group in each
-    // lane, bits 3 and 2 are plain sums, and the lanes with those clear store.
-#pragma unroll
-    for (int t = 0; t < TG; t++) {
-        if (t < tga) {
-            const f4v v = tot[t];
-            const bool bh = (lane >> 5) & 1, bl = (lane >> 4) & 1;
-            const float k0 = bh ? v[2] : v[0], k1 = bh ? v[3] : v[1];
-            const float s0 = bh ? v[0] : v[2], s1 = bh ? v[1] : v[3];
-            const float w0 = k0 + __shfl_xor(s0, 32), w1 = k1 + __shfl_xor(s1, 32);
-            float uu = (bl ? w1 : w0) + __shfl_xor(bl ? w0 : w1, 16);
-            uu += __shfl_xor(uu, 8);
-            uu += __shfl_xor(uu, 4);
-            const int m = 4 * t + 2 * bh + bl;
-            if ((lane & 12) == 0 && m < M && row_ok) a.y[(size_t)m * N + row] = uu;
-        }
-    }
+// K split: y = the chunks' partial sums added in chunk order
+__global__ void __launch_bounds__(256)
+q6rq_reduce(const float* __restrict__ part, int nsplit, long mn, float* __restrict__ y) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float s = part[i];
+    for (int c = 1; c < nsplit; c++) s += part[(size_t)c * mn + i];
+    y[i] = s;
 }
 
 static int q6rq_tg(int M) { return M <= 4 ? 1 : 2; }
@@ -360,9 +385,16 @@ hipError_t launch_gemv_q6rq(const uint8_t* w, const ActView& A, float* y, int M,
     const int TG = q6rq_tg(M);
     a.buf_bytes = (int)q6rq_buf(TG);
     const long quads = ((long)N + 3) / 4;
-    const dim3 grid((unsigned)((quads + kQ6rqWaves - 1) / kQ6rqWaves));
-    const bool coal = a.nchunk > 1;
-    const size_t shm = 2 * q6rq_buf(TG) + (coal ? (size_t)kQ6rqWaves * 4 * kQ6rqRowStride : 0);
+    // K over several chunks: one workgroup per (row-quad group, chunk) when
+    // the caller's scratch holds the partial sums (more waves), else the
+    // chunk loop with coalesced chunk copies
+    const size_t part_need = (size_t)a.nchunk * M * N * sizeof(float);
+    const bool split = a.nchunk > 1 && A.part && part_need <= A.part_bytes;
+    const bool coal = a.nchunk > 1 && !split;
+    a.part = split ? A.part : nullptr;
+    const long gx = (quads + kQ6rqWaves - 1) / kQ6rqWaves;
+    const dim3 grid((unsigned)gx, split ? (unsigned)a.nchunk : 1u);
+    const size_t shm = coal ? 2 * q6rq_buf(TG) + (size_t)kQ6rqWaves * 4 * kQ6rqRowStride : q6rq_buf(TG);
 #define LP_Q6RQ_LAUNCH(TGV, CV) hipLaunchKernelGGL((gemv_q6k_rq<TGV, CV>), grid, dim3(64 * kQ6rqWaves), shm, st, a)
     if (TG == 1) {
         if (coal) LP_Q6RQ_LAUNCH(1, true);
@@ -372,6 +404,10 @@ hipError_t launch_gemv_q6rq(const uint8_t* w, const ActView& A, float* y, int M,
         else LP_Q6RQ_LAUNCH(2, false);
     }
 #undef LP_Q6RQ_LAUNCH
+    if (split) {
+        const long mn = (long)M * N;
+        hipLaunchKernelGGL(q6rq_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, a.part, a.nchunk, mn, y);
+    }
     return hipGetLastError();
 }
 

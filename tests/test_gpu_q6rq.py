@@ -45,3 +45,17 @@ def test_q6rq_config3(orc):
         x = synth_x(M, K, seed=M + 40)
         y = gemm_dev(Q6_K, x, w, N)
         assert normwise(y[:, rows], orc.gemm_int(Q6_K, x, ws, len(rows))) <= TOL
+
+
+def test_q6rq_unsplit_long_k(orc):
+    """Long K whose partial sums exceed the workspace's scratch (8 rows x
+    5 chunks x 13200 outputs > 2 MiB): the chunk loop with coalesced chunk
+    copies; a sample of 128 rows against the oracle."""
+    K, N, M = 18944, 13200, 8
+    w = synth_weights(Q6_K, K, N, seed=97)
+    rb = K // 256 * 210
+    rows = np.sort(np.random.default_rng(8).choice(N, 128, replace=False))
+    ws = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    x = synth_x(M, K, seed=77)
+    y = gemm_dev(Q6_K, x, w, N)
+    assert normwise(y[:, rows], orc.gemm_int(Q6_K, x, ws, len(rows))) <= TOL
