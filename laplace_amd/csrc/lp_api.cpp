@@ -830,18 +830,23 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
                             st));
     if ((rc = lp_gemm_dev(f.rin, router_w, router_type, f.logits, T, H, n_exp, f.rws, f.rws_b, stream)) != LP_OK)
         return rc;
-    LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
     if (fused) {
         // one route table for both products: groups of 8 only if both run on
-        // the row-quad kernel
+        // the row-quad kernel; for a few tokens the top-k kernel builds it
         const int gs = std::min(moe_group_size(gate_up_type, H, P, n_exp), moe_group_size(down_type, inter, P, n_exp));
-        LP_HIP(launch_moe_route(idx, P, n_exp, f.route, gs, st));
+        if (moe_topk_route_supported(T)) {
+            LP_HIP(launch_moe_topk_route(f.logits, T, n_exp, top_k, idx, wts, f.route, gs, st));
+        } else {
+            LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
+            LP_HIP(launch_moe_route(idx, P, n_exp, f.route, gs, st));
+        }
         LP_HIP(launch_moe_grouped_routed(gate_up_type, gate_up_w, f.eq, gs, T, P, n_exp, 0, top_k, f.route,
                                          f.gu, H, 2 * inter, st));
         LP_HIP(launch_geglu(f.gu, P, inter, f.hidden, f.hq, st));
         LP_HIP(launch_moe_grouped_routed(down_type, down_w, f.hq, gs, P, P, n_exp, 1, top_k, f.route, f.eo,
                                          inter, H, st));
     } else {
+        LP_HIP(launch_moe_topk(f.logits, T, n_exp, top_k, idx, wts, st));
         if ((rc = lp_moe_grouped_dev(f.ein, 0, idx, gate_up_w, gate_up_type, f.gu, T, top_k, n_exp, H, 2 * inter,
                                      f.mws, f.mws_b, stream)) != LP_OK)
             return rc;

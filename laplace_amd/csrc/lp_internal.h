@@ -32,6 +32,11 @@ int moe_topk_max_experts();
 // norms of x [T, H]; when Aq.qs is set, ein is also quantized into Aq (H % 32 == 0)
 hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
                             float eps, float* rin, float* ein, const ActView& Aq, hipStream_t st);
+// Top-k and the route table in one launch (up to 16 tokens; preferred for
+// T <= 4: moe_topk_route_supported).
+bool moe_topk_route_supported(int T);
+hipError_t launch_moe_topk_route(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
+                                 void* route, int gsize, hipStream_t st);
 hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
                            hipStream_t st);
 // hidden [P, inter]; when Aq.qs is set, also quantized into Aq (inter % 32 == 0)

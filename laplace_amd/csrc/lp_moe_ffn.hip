@@ -6,6 +6,7 @@
 
 #include "lp_chunks.h"
 #include "lp_internal.h"
+#include "lp_route.h"
 
 namespace lp {
 
@@ -123,11 +124,12 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 // loop); the k-weight sum runs in pick order. n_exp <= 64 * kTopkPer.
 constexpr int kTopkPer = 16;
 
-__global__ void __launch_bounds__(64)
-moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __restrict__ idx,
-                float* __restrict__ wts) {
-    const int lane = threadIdx.x;
-    const float* l = logits + (size_t)blockIdx.x * n_exp;
+// Token t's top-k by one wave (lane = its lane); the picks also go to
+// lidx (LDS) when given.
+__device__ __forceinline__ void topk_token(const float* __restrict__ logits, int t, int n_exp, int top_k,
+                                           int* __restrict__ idx, float* __restrict__ wts, int* lidx) {
+    const int lane = threadIdx.x & 63;
+    const float* l = logits + (size_t)t * n_exp;
     float v[kTopkPer];
     float mx = -INFINITY;
 #pragma unroll
@@ -174,9 +176,30 @@ moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __r
     for (int k = 0; k < top_k; k++)
         wsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), k));
     if (lane < top_k) {
-        idx[(size_t)blockIdx.x * top_k + lane] = mine_i;
-        wts[(size_t)blockIdx.x * top_k + lane] = mine / wsum;
+        idx[(size_t)t * top_k + lane] = mine_i;
+        wts[(size_t)t * top_k + lane] = mine / wsum;
+        if (lidx) lidx[t * top_k + lane] = mine_i;
     }
+}
+
+__global__ void __launch_bounds__(64)
+moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __restrict__ idx,
+                float* __restrict__ wts) {
+    topk_token(logits, blockIdx.x, n_exp, top_k, idx, wts, nullptr);
+}
+
+// A few tokens (T <= 4): one workgroup does every token's top-k (a wave
+// each) and then builds the route table of the grouped expert passes from
+// the picks in LDS: one launch instead of two.
+__global__ void __launch_bounds__(1024)
+moe_topk_route_kernel(const float* __restrict__ logits, int T, int n_exp, int top_k, int* __restrict__ idx,
+                      float* __restrict__ wts, uint8_t* __restrict__ route, int max_groups, int gsize) {
+    extern __shared__ int tsm[];
+    int* lidx = tsm;                                   // T * top_k picks
+    const int wave = threadIdx.x >> 6;
+    if (wave < T) topk_token(logits, wave, n_exp, top_k, idx, wts, lidx);
+    __syncthreads();
+    build_route(lidx, T * top_k, n_exp, route, max_groups, gsize, tsm + ((T * top_k + 3) & ~3));
 }
 
 // hidden[p][i] = gelu_tanh(gate[p][i]) * up[p][i], gate|up = gu row p
@@ -247,6 +270,22 @@ hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int
                            hipStream_t st) {
     if (T <= 0) return hipSuccess;
     hipLaunchKernelGGL(moe_topk_kernel, dim3(T), dim3(64), 0, st, logits, n_exp, top_k, idx, wts);
+    return hipGetLastError();
+}
+
+// measured at 128 experts, top-8 (us per layer, separate kernels vs one):
+// T=1 37.4 / 36.9, T=4 51.5 / 50.2, T=16 85.3 / 89.0 (one wave per token
+// on one CU loses to a workgroup per token)
+bool moe_topk_route_supported(int T) { return T >= 1 && T <= 4; }
+
+hipError_t launch_moe_topk_route(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
+                                 void* route, int gsize, hipStream_t st) {
+    if (T < 1 || T > 16 || n_exp > kMoeMaxExperts || gsize < 4) return hipErrorInvalidValue;
+    const int P = T * top_k;
+    const int mg = moe_max_groups(P, n_exp);
+    const size_t shm = sizeof(int) * ((size_t)((P + 3) & ~3) + 3 * (size_t)n_exp + 2 * 16);
+    hipLaunchKernelGGL(moe_topk_route_kernel, dim3(1), dim3(1024), shm, st, logits, T, n_exp, top_k, idx, wts,
+                       static_cast<uint8_t*>(route), mg, gsize);
     return hipGetLastError();
 }
 
