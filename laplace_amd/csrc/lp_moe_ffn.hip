@@ -121,19 +121,22 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 // '>' scan; a pick is then set to -1e30 as the reference does), and the k
 // weights divided by their sum (src/arch_gemma4.cpp:546-563). The sum of
 // exponentials is a wave reduction (reassociated against the reference's
-// loop); the k-weight sum runs in pick order. n_exp <= 64 * kTopkPer.
+// loop); the k-weight sum runs in pick order. n_exp <= 64 * PER (PER
+// logits per lane, the smallest power of two that holds them, up to
+// kTopkPer).
 constexpr int kTopkPer = 16;
 
 // Token t's top-k by one wave (lane = its lane); the picks also go to
 // lidx (LDS) when given.
+template <int PER>
 __device__ __forceinline__ void topk_token(const float* __restrict__ logits, int t, int n_exp, int top_k,
                                            int* __restrict__ idx, float* __restrict__ wts, int* lidx) {
     const int lane = threadIdx.x & 63;
     const float* l = logits + (size_t)t * n_exp;
-    float v[kTopkPer];
+    float v[PER];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kTopkPer; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = lane + 64 * j;
         v[j] = e < n_exp ? l[e] : -INFINITY;
         mx = fmaxf(mx, v[j]);
@@ -141,20 +144,20 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ logits, int
     mx = wave_max(mx);
     float sm = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kTopkPer; j++) {
+    for (int j = 0; j < PER; j++) {
         v[j] = lane + 64 * j < n_exp ? expf(v[j] - mx) : 0.0f;
         sm += v[j];
     }
     sm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, group_sum(sm, 64)), 63));
 #pragma unroll
-    for (int j = 0; j < kTopkPer; j++) v[j] = lane + 64 * j < n_exp ? v[j] / sm : -INFINITY;
+    for (int j = 0; j < PER; j++) v[j] = lane + 64 * j < n_exp ? v[j] / sm : -INFINITY;
     float mine = 0.0f;
     int mine_i = 0;
     for (int k = 0; k < top_k; k++) {     // top_k <= 16 (the reference's top_idx[16])
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
-        for (int j = 0; j < kTopkPer; j++) {
+        for (int j = 0; j < PER; j++) {
             const int e = lane + 64 * j;
             if (e < n_exp && v[j] > bv) {  // ascending e within the lane: strict '>' keeps the lowest
                 bv = v[j];
@@ -168,7 +171,7 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ logits, int
         }
         if ((bi & 63) == lane) {
 #pragma unroll
-            for (int j = 0; j < kTopkPer; j++)
+            for (int j = 0; j < PER; j++)
                 if (lane + 64 * j == bi) v[j] = -1e30f;
         }
     }
@@ -182,22 +185,24 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ logits, int
     }
 }
 
+template <int PER>
 __global__ void __launch_bounds__(64)
 moe_topk_kernel(const float* __restrict__ logits, int n_exp, int top_k, int* __restrict__ idx,
                 float* __restrict__ wts) {
-    topk_token(logits, blockIdx.x, n_exp, top_k, idx, wts, nullptr);
+    topk_token<PER>(logits, blockIdx.x, n_exp, top_k, idx, wts, nullptr);
 }
 
 // A few tokens (T <= 4): one workgroup does every token's top-k (a wave
 // each) and then builds the route table of the grouped expert passes from
 // the picks in LDS: one launch instead of two.
+template <int PER>
 __global__ void __launch_bounds__(1024)
 moe_topk_route_kernel(const float* __restrict__ logits, int T, int n_exp, int top_k, int* __restrict__ idx,
                       float* __restrict__ wts, uint8_t* __restrict__ route, int max_groups, int gsize) {
     extern __shared__ int tsm[];
     int* lidx = tsm;                                   // T * top_k picks
     const int wave = threadIdx.x >> 6;
-    if (wave < T) topk_token(logits, wave, n_exp, top_k, idx, wts, lidx);
+    if (wave < T) topk_token<PER>(logits, wave, n_exp, top_k, idx, wts, lidx);
     __syncthreads();
     build_route(lidx, T * top_k, n_exp, route, max_groups, gsize, tsm + ((T * top_k + 3) & ~3));
 }
@@ -256,6 +261,13 @@ moe_combine_kernel(const float* __restrict__ eo, const int* __restrict__ idx, co
 
 int moe_topk_max_experts() { return 64 * kTopkPer; }
 
+// logits per lane of the top-k wave
+static int topk_per(int n_exp) {
+    int per = 1;
+    while (64 * per < n_exp) per <<= 1;
+    return per;
+}
+
 hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
                             float eps, float* rin, float* ein, const ActView& Aq, hipStream_t st) {
     if (T <= 0) return hipSuccess;
@@ -269,7 +281,15 @@ hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scal
 hipError_t launch_moe_topk(const float* logits, int T, int n_exp, int top_k, int* idx, float* wts,
                            hipStream_t st) {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(T), dim3(64), 0, st, logits, n_exp, top_k, idx, wts);
+#define LP_TK(PV) hipLaunchKernelGGL(moe_topk_kernel<PV>, dim3(T), dim3(64), 0, st, logits, n_exp, top_k, idx, wts)
+    switch (topk_per(n_exp)) {
+        case 1: LP_TK(1); break;
+        case 2: LP_TK(2); break;
+        case 4: LP_TK(4); break;
+        case 8: LP_TK(8); break;
+        default: LP_TK(16); break;
+    }
+#undef LP_TK
     return hipGetLastError();
 }
 
@@ -284,8 +304,16 @@ hipError_t launch_moe_topk_route(const float* logits, int T, int n_exp, int top_
     const int P = T * top_k;
     const int mg = moe_max_groups(P, n_exp);
     const size_t shm = sizeof(int) * ((size_t)((P + 3) & ~3) + 3 * (size_t)n_exp + 2 * 16);
-    hipLaunchKernelGGL(moe_topk_route_kernel, dim3(1), dim3(1024), shm, st, logits, T, n_exp, top_k, idx, wts,
-                       static_cast<uint8_t*>(route), mg, gsize);
+#define LP_TKR(PV) hipLaunchKernelGGL(moe_topk_route_kernel<PV>, dim3(1), dim3(1024), shm, st, logits, T, n_exp, \
+                                      top_k, idx, wts, static_cast<uint8_t*>(route), mg, gsize)
+    switch (topk_per(n_exp)) {
+        case 1: LP_TKR(1); break;
+        case 2: LP_TKR(2); break;
+        case 4: LP_TKR(4); break;
+        case 8: LP_TKR(8); break;
+        default: LP_TKR(16); break;
+    }
+#undef LP_TKR
     return hipGetLastError();
 }
 
