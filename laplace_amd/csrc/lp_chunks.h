@@ -441,4 +441,41 @@ __device__ __forceinline__ Q8Group quant_group8(const float4 v) {
     return r;
 }
 
+
+// gelu_tanh(g) * u (ops::geglu, src/ops.cpp:132-174:
+// 0.5 * g * (1 + tanh(c * (g + 0.044715 g^3)))), contraction off.
+__device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float g3 = (g * g) * g;
+    const float cst = 0.7978845608028654f;
+    const float gelu = 0.5f * g * (1.0f + tanhf(cst * (g + 0.044715f * g3)));
+    return gelu * u;
+}
+
+// GeGLU of one gate|up row (gate: K floats, then up: K floats) quantized in
+// 32-element blocks exactly as the MoE layer's GeGLU kernel quantizes it,
+// written to a GEMV's LDS staging: codes of element e at
+// codes[(e / 256) * 272 + e % 256], block b's d at
+// dsc[(b / 8) * s1 + (b % 8) * s2] and its scaled sum soff floats after.
+// Threads tid, tid + nt, ... (nt a multiple of 64) take one float4 each, 8
+// consecutive lanes per block; K % 32 == 0.
+__device__ __forceinline__ void stage_geglu_row(const float* __restrict__ gu, int K, uint8_t* codes, float* dsc,
+                                                int s1, int s2, int soff, int tid, int nt) {
+    for (int i4 = tid; i4 < (K >> 2); i4 += nt) {
+        const float4 g = reinterpret_cast<const float4*>(gu)[i4];
+        const float4 u = reinterpret_cast<const float4*>(gu + K)[i4];
+        const float4 h = make_float4(gelu_tanh_mul(g.x, u.x), gelu_tanh_mul(g.y, u.y), gelu_tanh_mul(g.z, u.z),
+                                     gelu_tanh_mul(g.w, u.w));
+        const Q8Group q = quant_group8(h);
+        const int e = 4 * i4;
+        *reinterpret_cast<uint32_t*>(codes + (e >> 8) * 272 + (e & 255)) = q.packed;
+        if ((i4 & 7) == 0) {
+            const int b = i4 >> 3;
+            float* dp = dsc + (b >> 3) * s1 + (b & 7) * s2;
+            dp[0] = q.d;
+            dp[soff] = q.sum;
+        }
+    }
+}
+
 }  // namespace lp

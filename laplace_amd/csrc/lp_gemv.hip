@@ -469,6 +469,7 @@ struct SbmArgs {
     int K, N, M;
     const uint8_t* route;
     int max_groups, multi, topk;
+    const float* gu;      // MOE: when set, the activations are GeGLU(gu rows) quantized while staged
 };
 
 template <int L, bool MOE>
@@ -512,6 +513,13 @@ gemv_q4k_sbm(SbmArgs a) {
     const uint32_t l0 = lds_addr_of(smem);
     for (int m = 0; m < mg; m++) {
         uint8_t* ar = smem + m * act_row_bytes;
+        if constexpr (MOE) {
+            if (a.gu) {
+                stage_geglu_row(a.gu + (size_t)arow[m] * 2 * K, K, ar, reinterpret_cast<float*>(ar + nsb * 272), 8, 1,
+                                nb, threadIdx.x, blockDim.x);
+                continue;
+            }
+        }
         const int8_t* q = a.A.qs + (size_t)arow[m] * K;
         for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x)
             *reinterpret_cast<u32x4*>(ar + (i >> 4) * 272 + (i & 15) * 16) = reinterpret_cast<const u32x4*>(q)[i];
@@ -1452,10 +1460,17 @@ hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A,
     return launch_moe_grouped_routed(type, w, A, gsize, rows, P, E, multi, topk, route, y, K, N, st);
 }
 
+bool moe_geglu_fusable(uint32_t type, int K, int gsize, const uint8_t* w) {
+    if (K % 32 != 0) return false;
+    if (gsize == kRqMoeGroup) return rq_moe_supported(type, K);
+    return gsize == kMoeGroup && type == T_Q4_K && sbm_supported(K, w);
+}
+
 hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
-                                     int K, int N, hipStream_t st) {
+                                     int K, int N, hipStream_t st, const float* gu) {
     if (P <= 0 || N <= 0) return hipSuccess;
+    if (gu && !moe_geglu_fusable(type, K, gsize, w)) return hipErrorInvalidValue;
     const int mg = moe_max_groups(P, E);
     if (gsize == kMoeGroupMf) {
         if (!moe_mf_supported(type, K)) return hipErrorInvalidValue;
@@ -1463,12 +1478,12 @@ hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActV
     }
     if (gsize == kRqMoeGroup) {
         if (!rq_moe_supported(type, K)) return hipErrorInvalidValue;
-        return launch_moe_rq(w, A, route, mg, gsize, multi, topk, y, K, N, st);
+        return launch_moe_rq(w, A, route, mg, gsize, multi, topk, y, K, N, st, gu);
     }
     if (gsize != kMoeGroup) return hipErrorInvalidValue;
     if (type == T_Q4_K && sbm_supported(K, w)) {
         SbmArgs args{w, (long)row_bytes(type, K) * N, A, y, K, N, 0, static_cast<const uint8_t*>(route), mg, multi,
-                     topk};
+                     topk, gu};
         return launch_q4k_sbm(args, mg, st);
     }
     GemvGeom g;

@@ -130,13 +130,17 @@ hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A,
 // of <= gsize pairs), and the grouped products on a route table built for the
 // same pairs and group size.
 hipError_t launch_moe_route(const int* idx, int P, int E, void* route, int gsize, hipStream_t st);
+// gu (the MoE layer's down pass): the activations are GeGLU of the pairs'
+// gate|up rows (2 K floats each), quantized while the GEMV stages them, where
+// moe_geglu_fusable says the kernel for (type, K, gsize, w) does that.
 hipError_t launch_moe_grouped_routed(uint32_t type, const uint8_t* w, const ActView& A, int gsize,
                                      int rows, int P, int E, int multi, int topk, const void* route, float* y,
-                                     int K, int N, hipStream_t st);
+                                     int K, int N, hipStream_t st, const float* gu = nullptr);
+bool moe_geglu_fusable(uint32_t type, int K, int gsize, const uint8_t* w);
 // Q4_K MoE groups of <= 8 pairs on the row-quad kernel (lp_rq.hip)
 bool rq_moe_supported(uint32_t type, int K);
 hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, int max_groups, int gsize,
-                         int multi, int topk, float* y, int K, int N, hipStream_t st);
+                         int multi, int topk, float* y, int K, int N, hipStream_t st, const float* gu = nullptr);
 // dequantize (lp_dequant.hip): elements per block (0 = type not handled)
 // and source bytes of n elements.
 int dequant_block_elems(uint32_t type);

@@ -208,15 +208,7 @@ moe_topk_route_kernel(const float* __restrict__ logits, int T, int n_exp, int to
 }
 
 // hidden[p][i] = gelu_tanh(gate[p][i]) * up[p][i], gate|up = gu row p
-// (ops::geglu, src/ops.cpp:132-174: 0.5 * g * (1 + tanh(c * (g + 0.044715 g^3))))
-__device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
-#pragma clang fp contract(off)
-    const float g3 = (g * g) * g;
-    const float cst = 0.7978845608028654f;
-    const float gelu = 0.5f * g * (1.0f + tanhf(cst * (g + 0.044715f * g3)));
-    return gelu * u;
-}
-
+// (gelu_tanh_mul)
 __global__ void __launch_bounds__(256)
 geglu_kernel(const float* __restrict__ gu, int inter, long n, float* __restrict__ hidden) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;

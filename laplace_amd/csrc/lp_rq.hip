@@ -41,6 +41,7 @@
 // hit 16 distinct 16-byte bank groups: super-block q at +68q dwords, token j
 // at +16j dwords mod 64); per super-block and block the tokens' xd and xs.
 
+#include "lp_chunks.h"
 #include "lp_internal.h"
 
 namespace lp {
@@ -65,6 +66,7 @@ struct RqArgs {
     const uint8_t* route;
     long ebytes;         // bytes per expert
     int max_groups, multi, topk;
+    const float* gu;     // MOE: when set, the activations are GeGLU(gu rows) quantized while staged
 };
 
 struct RqTile {
@@ -138,18 +140,26 @@ gemv_q4k_rq(RqArgs a) {
 
     // stage the tokens' codes and block scales (zero for padding tokens)
     const int kp = K >> 4;                    // 16-byte pieces per token
+    const int mq = MOE && a.gu ? M : 0;       // rows quantized from GeGLU(gu) below
     for (int i = threadIdx.x; i < MP * kp; i += blockDim.x) {
         const int m = i / kp, c = i - m * kp;
+        if (m < mq) continue;
         u32x4 v = {0u, 0u, 0u, 0u};
         if (m < M) v = reinterpret_cast<const u32x4*>(a.A.qs + act_row(m) * K)[c];
         *reinterpret_cast<u32x4*>(sq + (size_t)m * a.tok_stride + (c >> 4) * 272 + (c & 15) * 16) = v;
     }
     for (int i = threadIdx.x; i < MP * nb; i += blockDim.x) {
         const int m = i / nb, b = i - m * nb;
+        if (m < mq) continue;
         const int o = (b >> 3) * a.sc_stride + (b & 7) * MP + m;
         const size_t r = m < M ? act_row(m) : 0;
         sxd[o] = m < M ? a.A.d[r * nb + b] : 0.0f;
         sxs[o] = m < M ? a.A.sum[r * nb + b] : 0.0f;
+    }
+    if constexpr (MOE) {
+        for (int m = 0; m < mq; m++)
+            stage_geglu_row(a.gu + act_row(m) * 2 * K, K, sq + (size_t)m * a.tok_stride, sxd + m, a.sc_stride, MP,
+                            nsb * a.sc_stride, threadIdx.x, blockDim.x);
     }
     __syncthreads();
 
@@ -373,7 +383,7 @@ hipError_t launch_gemv_rq(const uint8_t* w, const ActView& A, float* y, int M, i
 bool rq_moe_supported(uint32_t type, int K) { return rq_supported(type, kRqMoeGroup, K, 1, nullptr); }
 
 hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, int max_groups, int gsize,
-                         int multi, int topk, float* y, int K, int N, hipStream_t st) {
+                         int multi, int topk, float* y, int K, int N, hipStream_t st, const float* gu) {
     if (N <= 0 || max_groups <= 0) return hipSuccess;
     if (!rq_supported(T_Q4_K, kRqMoeGroup, K, N, w)) return hipErrorInvalidValue;
     RqArgs a{};
@@ -389,6 +399,7 @@ hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, 
     a.max_groups = max_groups;
     a.multi = multi;
     a.topk = topk;
+    a.gu = gu;
     if (gsize != kRqMoeGroup) return hipErrorInvalidValue;
     return launch_rq<true>(a, 2, max_groups, st);
 }

@@ -36,6 +36,9 @@ def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed):
 @pytest.mark.parametrize("T,H,n_exp,top_k,inter,gu_t,dn_t,router_t", [
     (1, 512, 16, 4, 256, Q4_K, Q4_K, F32),
     (4, 512, 32, 8, 256, Q4_K, Q6_K, F32),
+    # 32 pairs over 8 experts: both passes on the row-quad group kernel, the
+    # down pass quantizing GeGLU(gate|up) while it stages its activations
+    (4, 512, 8, 8, 256, Q4_K, Q4_K, F32),
     (7, 1024, 64, 2, 512, Q8_0, Q4_0, Q8_0),
     # Gemma4 26B layer shape (tests/bench_cpu_gpu.cpp:55-57): H 2816, 128
     # experts, top-8, expert inter 704 (down K = 704: a Q8_0 tensor)
