@@ -193,7 +193,10 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False, 
     nbws = int(g.L.lp_act_workspace_bytes(M, K))
     ws = torch.empty(nbws, dtype=torch.uint8, device=g.dev)
     alg_bytes = w.nbytes + 4 * M * K + 4 * M * N
-    fused = (t in (Q4_K, Q4_0, Q8_0) and M == 1 and K % 256 == 0 and K // 256 <= 64)
+    # the library's fused M = 1 path (gemv_fused_supported): one launch that
+    # quantizes x itself
+    fused = (t in (Q4_K, Q4_0, Q8_0) and M == 1 and K % 256 == 0 and K // 256 <= 64
+             and not (t in (Q4_K, Q8_0) and K >= 12288))
 
     def step(i):
         g.check(g.L.lp_gemm_dev(xd.data_ptr(), ws_list[i % ncp].data_ptr(), t, y.data_ptr(),

@@ -1282,8 +1282,14 @@ static bool sbm_supported(int K, const uint8_t* w) {
            (size_t)kSbmMaxM * ((nsb * 272 + 8 * (K / 32) + 15) & ~15) + (size_t)kSbmWaves * 9216 <= 160 * 1024;
 }
 
+// Quantizing x inside the GEMV saves a launch but every workgroup redoes it;
+// from K = 12288 the separate quantize kernel measured faster for Q4_K and
+// Q8_0 (us, fused vs quantize + GEMV: Q4_K 4096x14336 17.7 / 12.7, 2048x16384
+// 10.2 / 8.5; Q8_0 4096x14336 22.3 / 16.7), not for Q4_0 (4096x14336 12.0 /
+// 12.6) nor below (Q4_K 4096x11008 10.0 / 11.7, 14336x4096 8.2 / 10.2).
 bool gemv_fused_supported(uint32_t type, int M, int K, const uint8_t* w) {
     if (M != 1) return false;
+    if ((type == T_Q4_K || type == T_Q8_0) && K >= 12288) return false;
     if (type == T_Q4_K) return sb_lanes(K) != 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
     return b32_sb_supported(type, K, w);
 }
