@@ -367,7 +367,12 @@ bool q6rq_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
 }
 
 bool q6rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w) {
-    return q6rq_supported(type, M, K, N, w) && M >= 3;
+    // M = 1, 2 only in one chunk: the dot4 kernel (gemv_q6k_sbm) is faster
+    // at long K there (us, 3584x18944: M=1 18.0 vs 21.1; M=2 21.2 vs 21.6
+    // unsplit, 20.3 split; 4096x14336 M=2 16.3 vs 18.2 split), slower in one
+    // chunk (4096x4096 M=1 7.9 vs 6.9, M=2 9.5 vs 7.0; 14336x4096 M=1 15.3 vs
+    // 14.1, M=2 19.1 vs 14.8)
+    return q6rq_supported(type, M, K, N, w) && (M >= 3 || K <= 4096);
 }
 
 hipError_t launch_gemv_q6rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {

@@ -1,4 +1,4 @@
-"""Q6_K at 3..8 activation rows on the row-quad int8 MFMA kernel
+"""Q6_K at 3..8 activation rows (1..2 when K <= 4096) on the row-quad int8 MFMA kernel
 (lp_q6rq.hip: 4x4x4 int8 blocks, a weight row quad per wave, K in chunks of
 16 super-blocks) against the oracle's gemm_int (dot_row_q6_k_int,
 src/matmul_simd.cpp:285-342): both token groups, K from one super-block
@@ -30,6 +30,19 @@ def test_q6rq(orc, K, N, M):
     ref = orc.gemm_int(Q6_K, x, w, N)
     assert np.isfinite(y).all()
     assert normwise(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N", [(1, 7), (1, 4096), (2, 130), (2, 1001)])
+@pytest.mark.parametrize("K", [256, 3584, 4096])
+def test_q6rq_one_two_rows(orc, K, N, M):
+    """One and two activation rows in one chunk (K <= 4096) also run here."""
+    print(f"q6rq Q6_K M={M} K={K} N={N}", flush=True)
+    from hip_util import L, to_dev
+    w = synth_weights(Q6_K, K, N, seed=K + 5 * N + M)
+    assert L().lp_gemm_route(Q6_K, M, K, N, to_dev(w).data_ptr()).decode() == "q6rq"
+    x = synth_x(M, K, seed=M * 7 + 3, outliers=0.01)
+    y = gemm_dev(Q6_K, x, w, N)
+    assert normwise(y, orc.gemm_int(Q6_K, x, w, N)) <= TOL
 
 
 def test_q6rq_config3(orc):
