@@ -49,7 +49,7 @@ namespace lp {
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-constexpr int kRqWaves = 4;
+constexpr int kRqWaves = 4;      // waves per workgroup (8 for large dense two-group products)
 constexpr int kRqMaxSb = 16;
 
 struct RqArgs {
@@ -74,8 +74,8 @@ struct RqTile {
     u32x4 c[8];          // codes: bytes 16 i .. 16 i + 15
 };
 
-template <int TG, int S, bool MOE>
-__global__ void __launch_bounds__(64 * kRqWaves)
+template <int TG, int S, bool MOE, int W = kRqWaves>
+__global__ void __launch_bounds__(64 * W)
 gemv_q4k_rq(RqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int MP = 4 * TG;
@@ -113,7 +113,7 @@ gemv_q4k_rq(RqArgs a) {
     const int sbq = qv ? sq_raw : nsb - 1;
     const int tga = (M + 3) >> 2;             // token groups in use
 
-    const long gw = (long)blockIdx.x * kRqWaves + __builtin_amdgcn_readfirstlane(wave);
+    const long gw = (long)blockIdx.x * W + __builtin_amdgcn_readfirstlane(wave);
     const long u0 = gw * a.per_wave;
     const long u1 = u0 + a.per_wave < a.nunits ? u0 + a.per_wave : a.nunits;
     const uint32_t lane_off = (uint32_t)((4 * sub + j) * a.rb + sbq * 144);
@@ -344,10 +344,19 @@ static hipError_t launch_rq(const RqArgs& a0, int TG, int groups, hipStream_t st
         const long target = (long)device_cu_count() * (TG == 1 ? 12 : 8);
         a.per_wave = (int)((a.nunits + target - 1) / target);
     }
+    // Two token groups over many rows: 8-wave workgroups (one per CU at the
+    // 8-waves target), whose activation staging serves twice the waves
+    // (us, 4 vs 8 waves: 18944x3584 M=5 17.7 / 16.6, M=8 18.8 / 17.2;
+    // 14336x4096 M=5 16.5 / 15.7, M=8 16.9 / 16.2; but 4096x4096 M=8 9.2 /
+    // 9.6, and one token group mixed: 18944x3584 M=4 14.3 / 17.8)
+    const int W = (!MOE && TG == 2 && a.N >= 8192) ? 8 : kRqWaves;
     const long waves = (a.nunits + a.per_wave - 1) / a.per_wave;
-    const dim3 grid((unsigned)((waves + kRqWaves - 1) / kRqWaves), (unsigned)groups);
+    const dim3 grid((unsigned)((waves + W - 1) / W), (unsigned)groups);
     const size_t shm = rq_lds(4 * TG, a.K);
-#define LP_RQ(TGV, SV) hipLaunchKernelGGL((gemv_q4k_rq<TGV, SV, MOE>), grid, dim3(64 * kRqWaves), shm, st, a)
+#define LP_RQ(TGV, SV)                                                                                        \
+    if (W == 8) hipLaunchKernelGGL((gemv_q4k_rq<TGV, SV, MOE, (TGV == 2 && !MOE) ? 8 : kRqWaves>), grid,         \
+                                   dim3(64 * W), shm, st, a);                                                 \
+    else hipLaunchKernelGGL((gemv_q4k_rq<TGV, SV, MOE>), grid, dim3(64 * kRqWaves), shm, st, a)
 #define LP_RQS(TGV)                     \
     switch (S) {                        \
         case 1: LP_RQ(TGV, 1); break;   \
