@@ -8,12 +8,20 @@
 // scales, I = sc_0 * S_0 + sc_1 * S_1 (exact), and the block adds
 // xd_mb * I in fp32; d_n multiplies once per super-block.
 //
-// Layout: a wave owns one row quad (4 consecutive weight rows) and all of
-// K, in chunks of 16 super-blocks (4096 elements). Lane l = 4q + j: weight
-// row j of the quad, super-block 16c + q of chunk c. Each lane loads its
-// super-block (210 bytes, 2-byte aligned) as 52 dwords from the dword at or
-// below its start plus one more dword and the 16-bit d, and funnel-shifts it.
-//
+// Layout: K in chunks of 16 super-blocks (4096 elements); a wave owns one
+// row quad (4 consecutive weight rows). Lane l = 4q + j: weight row j of the
+// quad, super-block 16c + q of chunk c.
+//   One chunk per workgroup (COAL = false): K <= 4096, or K split over the
+//   grid's second dimension with the chunks' partial sums in the caller's
+//   workspace scratch, added in chunk order by q6rq_reduce. Each lane loads
+//   its super-block (210 bytes, 2-byte aligned) as 52 dwords from the dword
+//   at or below its start plus one more dword and the 16-bit d, and
+//   funnel-shifts it.
+//   Chunk loop (COAL = true, long K without scratch): the wave copies its
+//   quad's chunk with coalesced 16-byte loads into its own LDS region and
+//   each lane reads its super-block back; the next chunk's copy is requested
+//   before this one is computed.
+
 // v_mfma_i32_4x4x4_16b_i8 is 16 independent 4x4x4 products; block q of the
 // instruction is lane quad q: A row i = lane 4q+i (token i's four codes),
 // B column j = lane 4q+j (row j's four 6-bit codes), D[q][i][j] in lane
@@ -21,11 +29,10 @@
 // 4 rows x 16 super-blocks; the accumulator starts at -32 * (the token's
 // 16-element code sum), so the chain ends at the reference's integer term.
 //
-// The workgroup's waves share the tokens' codes of the current chunk in LDS
-// (double-buffered: the next chunk's codes are loaded into registers while
-// this one is computed, written after it, one barrier per chunk), together
-// with per block the tokens' xd and the two -32 * code sums. The lane's next
-// super-block tile is loaded before the current one is computed. At the end
+// The workgroup's waves share the tokens' codes of the chunk in LDS,
+// together with per block the tokens' xd and the two -32 * code sums (the
+// chunk loop double-buffers them: the next chunk's are loaded into
+// registers while this one is computed, one barrier per chunk). At the end
 // the 16 super-block lanes of each row are added with cross-lane shuffles in
 // fixed order, spreading the 4 tokens of a group over the lanes on the way.
 //
