@@ -449,6 +449,170 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
     }
 }
 
+// One lane's Q4_K super-block (v: its 144 bytes) against the activation
+// codes of the same super-block at LDS address act_l (272-byte stride layout
+// of gemv_q4k_sb): 64 v_dot4 on unpacked nibbles and the eight fp32 block
+// terms in the reference's order (src/matmul_simd.cpp:226-283).
+__device__ __forceinline__ float q4k_sb_dot(const u32x4 (&v)[9], uint32_t act_l, const float (&xd)[8],
+                                            const float (&xs)[8]) {
+    const u32x4 h = v[0];
+    const float d = fp16_bits_to_f32(h.x), dmin = fp16_bits_to_f32(h.x >> 16);
+    float t = 0.0f;
+#pragma unroll
+    for (int jb = 0; jb < 4; jb++) {
+        const u32x4 c0 = v[1 + 2 * jb], c1 = v[2 + 2 * jb];
+        const uint32_t qv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        u32x4 lo0, lo1, hi0, hi1;
+        const uint32_t la = act_l + 64 * jb;
+        lds_b128<0>(lo0, la);
+        lds_b128<16>(lo1, la);
+        lds_b128<32>(hi0, la);
+        lds_b128<48>(hi1, la);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_wait_v(lo0);
+        lds_wait_v(lo1);
+        lds_wait_v(hi0);
+        lds_wait_v(hi1);
+        const uint32_t al[8] = {lo0.x, lo0.y, lo0.z, lo0.w, lo1.x, lo1.y, lo1.z, lo1.w};
+        const uint32_t ah[8] = {hi0.x, hi0.y, hi0.z, hi0.w, hi1.x, hi1.y, hi1.z, hi1.w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s0 = dot4(qv[i] & 0x0f0f0f0fu, al[i], s0);
+            s1 = dot4((qv[i] >> 4) & 0x0f0f0f0fu, ah[i], s1);
+        }
+        uint32_t sc0, m0, sc1, m1;
+        scale_min_k4(2 * jb, h.y, h.z, h.w, sc0, m0);
+        scale_min_k4(2 * jb + 1, h.y, h.z, h.w, sc1, m1);
+        t = fmaf((d * (float)sc0) * xd[2 * jb], (float)s0, t);
+        t = fmaf((d * (float)sc1) * xd[2 * jb + 1], (float)s1, t);
+        t = fmaf(-(dmin * (float)m0), xs[2 * jb], t);
+        t = fmaf(-(dmin * (float)m1), xs[2 * jb + 1], t);
+    }
+    return t;
+}
+
+// Q4_K GEMV for one activation row, flat super-block mapping. A workgroup
+// owns `rpw` whole consecutive rows, i.e. rpw * nsb consecutive super-blocks
+// (one contiguous, 16-byte aligned byte range); wave w takes the 64-super-block
+// segments w, w + W, ... of that range (at most two), each one 9216 bytes
+// loaded with fully coalesced 16-byte loads and transposed through the wave's
+// LDS buffer, so lane l holds super-block 64s + l whatever row it falls in: no
+// lane idles when nsb is not a power of two and the wave count follows the
+// bytes, not the rows. A lane's sum goes to LDS; a row's nsb sums are then added on
+// L lanes with the DPP tree of gemv_q4k_sb, so the rows are bit-identical to
+// that kernel's (and to its multi-matrix form). Activations as in gemv_q4k_sb
+// (FUSEQ: quantized by the workgroup, half of the waves requesting their
+// first segment meanwhile).
+template <bool FUSEQ>
+__global__ void __launch_bounds__(1024)
+gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
+              int K, int N, int rpw) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsb = K >> 8;
+    const int nb = K >> 5;
+    const long rb = (long)nsb * 144;
+    const long total = (long)N * rb;
+    const int r0 = blockIdx.x * rpw;
+    const int nrows = min(rpw, N - r0);
+    const int F = nrows * nsb;                    // super-blocks of this workgroup
+    const int nseg = (F + 63) >> 6;
+    const long base = (long)r0 * rb;
+    float* dl = reinterpret_cast<float*>(smem + nsb * 272);
+    float* sl_ = dl + nb;
+    const int xbuf_off = (nsb * 272 + 8 * nb + 15) & ~15;
+    uint8_t* wbuf = smem + xbuf_off + (size_t)wv * 9216;
+
+    auto load_seg = [&](int s, u32x4 (&v)[9]) {
+        const long gbeg = base + (long)s * 9216;
+#pragma unroll
+        for (int k = 0; k < 9; k++) {
+            long a = gbeg + 1024 * k + 16 * lane;
+            a = a + 16 <= total ? a : total - 16;
+            v[k] = ld_nt16(w + a);
+        }
+    };
+    int s = wv;
+    u32x4 v[9];
+    if constexpr (FUSEQ) {
+        const int nq = nw >= 8 ? 64 * (nw / 2) : (int)blockDim.x;
+        const bool early = (int)threadIdx.x >= nq;
+        if (early && s < nseg) load_seg(s, v);
+        if (!early) {
+            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
+                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
+                const int b = i >> 3, gq = i & 7;
+                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+                if (gq == 0) {
+                    dl[b] = q.d;
+                    sl_[b] = q.sum;
+                }
+            }
+        }
+        __syncthreads();
+        if (!early && s < nseg) load_seg(s, v);
+    } else {
+        if (s < nseg) load_seg(s, v);
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+            const u32x4 c = reinterpret_cast<const u32x4*>(A.qs)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = c;
+        }
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+            dl[i] = A.d[i];
+            sl_[i] = A.sum[i];
+        }
+        __syncthreads();
+    }
+    const uint32_t act0 = lds_addr_of(smem);
+    float part0 = 0.0f, part1 = 0.0f;
+#pragma unroll 1
+    for (int r = 0; r < 2 && s < nseg; r++) {
+        // a second segment (only where segments outnumber waves) is requested
+        // after the first is computed: two in registers would spill
+        if (r == 1) load_seg(s, v);
+#pragma unroll
+        for (int k = 0; k < 9; k++) *reinterpret_cast<u32x4*>(wbuf + 1024 * k + 16 * lane) = v[k];
+        const u32x4* mine = reinterpret_cast<const u32x4*>(wbuf + (size_t)lane * 144);
+#pragma unroll
+        for (int k = 0; k < 9; k++) v[k] = mine[k];
+        const int f = 64 * s + lane;
+        const int sb = f - (f / nsb) * nsb;
+        float xd[8], xs[8];
+        const float4* dp = reinterpret_cast<const float4*>(dl + 8 * sb);
+        const float4* sp = reinterpret_cast<const float4*>(sl_ + 8 * sb);
+        const float4 d0 = dp[0], d1 = dp[1], q0 = sp[0], q1 = sp[1];
+        xd[0] = d0.x; xd[1] = d0.y; xd[2] = d0.z; xd[3] = d0.w;
+        xd[4] = d1.x; xd[5] = d1.y; xd[6] = d1.z; xd[7] = d1.w;
+        xs[0] = q0.x; xs[1] = q0.y; xs[2] = q0.z; xs[3] = q0.w;
+        xs[4] = q1.x; xs[5] = q1.y; xs[6] = q1.z; xs[7] = q1.w;
+        const float t = q4k_sb_dot(v, act0 + sb * 272, xd, xs);
+        if (r == 0) part0 = t;
+        else part1 = t;
+        s += nw;
+    }
+    // every wave is past its transpose buffer: partial sums over them
+    __syncthreads();
+    float* ps = reinterpret_cast<float*>(smem + xbuf_off);
+    const int f0 = 64 * wv + lane, f1 = f0 + 64 * nw;
+    if (f0 < F) ps[f0] = part0;
+    if (f1 < F) ps[f1] = part1;
+    __syncthreads();
+    // a row's sums on L lanes (zeros past nsb) and the DPP tree of
+    // gemv_q4k_sb: the same bits as that kernel's rows
+    const int L = nsb <= 2 ? 2 : 1 << (32 - __builtin_clz(nsb - 1));
+    const int tot = nrows * L;
+    for (int e0 = 64 * wv; e0 < tot; e0 += 64 * nw) {
+        const int e = e0 + lane;
+        const int row = e / L, l = e & (L - 1);
+        const float t = e < tot && l < nsb ? ps[row * nsb + l] : 0.0f;
+        const float sum = group_sum(t, L);
+        if (l == L - 1 && e < tot) y[r0 + row] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K GEMV for 2..4 activation rows (and grouped MoE, groups of <= 4 pairs)
 // with the one-super-block-per-lane layout of gemv_q4k_sb: the weight bytes
@@ -1125,6 +1289,57 @@ static int sb_lanes(int K) {
     return L;
 }
 
+// Geometry of gemv_q4k_flat for (K, N): rows per workgroup and waves per
+// workgroup (false: not this kernel). Rows are spread over one workgroup per
+// CU; a wave takes at most two 64-super-block segments.
+static bool q4k_flat_geom(int K, int N, int& rpw, int& nw) {
+    if (K % 256 != 0 || N <= 0) return false;
+    const int nsb = K / 256;
+    if (nsb > 64) return false;
+    const size_t act_lds = ((size_t)nsb * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
+    int fit = (int)((160 * 1024 - act_lds) / 9216);
+    if (fit > 16) fit = 16;
+    if (fit < 1) return false;
+    const int cus = device_cu_count();
+    rpw = (N + cus - 1) / cus;
+    long nseg = ((long)rpw * nsb + 63) / 64;
+    if (nseg > 2L * fit) {
+        rpw = (int)(2L * fit * 64 / nsb);
+        if (rpw < 1) return false;
+        nseg = ((long)rpw * nsb + 63) / 64;
+    }
+    nw = nseg <= fit ? (int)nseg : fit;
+    return true;
+}
+
+static hipError_t launch_q4k_flat(const uint8_t* w, const ActView& A, const float* x, float* y, int K, int N,
+                                  hipStream_t st) {
+    int rpw, nw;
+    if (!q4k_flat_geom(K, N, rpw, nw)) return hipErrorInvalidValue;
+    const size_t act_lds = ((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
+    const size_t shm = act_lds + (size_t)nw * 9216;
+    const unsigned grid = (unsigned)((N + rpw - 1) / rpw);
+    if (x) hipLaunchKernelGGL((gemv_q4k_flat<true>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw);
+    else hipLaunchKernelGGL((gemv_q4k_flat<false>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw);
+    return hipGetLastError();
+}
+
+// Where gemv_q4k_sb's row groups exceed its resident waves (a second round
+// for some waves) and the flat kernel's segments fit in about one round. Both
+// kernels, quantization fused (us): 18944x3584 12.6-12.9 / 10.9; where the
+// row groups fit one round the flat kernel is slower (fewer waves per CU, so
+// fewer bytes in flight, and ~0.7 us for its row-sum pass): 14336x4096 8.3 /
+// 10.0, 4096x11008 10.4 / 12.7, 2048x2816 6.6 / 6.8; and at many rounds
+// (262144x2816 72.8 / 76.3).
+static bool q4k_flat_preferred(int K, int N) {
+    const int L = sb_lanes(K);
+    int rpw, nw;
+    if (!L || !q4k_flat_geom(K, N, rpw, nw)) return false;
+    const long groups = ((long)N + 64 / L - 1) / (64 / L);
+    const long nseg = ((long)rpw * (K / 256) + 63) / 64;
+    return groups > (long)device_cu_count() * 16 && nseg <= nw + 1;
+}
+
 // x != nullptr: quantize fp32 x in the kernel (A unused).
 // Defaults from measurement on MI355X (Q4_K 14336 x 4096): 16 waves per CU;
 // one 16-wave workgroup per CU when it quantizes x itself (the quantization
@@ -1132,6 +1347,7 @@ static int sb_lanes(int K) {
 template <bool XPOSE = true>
 static hipError_t launch_q4k_sb(const uint8_t* w, const ActView& A, const float* x, float* y, int K,
                                 int N, hipStream_t st, int waves_per_cu = 16, int wg_waves = 0) {
+    if (XPOSE && q4k_flat_preferred(K, N)) return launch_q4k_flat(w, A, x, y, K, N, st);
     if (wg_waves <= 0) wg_waves = x ? 16 : 8;
     const size_t act_lds = ((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
     if (XPOSE) {
@@ -1346,7 +1562,8 @@ const char* gemv_route_name(uint32_t type, int M, int K, int N, const uint8_t* w
     if (type == T_Q6_K && q6k_sbm_supported(K, M, w)) return "q6k_sbm";
     if (type == T_Q4_K && rq_preferred(type, M, K, N, w)) return "rq";
     if (M == 1) {
-        if (type == T_Q4_K && sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0) return "sb";
+        if (type == T_Q4_K && sb_lanes(K) && reinterpret_cast<uintptr_t>(w) % 16 == 0)
+            return q4k_flat_preferred(K, N) ? "flat" : "sb";
         if ((type == T_Q4_0 || type == T_Q8_0) && b32_sb_supported(type, K, w)) return "b32_sb";
         return "tile";
     }
