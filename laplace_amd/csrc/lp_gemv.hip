@@ -1110,6 +1110,43 @@ __device__ __forceinline__ void q6_sb_dot(const uint32_t (&raw)[53], uint32_t sh
     }
 }
 
+// One lane's Q6_K super-block at blk (2-byte aligned): 13 16-byte loads from
+// the dword at or below it, the dword holding bytes 206..209 only when the
+// block starts 2 bytes into a dword (else dword 51 again, so no load passes
+// the block's end), and d with a 16-bit load. Untracked loads: the caller
+// waits with q6_wait_sb before using any of them.
+__device__ __forceinline__ void q6_load_sb(const uint8_t* blk, u32x4 (&rw)[13], uint32_t& tail, uint32_t& dh,
+                                           uint32_t& sh) {
+    const uintptr_t ab = reinterpret_cast<uintptr_t>(blk);
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(ab & ~uintptr_t(3));
+    sh = (uint32_t)(ab & 3);                              // 0 or 2
+    asm volatile(
+        "global_load_dwordx4 %0, %13, off\n"
+        "global_load_dwordx4 %1, %13, off offset:16\n"
+        "global_load_dwordx4 %2, %13, off offset:32\n"
+        "global_load_dwordx4 %3, %13, off offset:48\n"
+        "global_load_dwordx4 %4, %13, off offset:64\n"
+        "global_load_dwordx4 %5, %13, off offset:80\n"
+        "global_load_dwordx4 %6, %13, off offset:96\n"
+        "global_load_dwordx4 %7, %13, off offset:112\n"
+        "global_load_dwordx4 %8, %13, off offset:128\n"
+        "global_load_dwordx4 %9, %13, off offset:144\n"
+        "global_load_dwordx4 %10, %13, off offset:160\n"
+        "global_load_dwordx4 %11, %13, off offset:176\n"
+        "global_load_dwordx4 %12, %13, off offset:192\n"
+        : "=&v"(rw[0]), "=&v"(rw[1]), "=&v"(rw[2]), "=&v"(rw[3]), "=&v"(rw[4]), "=&v"(rw[5]), "=&v"(rw[6]),
+          "=&v"(rw[7]), "=&v"(rw[8]), "=&v"(rw[9]), "=&v"(rw[10]), "=&v"(rw[11]), "=&v"(rw[12])
+        : "v"(base));
+    asm volatile("global_load_dword %0, %1, off" : "=v"(tail) : "v"(base + (sh ? 208 : 204)));
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(dh) : "v"(blk + 208));
+}
+__device__ __forceinline__ void q6_wait_sb(u32x4 (&rw)[13], uint32_t& tail, uint32_t& dh) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 13; k++) asm volatile("" : "+v"(rw[k]));
+    asm volatile("" : "+v"(tail), "+v"(dh));
+}
+
 template <int L, int M>
 __global__ void __launch_bounds__(64 * kQ6Waves)
 gemv_q6k_sbm(const uint8_t* __restrict__ w, ActView A, int arow0, float* __restrict__ y, int K, int N) {
@@ -1130,40 +1167,8 @@ gemv_q6k_sbm(const uint8_t* __restrict__ w, ActView A, int arow0, float* __restr
     uint32_t tail, dh, sh, l0 = 0;
     long g = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     auto row_of = [&](long gg) { const long r = gg * RPW + rsub; return r < N ? r : (long)N - 1; };
-    // Untracked loads: the caller waits with s_waitcnt vmcnt(0) and fences the registers.
-    auto load = [&](long row, int sb) {
-        const uint8_t* blk = w + row * rb + (long)sb * 210;
-        const uintptr_t ab = reinterpret_cast<uintptr_t>(blk);
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(ab & ~uintptr_t(3));
-        sh = (uint32_t)(ab & 3);                              // 0 or 2
-        asm volatile(
-            "global_load_dwordx4 %0, %13, off\n"
-            "global_load_dwordx4 %1, %13, off offset:16\n"
-            "global_load_dwordx4 %2, %13, off offset:32\n"
-            "global_load_dwordx4 %3, %13, off offset:48\n"
-            "global_load_dwordx4 %4, %13, off offset:64\n"
-            "global_load_dwordx4 %5, %13, off offset:80\n"
-            "global_load_dwordx4 %6, %13, off offset:96\n"
-            "global_load_dwordx4 %7, %13, off offset:112\n"
-            "global_load_dwordx4 %8, %13, off offset:128\n"
-            "global_load_dwordx4 %9, %13, off offset:144\n"
-            "global_load_dwordx4 %10, %13, off offset:160\n"
-            "global_load_dwordx4 %11, %13, off offset:176\n"
-            "global_load_dwordx4 %12, %13, off offset:192\n"
-            : "=&v"(rw[0]), "=&v"(rw[1]), "=&v"(rw[2]), "=&v"(rw[3]), "=&v"(rw[4]), "=&v"(rw[5]), "=&v"(rw[6]),
-              "=&v"(rw[7]), "=&v"(rw[8]), "=&v"(rw[9]), "=&v"(rw[10]), "=&v"(rw[11]), "=&v"(rw[12])
-            : "v"(base));
-        // dword 52 (block bytes 206..209) only when the block starts at byte 2 of a dword;
-        // else dword 51 again, so no load passes the block's end
-        asm volatile("global_load_dword %0, %1, off" : "=v"(tail) : "v"(base + (sh ? 208 : 204)));
-        asm volatile("global_load_ushort %0, %1, off" : "=v"(dh) : "v"(blk + 208));
-    };
-    auto wait_load = [&]() {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int k = 0; k < 13; k++) asm volatile("" : "+v"(rw[k]));
-        asm volatile("" : "+v"(tail), "+v"(dh));
-    };
+    auto load = [&](long row, int sb) { q6_load_sb(w + row * rb + (long)sb * 210, rw, tail, dh, sh); };
+    auto wait_load = [&]() { q6_wait_sb(rw, tail, dh); };
     auto dot = [&](int sb, float (&t)[M]) {
         uint32_t raw[53];
 #pragma unroll
@@ -1218,6 +1223,185 @@ gemv_q6k_sbm(const uint8_t* __restrict__ w, ActView A, int arow0, float* __restr
             if (sl == L - 1 && rv) y[(size_t)m * N + row] = sum;
         }
     }
+}
+
+// q6_sb_dot for one activation row with fewer LDS reads in flight (a
+// 32-element block's codes at a time): the same integer sums and fp32 terms
+// in the same order, in fewer registers (for 16-wave workgroups).
+__device__ __forceinline__ float q6_sb_dot1(const uint32_t (&raw)[53], uint32_t sh, float d, int sb, uint32_t l0,
+                                            int nsb, int nb) {
+    uint32_t wd[52];
+#pragma unroll
+    for (int k = 0; k < 52; k++) wd[k] = alignb(raw[k + 1], raw[k], sh);
+    float u = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const uint32_t la = l0 + sb * 272 + 128 * n;
+        const uint32_t ld = l0 + nsb * 272 + 32 * sb + 16 * n;
+        const uint32_t lq = l0 + nsb * 272 + 4 * nb + 64 * sb + 32 * n;
+        u32x4 dv, q0, q1;
+        lds_b128<0>(dv, ld);
+        lds_b128<0>(q0, lq);
+        lds_b128<16>(q1, lq);
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+            u32x4 a0, a1;
+            lds_b128<0>(a0, la + 32 * gg);
+            lds_b128<16>(a1, la + 32 * gg);
+            uint32_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t ql = wd[16 * n + 8 * (gg & 1) + k];
+                const uint32_t qh = wd[32 + 8 * n + k];
+                v[k] = ((ql >> (4 * (gg >> 1))) & 0x0f0f0f0fu) | (((qh >> (2 * gg)) & 0x03030303u) << 4);
+            }
+            const int si = 8 * n + 2 * gg;
+            const float sc0 = (float)(int8_t)((wd[48 + (si >> 2)] >> (8 * (si & 3))) & 0xffu);
+            const float sc1 = (float)(int8_t)((wd[48 + ((si + 1) >> 2)] >> (8 * ((si + 1) & 3))) & 0xffu);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_wait_v(dv); lds_wait_v(q0); lds_wait_v(q1); lds_wait_v(a0); lds_wait_v(a1);
+            const float xd[4] = {__uint_as_float(dv.x), __uint_as_float(dv.y), __uint_as_float(dv.z),
+                                 __uint_as_float(dv.w)};
+            const uint32_t qs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            int s0 = 0, s1 = 0;
+            s0 = dot4(v[0], a0.x, s0); s0 = dot4(v[1], a0.y, s0);
+            s0 = dot4(v[2], a0.z, s0); s0 = dot4(v[3], a0.w, s0);
+            s1 = dot4(v[4], a1.x, s1); s1 = dot4(v[5], a1.y, s1);
+            s1 = dot4(v[6], a1.z, s1); s1 = dot4(v[7], a1.w, s1);
+            s0 -= 32 * (int)qs[2 * gg];
+            s1 -= 32 * (int)qs[2 * gg + 1];
+            const float dx = d * xd[gg];
+            u = fmaf(dx * sc0, (float)s0, u);
+            u = fmaf(dx * sc1, (float)s1, u);
+            // the block's arithmetic completes before the next block's LDS
+            // reads (volatile, so ordered after this): otherwise the compiler
+            // sinks it below all of them and holds every read in registers
+            asm volatile("" : "+v"(u));
+        }
+    }
+    return u;
+}
+
+// Q6_K GEMV for one activation row, flat super-block mapping (the layout of
+// gemv_q4k_flat with per-lane loads): a workgroup owns `rpw` whole rows, lane
+// l of wave w takes super-block 64 (w + r nw) + l of them in round r, loads it
+// as gemv_q6k_sbm does (all of a round's loads issued together) and dots it
+// with the activation row in LDS (same layout and arithmetic as
+// gemv_q6k_sbm, q6_sb_dot1); the lanes' sums go to LDS and each row's nsb sums are added
+// by one wave (lane-strided, then a DPP tree).
+__global__ void __launch_bounds__(1024)
+gemv_q6k_flat(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int K, int N, int rpw) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsb = K >> 8, nb = K >> 5;
+    const long rb = (long)nsb * 210;
+    const int r0 = blockIdx.x * rpw;
+    const int nrows = min(rpw, N - r0);
+    const int F = nrows * nsb;
+    const int nseg = (F + 63) >> 6;
+    const uint8_t* base = w + (long)r0 * rb;
+    const int arb = (nsb * 272 + 12 * nb + 15) & ~15;
+    float* ps = reinterpret_cast<float*>(smem + arb);
+    u32x4 rw[13];
+    uint32_t tail, dh, sh;
+    int s = wv;
+    auto load = [&](int seg) {
+        int f = 64 * seg + lane;
+        f = f < F ? f : F - 1;
+        q6_load_sb(base + (long)f * 210, rw, tail, dh, sh);
+    };
+    // the first segment's loads (unconditional: indices are clamped) overlap
+    // the activation staging; every load is waited for in straight-line
+    // code before any control-flow merge, so no register still in flight is
+    // copied
+    load(s);
+    {
+        const int8_t* q = A.qs;
+        for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(q)[i];
+            *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = v;
+            const uint32_t qv[4] = {v.x, v.y, v.z, v.w};
+            int qs16 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs16 = dot4(qv[k], 0x01010101u, qs16);
+            reinterpret_cast<int*>(smem + nsb * 272 + 4 * nb)[i] = qs16;
+        }
+        float* dl = reinterpret_cast<float*>(smem + nsb * 272);
+        for (int b = threadIdx.x; b < nb; b += blockDim.x) dl[b] = A.d[b];
+    }
+    __syncthreads();
+    q6_wait_sb(rw, tail, dh);
+    const uint32_t l0 = lds_addr_of(smem);
+    auto compute = [&](int seg) {
+        const int f = 64 * seg + lane;
+        const int sb = f - (f / nsb) * nsb;
+        uint32_t raw[53];
+#pragma unroll
+        for (int k = 0; k < 13; k++) {
+            raw[4 * k] = rw[k].x; raw[4 * k + 1] = rw[k].y; raw[4 * k + 2] = rw[k].z; raw[4 * k + 3] = rw[k].w;
+        }
+        raw[52] = tail;
+        const float t = q6_sb_dot1(raw, sh, fp16_bits_to_f32((uint16_t)dh), sb, l0, nsb, nb);
+        if (f < F) ps[f] = t;
+    };
+    if (s < nseg) compute(s);
+    for (s += nw; s < nseg; s += nw) {
+        load(s);
+        q6_wait_sb(rw, tail, dh);
+        compute(s);
+    }
+    __syncthreads();
+    for (int r = wv; r < nrows; r += nw) {
+        float t = 0.0f;
+        for (int j = lane; j < nsb; j += 64) t += ps[r * nsb + j];
+        t = group_sum(t, 64);
+        if (lane == 63) y[r0 + r] = t;
+    }
+}
+
+// Rows per workgroup and waves for gemv_q6k_flat: one workgroup per CU, up
+// to 16 waves, segments beyond that in further rounds (two workgroups per CU
+// of up to 10 waves, all resident at 97 VGPRs, measured slower: 3584x18944
+// 20.6 against 18.5 us).
+static bool q6k_flat_geom(int K, int N, int& rpw, int& nw) {
+    if (K % 256 != 0 || N <= 0) return false;
+    const int nsb = K / 256, nb = K / 32;
+    const size_t arb = ((size_t)nsb * 272 + 12 * (size_t)nb + 15) & ~size_t(15);
+    const int cus = device_cu_count();
+    rpw = (N + cus - 1) / cus;
+    const long nseg = ((long)rpw * nsb + 63) / 64;
+    nw = nseg < 16 ? (int)nseg : 16;
+    const long rounds = (nseg + nw - 1) / nw;
+    return arb + (size_t)rounds * nw * 64 * 4 <= 80 * 1024;
+}
+
+static hipError_t launch_q6k_flat(const uint8_t* w, const ActView& A, float* y, int K, int N, hipStream_t st) {
+    int rpw, nw;
+    if (!q6k_flat_geom(K, N, rpw, nw)) return hipErrorInvalidValue;
+    const int nsb = K / 256, nb = K / 32;
+    const size_t arb = ((size_t)nsb * 272 + 12 * (size_t)nb + 15) & ~size_t(15);
+    const long nseg = ((long)rpw * nsb + 63) / 64;
+    const long rounds = (nseg + nw - 1) / nw;
+    const size_t shm = arb + (size_t)rounds * nw * 64 * 4;
+    const unsigned grid = (unsigned)((N + rpw - 1) / rpw);
+    hipLaunchKernelGGL(gemv_q6k_flat, dim3(grid), dim3(64 * nw), shm, st, w, A, y, K, N, rpw);
+    return hipGetLastError();
+}
+
+static int q6_lanes(int K);
+// Where gemv_q6k_sbm leaves CUs short of waves (fewer than 4 per CU: few rows
+// of long K). Both kernels at M = 1 (us): 1024x18944 15.5 / 8.3; at 1792
+// waves the two tie (3584x18944 18.5 / 18.5), at 2048 the sbm kernel is
+// faster (4096x14336 14.5 / 16.2). Both are bound by the lanes' own
+// 210-byte loads there (a loads-only form of the flat kernel: 14.3 us at
+// 3584x18944, against a 9.7 us read).
+static bool q6k_flat_preferred(int M, int K, int N, const uint8_t* w) {
+    int rpw, nw;
+    if (M != 1 || reinterpret_cast<uintptr_t>(w) % 2 != 0 || !q6k_flat_geom(K, N, rpw, nw)) return false;
+    const int L = q6_lanes(K);
+    return (long)N * L / 64 < 4L * device_cu_count();
 }
 
 static int q6_lanes(int K) {
@@ -1527,6 +1711,7 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
     }
     if constexpr (T == T_Q6_K) {
         if (q6rq_preferred(T, M, K, N, w)) return launch_gemv_q6rq(w, A, y, M, K, N, st);
+        if (q6k_flat_preferred(M, K, N, w)) return launch_q6k_flat(w, A, y, K, N, st);
         if (q6k_sbm_supported(K, M, w)) return launch_q6k_sbm(w, A, y, M, K, N, st);
     }
     switch (M) {
@@ -1559,6 +1744,7 @@ static hipError_t launch_gemv_type(const uint8_t* w, const ActView& A, float* y,
 const char* gemv_route_name(uint32_t type, int M, int K, int N, const uint8_t* w) {
     // the decisions of launch_gemv_type, in its order
     if (type == T_Q6_K && q6rq_preferred(type, M, K, N, w)) return "q6rq";
+    if (type == T_Q6_K && q6k_flat_preferred(M, K, N, w)) return "q6flat";
     if (type == T_Q6_K && q6k_sbm_supported(K, M, w)) return "q6k_sbm";
     if (type == T_Q4_K && rq_preferred(type, M, K, N, w)) return "rq";
     if (M == 1) {
