@@ -84,4 +84,37 @@ __device__ inline void build_route(const int* idx, int P, int E, uint8_t* __rest
     }
 }
 
+// The same table from one wave for P <= 64 pairs (lane p holds pair p):
+// pair p's slot is its rank in (expert, pair id) order and k_p its position
+// within its expert, both counted over broadcasts of every pair's expert;
+// the pairs with k_p % gsize == 0 start the groups, numbered in slot order.
+// No atomics or barriers; pairs within an expert come in pair-id order.
+__device__ inline void build_route_wave(const int* idx, int P, int E, uint8_t* __restrict__ route, int max_groups,
+                                        int gsize) {
+    const int lane = threadIdx.x & 63;
+    int* ngroups = reinterpret_cast<int*>(route);
+    int4* groups = reinterpret_cast<int4*>(route + 16);
+    int* pairs = reinterpret_cast<int*>(route + 16 + (size_t)max_groups * 16);
+    const int e = lane < P ? idx[lane] : -1;
+    const bool valid = lane < P && e >= 0 && e < E;
+    int rank = 0, k = 0, cnt = 0;
+    for (int q = 0; q < P; q++) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        if (eq >= 0 && eq < E) {
+            rank += (eq < e) || (eq == e && q < lane);
+            k += eq == e && q < lane;
+            cnt += eq == e;
+        }
+    }
+    const bool starter = valid && k % gsize == 0;
+    const uint64_t sb = __ballot(starter);
+    int gi = 0;
+    for (int q = 0; q < P; q++) {
+        if ((sb >> q) & 1) gi += __builtin_amdgcn_readlane(rank, q) < rank;
+    }
+    if (valid) pairs[rank] = lane;
+    if (starter) groups[gi] = make_int4(e, rank, cnt - k < gsize ? cnt - k : gsize, 0);
+    if (lane == 0) ngroups[0] = (int)__popcll(sb);
+}
+
 }  // namespace lp

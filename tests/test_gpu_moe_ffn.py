@@ -15,12 +15,16 @@ pytestmark = pytest.mark.gpu
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 
 
-def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed):
+def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed, paired_router=False):
     import torch
     from laplace_amd.matmul import Tensor
     from laplace_amd.moe import moe_ffn
     rng = np.random.default_rng(seed)
     p = moe_layer_inputs(rng, H, n_exp, inter, gu_t, dn_t, router_t)
+    if paired_router:
+        # F32 router rows 2i and 2i+1 identical: every logit appears twice
+        r = p["router_w"].view(np.float32).reshape(n_exp, H)
+        r[1::2] = r[0::2]
     x = (rng.standard_normal((T, H)) * 2.0).astype(np.float32)
     ref, ridx, rw = orc.moe_ffn(x, p["router_w"], router_t, p["router_scale"], p["pre_norm"], p["eps"],
                                 p["gu_w"], gu_t, p["dn_w"], dn_t, p["down_scale"], n_exp, top_k, inter)
@@ -53,6 +57,19 @@ def test_moe_ffn_matches_oracle(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, rout
     assert np.array_equal(idx, ridx)
     assert np.allclose(wts, rw, rtol=1e-5, atol=1e-7)
     assert np.isfinite(out).all()
+    assert normwise(out, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("T,top_k", [(1, 3), (3, 5), (9, 3)])
+def test_moe_ffn_router_ties(orc, T, top_k):
+    """Experts in pairs with identical router rows, so the logits tie exactly:
+    the top-k takes the lower expert index first (the reference's strict '>'
+    scan, src/arch_gemma4.cpp:546-563) in both the one-launch top-k and route
+    kernel (T <= 4) and the separate top-k kernel."""
+    (out, idx, wts), (ref, ridx, rw) = run_both(orc, T, 512, 32, top_k, 256, Q4_K, Q4_K, F32,
+                                                seed=100 + T, paired_router=True)
+    assert np.array_equal(idx, ridx)
+    assert np.allclose(wts, rw, rtol=1e-5, atol=1e-7)
     assert normwise(out, ref) <= 1e-4
 
 
