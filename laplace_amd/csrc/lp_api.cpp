@@ -250,6 +250,39 @@ struct HostCtx {
     size_t y_pin_cap = 0;
 };
 
+// Transfers up to this size go by a copy kernel through the pinned buffers'
+// device addresses (the kernel's PCIe reads and posted writes finish sooner
+// than a DMA copy at these sizes); larger ones by DMA.
+constexpr size_t kKernelCopyMax = 1u << 20;
+// pin: the pinned allocation (its base, from grow_pinned), off: the bytes
+// at pin + off
+static int copy_h2d(HostCtx& c, void* dst_dev, void* pin, size_t off, size_t bytes) {
+    uint8_t* src_pin = static_cast<uint8_t*>(pin) + off;
+#ifndef LP_NO_KCOPY
+    if (bytes <= kKernelCopyMax) {
+        void* base = nullptr;
+        LP_HIP(hipHostGetDevicePointer(&base, pin, 0));
+        LP_HIP(launch_copy(dst_dev, static_cast<uint8_t*>(base) + off, bytes, c.stream));
+        return LP_OK;
+    }
+#endif
+    LP_HIP(hipMemcpyAsync(dst_dev, src_pin, bytes, hipMemcpyHostToDevice, c.stream));
+    return LP_OK;
+}
+static int copy_d2h(HostCtx& c, void* pin, size_t off, const void* src_dev, size_t bytes) {
+    uint8_t* dst_pin = static_cast<uint8_t*>(pin) + off;
+#ifndef LP_NO_KCOPY
+    if (bytes <= kKernelCopyMax) {
+        void* base = nullptr;
+        LP_HIP(hipHostGetDevicePointer(&base, pin, 0));
+        LP_HIP(launch_copy(static_cast<uint8_t*>(base) + off, src_dev, bytes, c.stream));
+        return LP_OK;
+    }
+#endif
+    LP_HIP(hipMemcpyAsync(dst_pin, src_dev, bytes, hipMemcpyDeviceToHost, c.stream));
+    return LP_OK;
+}
+
 static std::mutex g_host_mtx;
 static std::unordered_map<int, HostCtx> g_host;
 
@@ -340,7 +373,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
     if ((rc = grow_pinned(c->x_pin, c->x_pin_cap, xb)) != LP_OK) return rc;
     if ((rc = grow_pinned(c->y_pin, c->y_pin_cap, yb)) != LP_OK) return rc;
     std::memcpy(c->x_pin, x, xb);
-    LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
+    if ((rc = copy_h2d(*c, c->xd, c->x_pin, 0, xb)) != LP_OK) return rc;
     if (fact_type(type)) {
         LP_HIP(launch_gemv_fact(type, wd, c->xd, c->yd, M, K, N, c->stream));
     } else if (gemv_fused_supported(type, M, K, wd)) {
@@ -359,7 +392,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         if ((rc = gemm_q(A, ws_planes(c->ws, M, K), wd, type, c->yd, M, K, N, c->stream)) != LP_OK)
             return rc;
     }
-    LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
+    if ((rc = copy_d2h(*c, c->y_pin, 0, c->yd, yb)) != LP_OK) return rc;
     LP_HIP(hipStreamSynchronize(c->stream));
     std::memcpy(y, c->y_pin, yb);
     return LP_OK;
@@ -458,11 +491,11 @@ static int host_moe_grouped(const float* x, int multi, const int* idx, const uin
     std::memcpy(c->x_pin, x, xb);
     int* idx_pin = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(c->x_pin) + xb);
     std::memcpy(idx_pin, idx, sizeof(int) * (size_t)P);
-    LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, xb, hipMemcpyHostToDevice, c->stream));
-    LP_HIP(hipMemcpyAsync(c->idx_d, idx_pin, sizeof(int) * (size_t)P, hipMemcpyHostToDevice, c->stream));
+    if ((rc = copy_h2d(*c, c->xd, c->x_pin, 0, xb)) != LP_OK) return rc;
+    if ((rc = copy_h2d(*c, c->idx_d, c->x_pin, xb, sizeof(int) * (size_t)P)) != LP_OK) return rc;
     if ((rc = moe_q(c->xd, multi, c->idx_d, wd, type, c->yd, T, topk, E, K, N, c->ws, c->stream)) != LP_OK)
         return rc;
-    LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, yb, hipMemcpyDeviceToHost, c->stream));
+    if ((rc = copy_d2h(*c, c->y_pin, 0, c->yd, yb)) != LP_OK) return rc;
     LP_HIP(hipStreamSynchronize(c->stream));
     std::memcpy(y, c->y_pin, yb);
     return LP_OK;
@@ -1005,9 +1038,9 @@ static int host_gemm_batch(const lp_batch_spec* specs, int n) {
         ds[i].x = c->xd + xo[i];
         ds[i].y = c->yd + yo[i];
     }
-    if (xt) LP_HIP(hipMemcpyAsync(c->xd, c->x_pin, 4 * xt, hipMemcpyHostToDevice, c->stream));
+    if (xt && (rc = copy_h2d(*c, c->xd, c->x_pin, 0, 4 * xt)) != LP_OK) return rc;
     if ((rc = batch_dev(ds.data(), n, c->ws, c->ws_cap, c->stream)) != LP_OK) return rc;
-    if (yt) LP_HIP(hipMemcpyAsync(c->y_pin, c->yd, 4 * yt, hipMemcpyDeviceToHost, c->stream));
+    if (yt && (rc = copy_d2h(*c, c->y_pin, 0, c->yd, 4 * yt)) != LP_OK) return rc;
     LP_HIP(hipStreamSynchronize(c->stream));
     for (int i = 0; i < n; i++) std::memcpy(specs[i].y, c->y_pin + yo[i], sizeof(float) * (size_t)specs[i].N);
     return LP_OK;

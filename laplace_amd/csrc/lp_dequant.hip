@@ -746,4 +746,31 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, h
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Byte copy by a kernel (16-byte pieces where both ends allow, else 4 bytes):
+// for small transfers between device memory and device-mapped pinned host
+// memory, where a kernel's PCIe reads and posted writes finish sooner than a
+// DMA copy is set up.
+__global__ void __launch_bounds__(256) copy_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                   size_t bytes, int wide) {
+    const size_t n16 = wide ? bytes / 16 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(src)[i];
+    for (size_t i = n16 * 4 + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes / 4; i += stride)
+        reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+}
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return hipSuccess;
+    if (bytes % 4 != 0 || reinterpret_cast<uintptr_t>(dst) % 4 != 0 || reinterpret_cast<uintptr_t>(src) % 4 != 0)
+        return hipErrorInvalidValue;
+    const int wide = reinterpret_cast<uintptr_t>(dst) % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
+    size_t blocks = (bytes + 4095) / 4096;
+    if (blocks > 256) blocks = 256;
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, st, static_cast<uint8_t*>(dst),
+                       static_cast<const uint8_t*>(src), bytes, wide);
+    return hipGetLastError();
+}
+
 }  // namespace lp

@@ -146,6 +146,9 @@ hipError_t launch_moe_rq(const uint8_t* w, const ActView& A, const void* route, 
 int dequant_block_elems(uint32_t type);
 size_t dequant_src_bytes(uint32_t type, long n);
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, hipStream_t st);
+// Byte copy by a kernel (bytes, dst and src multiples of 4): small transfers
+// to and from device-mapped pinned host memory.
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t st);
 // streaming-read probe (measurement): unroll in {1, 4, 9}
 hipError_t launch_read_probe(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
                              hipStream_t st);
