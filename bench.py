@@ -292,6 +292,8 @@ def measure_gemv(g: Gpu, t, N, K, M, steps, warmup, seed=0, read_ceiling=False, 
         "us_gemv": us_kernel, "kernel_launches": kernel_launches,
         "gbs_gemv": alg_bytes / (us_kernel * 1e-6) / 1e9,
         "w_host": w, "x_host": x, "fused": fused,
+        # the kernel the library routes this shape to (lp_gemm_route)
+        "route": g.L.lp_gemm_route(t, M, K, N, ws_list[0].data_ptr()).decode(),
     }
 
 
@@ -795,7 +797,7 @@ def main():
                     "gbs_step": round(e["gbs_step"], 1),
                     "gbs_gemv": round(e["gbs_gemv"], 1),
                     "hbm_frac_gemv": round(e["gbs_gemv"] / HBM_PEAK_GBS, 4),
-                    "us_gemv": round(e["us_gemv"], 3)}
+                    "us_gemv": round(e["us_gemv"], 3), "route": e["route"]}
             if e["read_ceiling"]:
                 line["read_ceiling_us"] = e["read_ceiling"]["us"]
                 line["frac_of_read_ceiling"] = round(e["read_ceiling"]["us"] / e["us_gemv"], 4)
