@@ -555,7 +555,7 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
         __syncthreads();
         if (!early && s < nseg) load_seg(s, v);
     } else {
-        if (s < nseg) load_seg(s, v);
+        // activation codes first: weight requests ahead of them delay them
         for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
             const u32x4 c = reinterpret_cast<const u32x4*>(A.qs)[i];
             *reinterpret_cast<u32x4*>(smem + (i >> 4) * 272 + (i & 15) * 16) = c;
@@ -565,6 +565,7 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
             sl_[i] = A.sum[i];
         }
         __syncthreads();
+        if (s < nseg) load_seg(s, v);
     }
     const uint32_t act0 = lds_addr_of(smem);
     float part0 = 0.0f, part1 = 0.0f;
@@ -1287,7 +1288,8 @@ __device__ __forceinline__ float q6_sb_dot1(const uint32_t (&raw)[53], uint32_t 
 // l of wave w takes super-block 64 (w + r nw) + l of them in round r, loads it
 // as gemv_q6k_sbm does (all of a round's loads issued together) and dots it
 // with the activation row in LDS (same layout and arithmetic as
-// gemv_q6k_sbm, q6_sb_dot1); the lanes' sums go to LDS and each row's nsb sums are added
+// gemv_q6k_sbm, q6_sb_dot1), its loads issued after the activation rows are
+// staged; the lanes' sums go to LDS and each row's nsb sums are added
 // by one wave (lane-strided, then a DPP tree).
 __global__ void __launch_bounds__(1024)
 gemv_q6k_flat(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, int K, int N, int rpw) {
@@ -1312,11 +1314,6 @@ gemv_q6k_flat(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, i
         f = f < F ? f : F - 1;
         q6_load_sb(base + (long)f * 210, rw, tail, dh, sh);
     };
-    // the first segment's loads (unconditional: indices are clamped) overlap
-    // the activation staging; every load is waited for in straight-line
-    // code before any control-flow merge, so no register still in flight is
-    // copied
-    load(s);
     {
         const int8_t* q = A.qs;
         for (int i = threadIdx.x; i < (K >> 4); i += blockDim.x) {
@@ -1332,6 +1329,10 @@ gemv_q6k_flat(const uint8_t* __restrict__ w, ActView A, float* __restrict__ y, i
         for (int b = threadIdx.x; b < nb; b += blockDim.x) dl[b] = A.d[b];
     }
     __syncthreads();
+    // the weights are requested after the activation rows are read: issued
+    // before, those reads queue behind the weight stream (3584x18944: 17.7
+    // against 15.8 us)
+    load(s);
     q6_wait_sb(rw, tail, dh);
     const uint32_t l0 = lds_addr_of(smem);
     auto compute = [&](int seg) {
@@ -1390,18 +1391,14 @@ static hipError_t launch_q6k_flat(const uint8_t* w, const ActView& A, float* y, 
     return hipGetLastError();
 }
 
-static int q6_lanes(int K);
-// Where gemv_q6k_sbm leaves CUs short of waves (fewer than 4 per CU: few rows
-// of long K). Both kernels at M = 1 (us): 1024x18944 15.5 / 8.3; at 1792
-// waves the two tie (3584x18944 18.5 / 18.5), at 2048 the sbm kernel is
-// faster (4096x14336 14.5 / 16.2). Both are bound by the lanes' own
-// 210-byte loads there (a loads-only form of the flat kernel: 14.3 us at
-// 3584x18944, against a 9.7 us read).
+// M = 1 at any K the geometry takes (K <= 4096 runs on gemv_q6k_rq first).
+// Against gemv_q6k_sbm (us): 3584x18944 15.8 / 18.1, 4096x14336 13.5-13.9 /
+// 14.2-14.3, 1024x18944 8.1 / 15.5 (its 512 waves leave CUs idle). With the
+// weights requested before the activation staging the flat kernel only tied
+// at 3584x18944 (17.7-18.5).
 static bool q6k_flat_preferred(int M, int K, int N, const uint8_t* w) {
     int rpw, nw;
-    if (M != 1 || reinterpret_cast<uintptr_t>(w) % 2 != 0 || !q6k_flat_geom(K, N, rpw, nw)) return false;
-    const int L = q6_lanes(K);
-    return (long)N * L / 64 < 4L * device_cu_count();
+    return M == 1 && reinterpret_cast<uintptr_t>(w) % 2 == 0 && q6k_flat_geom(K, N, rpw, nw);
 }
 
 static int q6_lanes(int K) {
