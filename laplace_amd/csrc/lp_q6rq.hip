@@ -342,10 +342,23 @@ gemv_q6k_rq(Q6rqArgs a) {
         const int c = blockIdx.y;
         const long qd = (long)blockIdx.x * kQ6rqWaves + wave;
         Q6Tile t0;
-        load(c, qd, t0);
-        stage_load(c);
-        stage_store(0);
-        __syncthreads();
+        // the activation rows are requested before the weights (issued after
+        // them, they queue behind the weight stream); with one token group
+        // the weights only after the staging barrier. us at 3584x18944, M =
+        // 4 / 8: weights first 21.7 / 25.5; activations first 21.1 / 23.3;
+        // weights after the barrier 19.7 / 24.2 (14336x4096 M = 8: 19.5,
+        // 18.3, 17.8)
+        if constexpr (TG == 1) {
+            stage_load(c);
+            stage_store(0);
+            __syncthreads();
+            load(c, qd, t0);
+        } else {
+            stage_load(c);
+            load(c, qd, t0);
+            stage_store(0);
+            __syncthreads();
+        }
         uint32_t wd[52], dh;
         tile_words(t0, wd, dh);
         compute(c, wd, dh, 0);
