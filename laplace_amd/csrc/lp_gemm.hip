@@ -438,8 +438,10 @@ __device__ __forceinline__ void rd_lo(i8x32 (&o)[TT], uint32_t a0, uint32_t a1) 
 // Tile of linear index `lin`: groups of kGroupM token tiles walk the weight
 // tiles together (consecutive tiles share a weight tile, the next kGroupM
 // share the next one), so the tiles in flight on one XCD reuse both operands
-// in its L2.
-constexpr int kGroupM = 8;
+// in its L2. Measured (us, groups of 8 / 2): N 4096 M 512 66-69 / 63-64,
+// N 14336 M 512 162 / 158-160, N 14336 M 2048 479-481 / 472-474 (4 close
+// to 2, 16 slower at M 2048).
+constexpr int kGroupM = 2;
 __device__ __forceinline__ void sp_tile(int lin, int ntm, int ntn, int& tm, int& tn) {
     const int per_group = kGroupM * ntn;
     const int grp = lin / per_group, in = lin % per_group;
