@@ -274,6 +274,61 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // src/arch_gemma4.cpp:318-327, :694-700): matrix i owns row groups
 // [gstart[i], gstart[i+1]) of one index space, so one launch (one ramp-up and
 // one tail) serves all of them.
+// Quantization of x by the first nq threads of a workgroup into the LDS
+// layout of gemv_q4k_sb / gemv_b32_sb (272-byte super-block stride, then the
+// block scales dl and sums sl), the quantizer's arithmetic (quant_group8).
+// XR > 0: the "x first" form for long K: the threads load their XR float4 of
+// x into registers, the workgroup passes a barrier (so every x request is
+// issued before the other waves' weight requests), and then quantize.
+template <int XR>
+__device__ __forceinline__ void quantize_x_lds(const float* __restrict__ x, int K, int nq, uint8_t* smem, float* dl,
+                                               float* sl) {
+    if constexpr (XR == 0) {
+        if ((int)threadIdx.x < nq) {
+            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
+                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
+                const int b = i >> 3, gq = i & 7;
+                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+                if (gq == 0) {
+                    dl[b] = q.d;
+                    sl[b] = q.sum;
+                }
+            }
+        }
+    } else {
+        const bool mine = (int)threadIdx.x < nq;
+        float4 xr[XR];
+        if (mine) {
+#pragma unroll
+            for (int j = 0; j < XR; j++) {
+                const int i = threadIdx.x + j * nq;
+                if (i < (K >> 2)) xr[j] = reinterpret_cast<const float4*>(x)[i];
+            }
+        }
+        __syncthreads();
+        if (mine) {
+#pragma unroll
+            for (int j = 0; j < XR; j++) {
+                const int i = threadIdx.x + j * nq;
+                if (i < (K >> 2)) {
+                    const Q8Group q = quant_group8(xr[j]);
+                    const int b = i >> 3, gq = i & 7;
+                    *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
+                    if (gq == 0) {
+                        dl[b] = q.d;
+                        sl[b] = q.sum;
+                    }
+                }
+            }
+        }
+    }
+}
+// x first from K = 8192 (us, x read alongside the first weight requests /
+// x first: Q4_0 4096x14336 12.2-12.5 / 10.3-10.4, 4096x11008 9.9-10.4 / 8.8;
+// Q4_K 14336x8192 16.8 / 16.1), not at K = 4096 (Q4_K 14336x4096 8.4-8.6 /
+// 9.0: the barrier costs more than x's queueing there).
+constexpr int kXFirstMinK = 8192;
+
 template <int L, bool XPOSE, bool FUSEQ, bool MULTI = false>
 __global__ void __launch_bounds__(1024)
 gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
@@ -346,17 +401,12 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         // of them, were slower: x's loads then queue behind the weights).
         const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
-        if (early && g < gend) load_group(g, v);
-        if (!early) {
-            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
-                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
-                const int b = i >> 3, gq = i & 7;
-                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
-                if (gq == 0) {
-                    dl[b] = q.d;
-                    sl_[b] = q.sum;
-                }
-            }
+        if (nq < (int)blockDim.x && K >= kXFirstMinK && (K >> 2) <= 6 * nq) {
+            quantize_x_lds<6>(x, K, nq, smem, dl, sl_);
+            if (early && g < gend) load_group(g, v);
+        } else {
+            if (early && g < gend) load_group(g, v);
+            quantize_x_lds<0>(x, K, nq, smem, dl, sl_);
         }
         __syncthreads();
 #pragma unroll
@@ -966,17 +1016,12 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         // waves request their weights while the first half quantizes x
         const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
-        if (early && g0 * RPW < N) load_chunk(g0, 0, v);
-        if (!early) {
-            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
-                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
-                const int b = i >> 3, gq = i & 7;
-                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
-                if (gq == 0) {
-                    dl[b] = q.d;
-                    sl_[b] = q.sum;
-                }
-            }
+        if (nq < (int)blockDim.x && K >= kXFirstMinK && (K >> 2) <= 8 * nq) {
+            quantize_x_lds<8>(x, K, nq, smem, dl, sl_);
+            if (early && g0 * RPW < N) load_chunk(g0, 0, v);
+        } else {
+            if (early && g0 * RPW < N) load_chunk(g0, 0, v);
+            quantize_x_lds<0>(x, K, nq, smem, dl, sl_);
         }
         __syncthreads();
 #pragma unroll
