@@ -277,9 +277,9 @@ static hipError_t launch_gemv_t(const uint8_t* w, const ActView& A, float* y, in
 // Quantization of x by the first nq threads of a workgroup into the LDS
 // layout of gemv_q4k_sb / gemv_b32_sb (272-byte super-block stride, then the
 // block scales dl and sums sl), the quantizer's arithmetic (quant_group8).
-// XR > 0: the "x first" form for long K: the threads load their XR float4 of
-// x into registers, the workgroup passes a barrier (so every x request is
-// issued before the other waves' weight requests), and then quantize.
+// XR > 0: the "x first" form: the threads load their XR float4 of x into
+// registers, the workgroup passes a barrier (so every x request is issued
+// before the other waves' weight requests), and then they quantize.
 template <int XR>
 __device__ __forceinline__ void quantize_x_lds(const float* __restrict__ x, int K, int nq, uint8_t* smem, float* dl,
                                                float* sl) {
@@ -323,11 +323,11 @@ __device__ __forceinline__ void quantize_x_lds(const float* __restrict__ x, int 
         }
     }
 }
-// x first from K = 8192 (us, x read alongside the first weight requests /
-// x first: Q4_0 4096x14336 12.2-12.5 / 10.3-10.4, 4096x11008 9.9-10.4 / 8.8;
-// Q4_K 14336x8192 16.8 / 16.1), not at K = 4096 (Q4_K 14336x4096 8.4-8.6 /
-// 9.0: the barrier costs more than x's queueing there).
-constexpr int kXFirstMinK = 8192;
+// Measured (us, x read alongside the first weight requests / x first):
+// Q4_K 14336x4096 8.46-8.49 / 8.00-8.09, 4096x4096 6.95 / 6.32, 2048x2816
+// 6.65 / 6.02, 4096x11008 10.4-10.5 / 9.4-9.7; Q4_0 14336x4096 8.40 /
+// 8.04-8.14, 4096x14336 11.8-12.2 / 10.3, 4096x4096 6.75 / 6.21; Q8_0
+// 4096x4096 7.33 / 7.31.
 
 template <int L, bool XPOSE, bool FUSEQ, bool MULTI = false>
 __global__ void __launch_bounds__(1024)
@@ -399,9 +399,11 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         // stream starts without waiting for x (measured 8.8 -> 8.2 us at
         // 14336 x 4096; a quarter or three quarters of the waves early, or all
         // of them, were slower: x's loads then queue behind the weights).
+        // The quantizing half's x requests go out first, one barrier ahead of
+        // the weight requests (quantize_x_lds<6>: 8.46 -> 8.05 us).
         const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
-        if (nq < (int)blockDim.x && K >= kXFirstMinK && (K >> 2) <= 6 * nq) {
+        if (nq < (int)blockDim.x && (K >> 2) <= 6 * nq) {
             quantize_x_lds<6>(x, K, nq, smem, dl, sl_);
             if (early && g < gend) load_group(g, v);
         } else {
@@ -590,18 +592,10 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
     if constexpr (FUSEQ) {
         const int nq = nw >= 8 ? 64 * (nw / 2) : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
+        // (x first, as in gemv_q4k_sb, measured no faster here: 18944x3584
+        // 10.56-10.85 against 10.41-10.62 us)
         if (early && s < nseg) load_seg(s, v);
-        if (!early) {
-            for (int i = threadIdx.x; i < (K >> 2); i += nq) {
-                const Q8Group q = quant_group8(reinterpret_cast<const float4*>(x)[i]);
-                const int b = i >> 3, gq = i & 7;
-                *reinterpret_cast<uint32_t*>(smem + (b >> 3) * 272 + 32 * (b & 7) + 4 * gq) = q.packed;
-                if (gq == 0) {
-                    dl[b] = q.d;
-                    sl_[b] = q.sum;
-                }
-            }
-        }
+        quantize_x_lds<0>(x, K, nq, smem, dl, sl_);
         __syncthreads();
         if (!early && s < nseg) load_seg(s, v);
     } else {
@@ -1016,7 +1010,7 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         // waves request their weights while the first half quantizes x
         const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
-        if (nq < (int)blockDim.x && K >= kXFirstMinK && (K >> 2) <= 8 * nq) {
+        if (nq < (int)blockDim.x && (K >> 2) <= 8 * nq) {
             quantize_x_lds<8>(x, K, nq, smem, dl, sl_);
             if (early && g0 * RPW < N) load_chunk(g0, 0, v);
         } else {
