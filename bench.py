@@ -716,6 +716,27 @@ def load_traffic(name):
         return json.load(f).get("traffic_bytes_per_launch")
 
 
+READ_SWEEP_BYTES = [33_030_144, 49_545_216, 66_060_288, 99_090_432, 132_120_576, 198_180_864,
+                    264_241_152, 330_301_440, 415_236_096]
+
+
+def read_sweep(g: Gpu):
+    """Streaming-read time of N bytes by the best lp_read_probe_dev launch
+    shape, N from the headline Q4_K weight (14336 x 4096, 33.0 MB) to the
+    LM head's (262144 x 2816 Q4_K, 415.2 MB): where the part's read rate
+    crosses 70 % of the 8 TB/s spec. Rotating copies (>= 2, >= 512 MiB in
+    all) so every launch reads HBM, not the 256 MB Infinity Cache."""
+    torch = g.torch
+    for nb in READ_SWEEP_BYTES:
+        ncp = max(2, -(-ROTATE_MIN_BYTES // nb))
+        bufs = [torch.randint(0, 256, (nb,), dtype=torch.uint8, device=g.dev) for _ in range(ncp)]
+        reps = max(4, int(400e6 // (nb * ncp)) + 1)
+        r = measure_read_ceiling(g, bufs, nb, reps, 2)
+        print(json.dumps({"read_sweep_bytes": nb, "copies": ncp, **r}), flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -728,6 +749,9 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run N torch device copies of 256 MiB (a copy kernel of known "
                          "size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
+    ap.add_argument("--read-sweep", action="store_true",
+                    help="only the streaming-read ceiling (lp_read_probe_dev) over read sizes "
+                         "from the headline weight (33 MB) to the LM head (415 MB), one JSON line each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -742,6 +766,9 @@ def main():
             b.copy_(a)
         g.torch.cuda.synchronize()
         del a, b
+    if args.read_sweep:
+        read_sweep(g)
+        return
     t, N, K, M = Q4_K, 14336, 4096, 1
     r = measure_gemv(g, t, N, K, M, args.steps, args.warmup, read_ceiling=True)
     name = "q4k_gemv_14336x4096_m1"
@@ -814,7 +841,7 @@ def main():
                        "value": head["tops"], "unit": "TOPS", "workload": head["workload"],
                        "us_per_step": head["us_step"],
                        "roofline": {"bound": "mfma", "achieved": head["tops"],
-                                    "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                                    "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                                     "frac": head["frac_int8_peak"], "traffic": None},
                        "all": gemms}
         if not args.no_cpu:

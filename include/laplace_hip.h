@@ -124,7 +124,11 @@ int lp_act_unpack_dev(const void* ws, int M, int K, float* d, float* sum, int32_
 int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
                 void* ws, size_t ws_bytes, void* stream);
 
-/* Same product from activations already quantized into ws. */
+/* Same product from activations already quantized into ws. ws must be the
+ * buffer lp_quantize_act_dev filled for the same M and K, of at least
+ * lp_act_workspace_bytes(M, K) bytes: besides the quantized blocks, the
+ * kernels chosen here use its tail (the GEMM planes for M >= 5, partial sums
+ * for 3 <= M <= 8), and this call takes no size to check it against. */
 int lp_gemm_q_dev(const void* ws, const uint8_t* w, uint32_t type, float* y, int M, int K, int N,
                   void* stream);
 

@@ -177,8 +177,15 @@ __device__ __forceinline__ void topk_token(const float* __restrict__ logits, int
             key = kj > key ? kj : key;
         }
         key = wave_kmax(key);
-        const float bv = key_value(key);
-        const int bi = (int)~(uint32_t)key;
+        // The reference's scan starts at best = 0 and moves only on a strict
+        // '>', so a NaN held by expert 0 is never beaten, and NaNs elsewhere
+        // never win (they carry key 0 here). A NaN or +inf logit makes every
+        // probability NaN, and the reference then picks expert 0 for every k
+        // (its -1e30 after the first pick still beats the NaNs).
+        const float v0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0]), 0));
+        const bool take0 = v0 != v0 || key == 0ull;
+        const float bv = take0 ? v0 : key_value(key);
+        const int bi = take0 ? 0 : (int)~(uint32_t)key;
         if (lane == k) {
             mine = bv;
             mine_i = bi;

@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 
 
-def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed, paired_router=False):
+def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed, paired_router=False, nan_row=None):
     import torch
     from laplace_amd.matmul import Tensor
     from laplace_amd.moe import moe_ffn
@@ -25,6 +25,9 @@ def run_both(orc, T, H, n_exp, top_k, inter, gu_t, dn_t, router_t, seed, paired_
         # F32 router rows 2i and 2i+1 identical: every logit appears twice
         r = p["router_w"].view(np.float32).reshape(n_exp, H)
         r[1::2] = r[0::2]
+    if nan_row is not None:
+        # one F32 router row of NaN: that expert's logit is NaN for every token
+        p["router_w"].view(np.float32).reshape(n_exp, H)[nan_row] = np.nan
     x = (rng.standard_normal((T, H)) * 2.0).astype(np.float32)
     ref, ridx, rw = orc.moe_ffn(x, p["router_w"], router_t, p["router_scale"], p["pre_norm"], p["eps"],
                                 p["gu_w"], gu_t, p["dn_w"], dn_t, p["down_scale"], n_exp, top_k, inter)
@@ -71,6 +74,21 @@ def test_moe_ffn_router_ties(orc, T, top_k):
     assert np.array_equal(idx, ridx)
     assert np.allclose(wts, rw, rtol=1e-5, atol=1e-7)
     assert normwise(out, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("T,nan_row", [(1, 5), (3, 0), (9, 17)])
+def test_moe_ffn_nan_router(orc, T, nan_row):
+    """A NaN router logit makes every softmax probability NaN. The
+    reference's scan (best = 0, strict '>', src/arch_gemma4.cpp:555-559) then
+    picks expert 0 for every k, so every pick must stay in range and equal the
+    oracle's (all zero), in both top-k kernels (T <= 4 and beyond); the
+    weights and outputs are NaN on both sides."""
+    (out, idx, wts), (ref, ridx, rw) = run_both(orc, T, 512, 32, 4, 256, Q4_K, Q4_K, F32,
+                                                seed=300 + T, nan_row=nan_row)
+    assert (ridx == 0).all()
+    assert np.array_equal(idx, ridx)
+    assert np.array_equal(np.isnan(wts), np.isnan(rw))
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
 
 
 def test_moe_ffn_rejects_bad_shapes():

@@ -20,6 +20,7 @@ def _pair(t, M, K, N, seed):
     w = synth_weights(t, K, N, seed=seed)
     x = synth_x(M, K, seed=seed + 1, outliers=0.01)
     xd, wd = to_dev(x), to_dev(w)
+    route = L().lp_gemm_route(t, M, K, N, wd.data_ptr()).decode()
     y0 = torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda")
     y1 = torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda")
     nb = int(L().lp_act_workspace_bytes(M, K))
@@ -29,18 +30,22 @@ def _pair(t, M, K, N, seed):
     _lib.check(L().lp_gemm_dev_noalloc(xd.data_ptr(), wd.data_ptr(), t, y1.data_ptr(), M, K, N, stream()),
                "lp_gemm_dev_noalloc")
     torch.cuda.synchronize()
-    return y0.cpu().numpy(), y1.cpu().numpy()
+    return y0.cpu().numpy(), y1.cpu().numpy(), route
 
 
 @pytest.mark.parametrize("t,big,small", [
     (Q4_K, (96, 2048, 512), (8, 1024, 256)),        # GEMM planes, then the int8 MFMA kernel
     (Q4_K, (16, 4096, 768), (3, 1024, 256)),        # small-M MFMA, then the dot4 GEMV
     (Q6_K, (12, 2048, 640), (2, 1024, 256)),
+    # K-split Q6_K row quads: partial sums in the workspace's tail region
+    (Q6_K, (8, 18944, 512), (3, 8448, 256)),
     (Q8_0, (40, 1024, 384), (5, 512, 128)),         # row chunks
-], ids=["q4k_gemm", "q4k_small", "q6k", "q80"])
+], ids=["q4k_gemm", "q4k_small", "q6k", "q6k_rq_split", "q80"])
 def test_noalloc_matches_workspace_entry(t, big, small):
     for i, (M, K, N) in enumerate((big, small)):
-        y0, y1 = _pair(t, M, K, N, seed=100 * t + i)
+        y0, y1, route = _pair(t, M, K, N, seed=100 * t + i)
+        if t == Q6_K and K > 4096 and 3 <= M <= 8:
+            assert route == "q6rq", (M, K, N, route)
         assert np.isfinite(y0).all()
         assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), (t, M, K, N)
 
