@@ -24,7 +24,7 @@ OBJ = os.path.join(ROOT, "_build", "obj")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_rq.hip", "lp_q6rq.hip", "lp_api.cpp"]
+SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_gemm_fr.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_rq.hip", "lp_q6rq.hip", "lp_api.cpp"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

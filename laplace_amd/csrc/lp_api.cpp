@@ -384,7 +384,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
     } else if (use_gemm(type, M, K, N, wd)) {
         void* planes = ws_planes(c->ws, M, K);
-        LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream));
+        LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream, N));
         LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
     } else {
         const ActView A = ws_view_full(c->ws, M, K);
@@ -721,7 +721,7 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
         }
         void* planes = ws_planes(ws, M, K);
         hipStream_t hs = static_cast<hipStream_t>(stream);
-        LP_HIP(launch_planes_from_x(x, planes, M, K, hs));
+        LP_HIP(launch_planes_from_x(x, planes, M, K, hs, N));
         LP_HIP(launch_gemm_planes(type, w, planes, y, M, K, N, hs));
         return LP_OK;
     }

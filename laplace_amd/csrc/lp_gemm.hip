@@ -24,6 +24,7 @@
 // two-plane fp16 form (hi = fp16(xd*q), lo = fp16(xd*q - hi)) on
 // v_mfma_f32_16x16x32_f16 (gemv_q4k_mf).
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 
 #include "lp_chunks.h"
 #include "lp_internal.h"
@@ -1261,7 +1262,20 @@ __global__ void __launch_bounds__(256) zero_f32_kernel(float* __restrict__ y, si
 size_t gemm_planes_bytes(int M, int K) {
     const size_t up = 256;
     auto r = [&](size_t v) { return (v + up - 1) / up * up; };
-    return 2 * r((size_t)M * K * 2) + 2 * r((size_t)M * (K / 32) * 2) + r((size_t)M * 4);
+    const size_t sp = 2 * r((size_t)M * K * 2) + 2 * r((size_t)M * (K / 32) * 2) + r((size_t)M * 4);
+    const size_t fr = gemm_fr_supported(T_Q4_K, M, K) ? gemm_fr_planes_bytes(M, K) : 0;
+    return sp > fr ? sp : fr;
+}
+
+// The fragment-order GEMM (lp_gemm_fr.hip) for these shapes. LP_GEMM_FR=0
+// keeps the split-precision kernel (comparison runs).
+static bool gemm_fr_preferred(int M, int K, int N) {
+    static const int env = [] {
+        const char* e = getenv("LP_GEMM_FR");
+        return e ? atoi(e) : -1;
+    }();
+    if (env == 0 || !gemm_fr_supported(T_Q4_K, M, K)) return false;
+    return N >= 256;
 }
 
 
@@ -1273,8 +1287,9 @@ bool gemm_supported(uint32_t type, int M, int K) {
 // (M <= kMfMaxM), the split-precision pair for the GEMM otherwise.
 static bool planes_sp(int M) { return M > kMfMaxM; }
 
-hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st) {
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N) {
     if (M <= 0) return hipSuccess;
+    if (gemm_fr_preferred(M, K, N)) return launch_fr_planes(x, ActView{}, planes, M, K, st);
     // NF float4 per thread, at most 1024 threads (K <= 32768); 8 | K/4/NF since 32 | K
     const int n4 = K / 4;
     const int nf = n4 <= 1024 ? 1 : n4 <= 2048 ? 2 : n4 <= 4096 ? 4 : 8;
@@ -1321,6 +1336,7 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
                               hipStream_t st) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
+    if (gemm_fr_preferred(M, K, N)) return launch_fr_gemm(w, planes, y, M, K, N, st);
     const Planes P = carve_planes(planes, M, K);
     if (M <= kMfMaxM) {
         MfArgs a{w, (long)row_bytes(type, K), N, K, M, P, y};
@@ -1349,7 +1365,8 @@ hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* 
                        int M, int K, int N, hipStream_t st) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
-    hipError_t e = launch_planes_from_act(A, planes, M, K, st);
+    hipError_t e = gemm_fr_preferred(M, K, N) ? launch_fr_planes(nullptr, A, planes, M, K, st)
+                                              : launch_planes_from_act(A, planes, M, K, st);
     if (e != hipSuccess) return e;
     return launch_gemm_planes(type, w, planes, y, M, K, N, st);
 }

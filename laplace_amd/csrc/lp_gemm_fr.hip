@@ -1,0 +1,706 @@
+// lp_gemm_fr.hip - prefill GEMM for Q4_K weights (M >= 128 tokens) on planes
+// stored in MFMA fragment order.
+//
+// Reference semantics: gemm_int<dot_row_q4_k_int_neon> row by row
+// (src/matmul_simd.cpp:226-283, 432-455):
+//   y[m,n] = sum_sb [ d_n * sum_{b in sb} sc_nb * xd_mb * P_mnb
+//                     - dmin_n * sum_{b in sb} mn_nb * xs_mb ]
+// with P_mnb = sum_{k in b} nib_nk * q_mk and xd/xs/q the ActQ8 activation
+// blocks (src/matmul_simd.cpp:348-410).
+//
+// Operands (the split-precision folding of the block scales):
+//   t[m,k]  = xd_mb * q_mk * 2^(9 - E_m)   (E_m: exponent of the row's largest
+//             block scale, so |t| <= 65024)
+//   hi      = fp16(t),  lo = e4m3(t - hi)      (activation planes)
+//   V[n,k]  = sc_nb * nib_nk / 4  (exact in fp16),  V8 = e4m3(V)
+// main_sb = sum_k hi*V (fp16 MFMA, exact products) + sum_k lo*V8 (fp8 MFMA),
+// and per super-block acc += d_n * 2^-7 * main_sb - dmin_n * min_sb with
+// min_sb = sum_b m_nb * xs_mb * 2^-E_m (xs split into fp16 hi + lo, one fp16
+// MFMA against the exact 6-bit m). y = acc * 2^E_m. The residual term leaves
+// a per-product error below 2^-14 of |t*V|.
+//
+// Fragment-order planes. The activation planes are written by this file's
+// planes kernel in the exact order the MFMA lanes read them, so every copy is
+// a contiguous 1 KiB piece and every LDS read is lane-linear (no swizzle, no
+// bank conflicts). Within a 64-element K step, lane half g (lane / 32),
+// sub-step s (0..3) and position p (0..7) hold element
+//   e(g, s, p) = 16g + 4s + perm(p & 3) + (p >= 4 ? 32 : 0),  perm = {0,2,1,3}
+// which is what the weight decode produces from the 16 code bytes 16g..16g+15
+// of the step's 32-byte code chunk (dword s of them: low nibbles are elements
+// 0..31 of the step, high nibbles 32..63, src/matmul_simd.cpp:240-262). The
+// MFMAs pair A and B values of the same lane half and position, so the sums
+// are those of the natural order.
+//   HI [T][ks][s][lane][8 fp16]       T = 32-token tile, ks = 64-element K step
+//   LO [T][ks][h][lane][16 e4m3]      byte 8s + p of a lane's 32, half h = byte/16
+//   SX [T][sb][lane][8 fp16]          lanes 0-31: fp16(xs 2^-E) of the token's
+//                                     8 blocks of super-block sb; 32-63: residuals
+//   escale [Mp]                       2^E_m
+//
+// GEMM tiling: a workgroup is 4 waves and a tile of 128 tokens x 256 weight
+// rows; wave w owns every token of the tile and weight rows 64w..64w+63
+// (4 x 2 MFMA tiles of 32 x 32: A = activations, B = weights, D lane = weight
+// row). Each wave decodes only its own rows and reads the shared activation
+// tile from LDS: 96 B of LDS per token per K step against 1536 MFMA cycles,
+// half of the LDS bytes per MFMA of a 32-row wave. Per K step the wave copies
+// one token tile's planes (6 KiB) and its two row tiles' codes (2 KiB) into
+// LDS with buffer_load_dwordx4 ... lds; headers and min-term planes once per
+// super-block. NS stages in flight, one barrier per K step, one workgroup per
+// CU (LDS NS x 32 KiB + 16 KiB).
+#include <hip/hip_runtime.h>
+
+#include "lp_chunks.h"
+#include "lp_internal.h"
+
+namespace lp {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef int i8x32 __attribute__((ext_vector_type(8)));   // 32 fp8 bytes
+
+constexpr int kTm = 4;            // 32-token tiles per workgroup (all waves share them)
+constexpr int kRt = 2;            // 32-row tiles per wave
+constexpr int kNw = 4;            // waves
+constexpr int kBm = 32 * kTm, kBn = 32 * kRt * kNw;
+constexpr int kHi = kTm * 4096, kLo = kTm * 2048, kCodes = kRt * kNw * 1024;
+constexpr int kStage = kHi + kLo + kCodes;                   // 32 KiB
+constexpr int kHdr = kBn * 16, kSx = kTm * 1024;
+constexpr int kSbuf = kHdr + kSx;                            // 8 KiB
+constexpr int kDmaStep = 4 + 2 + kRt;                        // per wave and K step
+constexpr int kDmaSb = 2;                                    // per wave and super-block
+static_assert(kTm == kNw, "wave w copies token tile w");
+
+struct FrArgs {
+    const uint8_t* hi;
+    const uint8_t* lo;
+    const uint8_t* sx;
+    const float* escale;
+    const uint8_t* w;
+    size_t rb;
+    float* y;
+    int M, N, K;
+    int ntm, ntn;       // token / row tiles of the grid
+    int tiles_pad;      // 32-token tiles of the planes (Mp / 32)
+    int nfull;          // tiles [0, nfull) run whole; each later tile is two workgroups,
+                        // one per half of K, adding into a zeroed y (two fp32 additions
+                        // onto 0 give the same sum in either order)
+    unsigned long long* stamp;   // phase cycle sums (instrumented build only)
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
+}
+// LDS reads as inline assembly with explicit lgkmcnt waits: a compiler-
+// generated ds_read after direct-to-LDS copies makes the compiler wait for
+// every copy in flight (vmcnt(0)), the prefetches of later steps included.
+template <int OFF>
+__device__ __forceinline__ void rd128(u32x4& o, uint32_t a) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(o) : "v"(a), "n"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void rd128h(h8& o, uint32_t a) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(o) : "v"(a), "n"(OFF));
+}
+template <int N, typename V, int T>
+__device__ __forceinline__ void lgkm(V (&a)[T]) {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+    for (int i = 0; i < T; i++) asm volatile("" : "+v"(a[i]));
+}
+
+// One dword of codes (bytes b0..b3) -> 8 fp16 V in positions
+// [lo b0, lo b2, lo b1, lo b3, hi b0, hi b2, hi b1, hi b3]: masking nibbles
+// into fp16 1024 + n (low) or 1024 + 16n (high) and one packed fma each,
+// (h - 1024) * sc/4 (or sc/64), exact.
+__device__ __forceinline__ h8 decode4(uint32_t u, h2 ml, h2 al, h2 mh, h2 ah) {
+    const uint32_t u8 = u >> 8;
+    uint32_t a, b, c, d;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(a) : "v"(0x000f000fu), "v"(u), "s"(0x64006400u));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(b) : "v"(0x000f000fu), "v"(u8), "s"(0x64006400u));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(c) : "v"(0x00f000f0u), "v"(u), "s"(0x64006400u));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(d) : "v"(0x00f000f0u), "v"(u8), "s"(0x64006400u));
+    const h2 va = __builtin_elementwise_fma(__builtin_bit_cast(h2, a), ml, al);
+    const h2 vb = __builtin_elementwise_fma(__builtin_bit_cast(h2, b), ml, al);
+    const h2 vc = __builtin_elementwise_fma(__builtin_bit_cast(h2, c), mh, ah);
+    const h2 vd = __builtin_elementwise_fma(__builtin_bit_cast(h2, d), mh, ah);
+    return h8{va[0], va[1], vb[0], vb[1], vc[0], vc[1], vd[0], vd[1]};
+}
+
+__device__ __forceinline__ uint32_t e4m3x4(uint32_t h01, uint32_t h23) {
+    uint32_t w;
+    asm("v_cvt_scalef32_pk_fp8_f16 %0, %1, 1.0\n\tv_cvt_scalef32_pk_fp8_f16 %0, %2, 1.0 op_sel:[0,0,1]"
+        : "=&v"(w) : "v"(h01), "v"(h23));
+    return w;
+}
+
+// 6-bit scale j of a Q4_K header (words hy = scales[0..3], hz = [4..7],
+// hw = [8..11]); get_scale_min_k4 (src/kernels.h:82-90).
+__device__ __forceinline__ uint32_t q4k_sc(uint32_t hy, uint32_t hw, int j) {
+    return j < 4 ? __builtin_amdgcn_ubfe(hy, 8 * j, 6)
+                 : __builtin_amdgcn_ubfe(hw, 8 * (j - 4), 4) | (__builtin_amdgcn_ubfe(hy, 8 * (j - 4) + 6, 2) << 4);
+}
+__device__ __forceinline__ uint32_t q4k_m(uint32_t hz, uint32_t hw, int j) {
+    return j < 4 ? __builtin_amdgcn_ubfe(hz, 8 * j, 6)
+                 : __builtin_amdgcn_ubfe(hw, 8 * (j - 4) + 4, 4) | (__builtin_amdgcn_ubfe(hz, 8 * (j - 4) + 6, 2) << 4);
+}
+
+// Per wave: copy sources fixed for the tile; a step changes scalar offsets.
+struct FrPlan {
+    Rsrc rs_hi, rs_lo, rs_w, rs_sx;
+    uint32_t code_off[kRt], hdr_off;
+    int ks_all, nsb_all;
+};
+
+// Copy i of K step kt into stage `st` / super-block buffer `sbb`: 0-3 the hi
+// sub-steps, 4-5 the lo halves, 6-7 the two row tiles' codes, 8-9 the
+// super-block's headers and min-term planes (steps that start one). The
+// copies move through the CU's vector-memory path at ~64 B per clock and a
+// wave's issue waits for it, so the compute loop issues one copy after each
+// fp8 MFMA (64 cycles of MFMA work) instead of a burst.
+__device__ __forceinline__ void fr_issue(const FrPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
+#ifdef FR_NO_DMA
+    if (kt >= 3) return;
+#endif
+    const uint32_t lane16 = (threadIdx.x & 63) * 16;
+    const int sb = kt >> 2, jb = kt & 3;
+    if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
+    else if (i < 6) dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (i - 4) * 1024), st + kHi + wave * 2048 + (i - 4) * 1024);
+    else if (i < 8)
+        dma16(d.rs_w, d.code_off[i - 6], (uint32_t)(sb * 144 + 32 * jb), st + kHi + kLo + (wave * kRt + i - 6) * 1024);
+    else if (jb == 0) {
+        if (i == 8) dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
+        else dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + kHdr + wave * 1024);
+    }
+}
+
+__device__ __forceinline__ int fr_count(int k, int nk) { return k < nk ? kDmaStep + ((k & 3) == 0 ? kDmaSb : 0) : 0; }
+
+// STAMP: an instrumented build that sums s_memtime cycles per phase of a K
+// step (copy wait + barrier, copy issue, fp16/fp8 products, super-block
+// epilogue) into g.stamp; each stamp sits where no LDS read is in flight.
+template <int NS, bool STAMP = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_q4k_fr(FrArgs g) {
+    unsigned long long ph[4] = {0, 0, 0, 0}, tprev = 0;
+    const unsigned long long c_beg = STAMP ? __builtin_amdgcn_s_memtime() : 0;
+    const unsigned long long r_beg = STAMP ? __builtin_amdgcn_s_memrealtime() : 0;
+    auto stamp = [&](int i) {
+        if (STAMP) {
+            const unsigned long long t = __builtin_amdgcn_s_memtime();
+            if (i >= 0) ph[i] += t - tprev;
+            tprev = t;
+        }
+    };
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // blocks are dealt to the 8 XCDs round-robin: each XCD gets a contiguous
+    // run of tiles, row tiles fastest (the workgroups in flight on one XCD
+    // share their activation tile in its L2)
+    // the whole tiles first; blocks are dealt to the 8 XCDs round-robin, so
+    // each XCD gets a contiguous run of them. The split tiles fill the last
+    // round of the grid with half-length work.
+    const int bid = blockIdx.x;
+    int tile, part = 0, ksplit = 1;
+    if (bid < g.nfull) {
+        tile = (g.nfull & 7) == 0 ? (bid & 7) * (g.nfull >> 3) + (bid >> 3) : bid;
+    } else {
+        tile = g.nfull + ((bid - g.nfull) >> 1);
+        part = (bid - g.nfull) & 1;
+        ksplit = 2;
+    }
+    const int tm = tile / g.ntn, tn = tile % g.ntn;
+    const int m0 = tm * kBm, n0 = tn * kBn;
+    const int nsb_all = g.K >> 8, ks_all = g.K >> 6;
+    const int sb_beg = part * nsb_all / ksplit, sb_end = (part + 1) * nsb_all / ksplit;
+    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;
+
+    FrPlan d;
+    {
+        int T = tm * kTm + wave;                               // this wave's token tile for the copies
+        T = T < g.tiles_pad ? T : g.tiles_pad - 1;
+        d.rs_hi = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
+        d.rs_lo = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
+        d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
+        const int nt = g.N - n0 < kBn ? g.N - n0 : kBn;
+        d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+#pragma unroll
+        for (int r = 0; r < kRt; r++) {
+            int row = (wave * kRt + r) * 32 + (lane & 31);
+            row = row < nt ? row : nt - 1;
+            d.code_off[r] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
+        }
+        int hrow = wave * 64 + lane;
+        hrow = hrow < nt ? hrow : nt - 1;
+        d.hdr_off = (uint32_t)((size_t)hrow * g.rb);
+    }
+    auto stage = [&](int i) { return smem + i * kStage; };
+    auto sbuf = [&](int i) { return smem + NS * kStage + i * kSbuf; };
+
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t l16 = lds0 + lane * 16;
+    const uint32_t hdr_a = lds0 + NS * kStage + (wave * 64 + (lane & 31)) * 16;   // + rt * 512
+
+    f16v acc[kTm][kRt], mn[kTm][kRt];
+#pragma unroll
+    for (int a = 0; a < kTm; a++)
+#pragma unroll
+        for (int b = 0; b < kRt; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+
+    uint32_t hy[kRt], hz[kRt], hw[kRt];
+    float dsc[kRt], dmn[kRt];
+
+    // prologue: steps kt0 .. kt0+NS-2 in flight
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++)
+        if (kt0 + i < nk)
+#pragma unroll
+            for (int p = 0; p < 10; p++) fr_issue(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
+
+    for (int sb = sb_beg; sb < sb_end; sb++) {
+        const uint32_t sbo = (uint32_t)((sb & 1) * kSbuf);
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            const int kt = 4 * sb + jb;
+            int later = 0;                       // copies of steps kt+1 .. kt+NS-2 (may stay in flight)
+#pragma unroll
+            for (int i = 1; i < NS - 1; i++) later += fr_count(kt + i, nk);
+            stamp(-1);
+            wait_dma(later);
+            // after this barrier every wave has finished step kt-1, whose
+            // stage is the one step kt+NS-1 is copied into
+#ifndef FR_NO_BAR
+            __builtin_amdgcn_s_barrier();
+#endif
+            stamp(0);
+            const bool pf = kt + NS - 1 < nk;
+            uint8_t* const pst = stage((kt + NS - 1 - kt0) % NS);
+            uint8_t* const psb = sbuf(((kt + NS - 1) >> 2) & 1);
+            stamp(1);
+            const uint32_t so = (uint32_t)(((kt - kt0) % NS) * kStage);
+
+            if (jb == 0) {
+                u32x4 h[kRt];
+                rd128<0>(h[0], hdr_a + sbo);
+                rd128<512>(h[1], hdr_a + sbo);
+                lgkm<0>(h);
+#pragma unroll
+                for (int r = 0; r < kRt; r++) {
+                    dsc[r] = fp16_bits_to_f32(h[r].x) * 0.0078125f;   // d * 2^-7 (main carries 2^7)
+                    dmn[r] = fp16_bits_to_f32(h[r].x >> 16);
+                    hy[r] = h[r].y;
+                    hz[r] = h[r].z;
+                    hw[r] = h[r].w;
+                }
+            }
+            // decode constants: low nibbles block 2jb (sc/4), high 2jb+1 (sc/64)
+            h2 ml[kRt], al[kRt], mh[kRt], ah[kRt];
+#pragma unroll
+            for (int r = 0; r < kRt; r++) {
+                const float sl = (float)q4k_sc(hy[r], hw[r], 2 * jb) * 0.25f;
+                const float sh = (float)q4k_sc(hy[r], hw[r], 2 * jb + 1) * (0.25f * 0.0625f);
+                const _Float16 a = (_Float16)sl, b = (_Float16)(-1024.0f * sl);
+                const _Float16 c = (_Float16)sh, e = (_Float16)(-1024.0f * sh);
+                ml[r] = h2{a, a};
+                al[r] = h2{b, b};
+                mh[r] = h2{c, c};
+                ah[r] = h2{e, e};
+            }
+
+            const uint32_t b = l16 + so;
+            u32x4 cw[kRt];
+            h8 A[2][kTm];
+            rd128<kHi + kLo>(cw[0], b + (wave * kRt) * 1024);
+            rd128<kHi + kLo + 1024>(cw[1], b + (wave * kRt) * 1024);
+            rd128h<0>(A[0][0], b);
+            rd128h<4096>(A[0][1], b);
+            rd128h<8192>(A[0][2], b);
+            rd128h<12288>(A[0][3], b);
+            rd128h<1024>(A[1][0], b);
+            rd128h<1024 + 4096>(A[1][1], b);
+            rd128h<1024 + 8192>(A[1][2], b);
+            rd128h<1024 + 12288>(A[1][3], b);
+            lgkm<8>(cw);
+            uint32_t v8[kRt][8];
+            u32x4 L[kTm][2];
+            // software-pipelined: sub-step s+1's weights are decoded (and s's
+            // converted to e4m3) between sub-step s's MFMAs
+            h8 Vc[kRt];
+#pragma unroll
+            for (int r = 0; r < kRt; r++) Vc[r] = decode4(cw[r][0], ml[r], al[r], mh[r], ah[r]);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                if (s == 0) lgkm<4>(A[0]);
+                else if (s == 1) lgkm<4>(A[1]);
+                else if (s == 2) lgkm<4>(A[0]);
+                else lgkm<8>(A[1]);
+                h8 Vn[kRt];
+#pragma unroll
+                for (int r = 0; r < kRt; r++)
+#pragma unroll
+                    for (int t = 0; t < kTm; t++)
+                        mn[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s & 1][t], Vc[r],
+                                                                          (jb == 0 && s == 0) ? f16v{} : mn[t][r],
+                                                                          0, 0, 0);
+                if (s < 3) {
+#pragma unroll
+                    for (int r = 0; r < kRt; r++) {
+#ifdef FR_NO_DECODE
+                        Vn[r] = Vc[r];
+#else
+                        Vn[r] = decode4(cw[r][s + 1], ml[r], al[r], mh[r], ah[r]);
+#endif
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < kRt; r++) {
+                    const u32x4 q = __builtin_bit_cast(u32x4, Vc[r]);
+#ifdef FR_NO_DECODE
+                    v8[r][2 * s] = q.x;
+                    v8[r][2 * s + 1] = q.y;
+#else
+                    v8[r][2 * s] = e4m3x4(q.x, q.y);
+                    v8[r][2 * s + 1] = e4m3x4(q.z, q.w);
+#endif
+                }
+#pragma unroll
+                for (int i = 0; i < 2 * kTm; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // then up to four VALU
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (s < 3) {
+#pragma unroll
+                    for (int r = 0; r < kRt; r++) Vc[r] = Vn[r];
+                }
+#ifdef FR_NO_LDS
+                if (kt > 0) {
+                    asm volatile("" : "+v"(A[0][0]), "+v"(A[0][1]), "+v"(A[0][2]), "+v"(A[0][3]));
+                    asm volatile("" : "+v"(A[1][0]), "+v"(A[1][1]), "+v"(A[1][2]), "+v"(A[1][3]));
+                    for (int t = 0; t < kTm; t++) asm volatile("" : "+v"(L[t][0]), "+v"(L[t][1]));
+                } else
+#endif
+                if (s == 0) {
+                    rd128h<2048>(A[0][0], b);
+                    rd128h<2048 + 4096>(A[0][1], b);
+                    rd128h<2048 + 8192>(A[0][2], b);
+                    rd128h<2048 + 12288>(A[0][3], b);
+                } else if (s == 1) {
+                    rd128h<3072>(A[1][0], b);
+                    rd128h<3072 + 4096>(A[1][1], b);
+                    rd128h<3072 + 8192>(A[1][2], b);
+                    rd128h<3072 + 12288>(A[1][3], b);
+                } else if (s == 2) {
+                    rd128<kHi>(L[0][0], b);
+                    rd128<kHi + 1024>(L[0][1], b);
+                    rd128<kHi + 2048>(L[1][0], b);
+                    rd128<kHi + 3072>(L[1][1], b);
+                    rd128<kHi + 4096>(L[2][0], b);
+                    rd128<kHi + 5120>(L[2][1], b);
+                    rd128<kHi + 6144>(L[3][0], b);
+                    rd128<kHi + 7168>(L[3][1], b);
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int t = 0; t < kTm; t++) {
+                asm volatile("" : "+v"(L[t][0]), "+v"(L[t][1]));
+            }
+#pragma unroll
+            for (int r = 0; r < kRt; r++) {
+                const i8x32 bv = {(int)v8[r][0], (int)v8[r][1], (int)v8[r][2], (int)v8[r][3],
+                                  (int)v8[r][4], (int)v8[r][5], (int)v8[r][6], (int)v8[r][7]};
+#pragma unroll
+                for (int t = 0; t < kTm; t++) {
+                    const i8x32 av = {(int)L[t][0].x, (int)L[t][0].y, (int)L[t][0].z, (int)L[t][0].w,
+                                      (int)L[t][1].x, (int)L[t][1].y, (int)L[t][1].z, (int)L[t][1].w};
+                    mn[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, mn[t][r], 0, 0, 0, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (pf) fr_issue(d, wave, kt + NS - 1, pst, psb, r * kTm + t);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (pf) {
+                fr_issue(d, wave, kt + NS - 1, pst, psb, 8);
+                fr_issue(d, wave, kt + NS - 1, pst, psb, 9);
+            }
+
+            stamp(2);
+#ifdef FR_NO_EPI
+            if (jb == 3 && sb == sb_end - 1) {
+#else
+            if (jb == 3) {
+#endif
+                // min term: sum_b m_b * (xs_hi + xs_lo)_b as one K = 16 product
+                // (lanes 0-31: k = blocks 0..7 on the hi plane, 32-63: the same
+                // blocks on the residual plane; B = the exact m in both halves)
+                h8 S[kTm];
+                rd128h<0>(S[0], lds0 + NS * kStage + sbo + kHdr + lane * 16);
+                rd128h<1024>(S[1], lds0 + NS * kStage + sbo + kHdr + lane * 16);
+                rd128h<2048>(S[2], lds0 + NS * kStage + sbo + kHdr + lane * 16);
+                rd128h<3072>(S[3], lds0 + NS * kStage + sbo + kHdr + lane * 16);
+                h8 mb[kRt];
+#pragma unroll
+                for (int r = 0; r < kRt; r++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) mb[r][j] = (_Float16)(float)q4k_m(hz[r], hw[r], j);
+                lgkm<0>(S);
+#pragma unroll
+                for (int r = 0; r < kRt; r++)
+#pragma unroll
+                    for (int t = 0; t < kTm; t++) {
+                        const f16v mm = __builtin_amdgcn_mfma_f32_32x32x16_f16(S[t], mb[r], f16v{}, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 16; i++) {
+                            acc[t][r][i] = fmaf(dsc[r], mn[t][r][i], acc[t][r][i]);
+                            acc[t][r][i] = fmaf(-dmn[r], mm[i], acc[t][r][i]);
+                        }
+                    }
+            }
+            stamp(3);
+        }
+    }
+
+    if (STAMP && lane == 0) {
+        for (int i = 0; i < 4; i++) atomicAdd(&g.stamp[i], ph[i]);
+        atomicAdd(&g.stamp[4], __builtin_amdgcn_s_memtime() - c_beg);
+        atomicAdd(&g.stamp[5], __builtin_amdgcn_s_memrealtime() - r_beg);
+    }
+    // D[token][row] -> y[token * N + row] * 2^E_token; the tile's 128 row
+    // scales go through a wave-private LDS slot (one load wait, not one per output)
+    float* esl = reinterpret_cast<float*>(smem + NS * kStage + 2 * kSbuf) + wave * kBm;
+#pragma unroll
+    for (int h = 0; h < kBm / 64; h++) {
+        const int m = m0 + 64 * h + lane;
+        esl[64 * h + lane] = m < g.M ? g.escale[m] : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int gl = lane >> 5;
+#pragma unroll
+    for (int r = 0; r < kRt; r++) {
+        const int n = n0 + (wave * kRt + r) * 32 + (lane & 31);
+#pragma unroll
+        for (int t = 0; t < kTm; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int ml = t * 32 + 8 * (i >> 2) + 4 * gl + (i & 3);
+                const int m = m0 + ml;
+                if (m < g.M && n < g.N) {
+                    const float val = acc[t][r][i] * esl[ml];
+                    if (ksplit == 1) g.y[(size_t)m * g.N + n] = val;
+                    else atomicAdd(&g.y[(size_t)m * g.N + n], val);
+                }
+            }
+    }
+}
+
+// Row exponents: escale[m] = 2^E_m, E_m the exponent of fl(max_b amax_b / 127)
+// over the row's blocks without a NaN (block scales are monotone in amax);
+// rows M..Mp-1 get 1. One wave per row.
+// From quantized blocks (ACT): the largest block scale of the row (fmaxf
+// skips a NaN block's scale), the same value.
+template <bool ACT>
+__global__ void __launch_bounds__(256) fr_rowexp_kernel(const float* __restrict__ x, ActView Aq, int M, int Mp,
+                                                        int K, float* __restrict__ escale) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= Mp) return;
+    const int lane = threadIdx.x & 63;
+    float mx = 0.0f;
+    if (ACT && m < M) {
+        const float* dr = Aq.d + (size_t)m * (K >> 5);
+        for (int b = lane; b < (K >> 5); b += 64) mx = fmaxf(mx, fabsf(dr[b]));
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    } else if (m < M) {
+        const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * K);
+        for (int i = lane; i < K / 4; i += 64) {
+            const float4 u = xr[i];
+            float amax = fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w)));
+            uint32_t nan = (u.x != u.x) | (u.y != u.y) | (u.z != u.z) | (u.w != u.w);
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+                nan |= __shfl_xor(nan, o, 8);
+            }
+            if (!nan) mx = fmaxf(mx, amax);
+        }
+#pragma unroll
+        for (int o = 8; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    }
+    if (!ACT) mx = mx / 127.0f;
+    int e = 0;
+    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+    if (lane == 0) escale[m] = ldexpf(1.0f, e);
+}
+
+// Planes of one 32-token tile and one super-block (grid: super-blocks x
+// tiles), from fp32 x: quantize each 32-element block exactly as
+// quantize_act_kernel does, form t = xd*q*2^(9-E) and its split, write the
+// tile's fragment-order pieces to LDS, then copy them out with contiguous
+// 16-byte stores (16 KiB HI, 8 KiB LO, 1 KiB SX). Wave w takes tokens
+// 4w..4w+3, lane l elements 4l..4l+3 of the super-block (8 lanes per block).
+// ACT: from the quantized blocks instead of x (codes, d and sum as stored).
+template <bool ACT>
+__global__ void __launch_bounds__(512) fr_planes_kernel(const float* __restrict__ x, ActView Aq, int M, int K,
+                                                        const float* __restrict__ escale, uint8_t* __restrict__ hi,
+                                                        uint8_t* __restrict__ lo, uint8_t* __restrict__ sx) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) uint8_t t_hi[16384];
+    __shared__ __attribute__((aligned(16))) uint8_t t_lo[8192];
+    __shared__ __attribute__((aligned(16))) uint8_t t_sx[1024];
+    const int sb = blockIdx.x, T = blockIdx.y;
+    const int ks_all = K >> 6, nsb = K >> 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ksl = lane >> 4;                    // K step within the super-block
+    const int hin = (lane >> 3) & 1;              // elements 32..63 of the step (high nibbles)
+    const int g = (lane >> 2) & 1, s = lane & 3;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = wave * 4 + j;               // token within the tile
+        const int m = T * 32 + r;
+        Q8Group q;
+        if (ACT) {
+            q.packed = 0;
+            q.d = 0.0f;
+            q.sum = 0.0f;
+            if (m < M) {
+                const size_t bi = (size_t)m * (K >> 5) + 8 * sb + (lane >> 3);
+                q.packed = *reinterpret_cast<const uint32_t*>(Aq.qs + (size_t)m * K + 256 * sb + 4 * lane);
+                q.d = Aq.d[bi];
+                q.sum = Aq.sum[bi];
+            }
+        } else {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (m < M) v = *reinterpret_cast<const float4*>(x + (size_t)m * K + 256 * sb + 4 * lane);
+            q = quant_group8(v);
+        }
+        const float inv = 1.0f / escale[T * 32 + r];     // a power of two: exact
+        const float ds = q.d * inv;
+        _Float16 h[4], rl[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float t = ds * (float)(int8_t)(q.packed >> (8 * c));
+            t = t * 512.0f;
+            asm volatile("" : "+v"(t));           // hi and lo both from fl32(t): no fused fp16 product
+            h[c] = (_Float16)t;
+            rl[c] = (_Float16)(t - (float)h[c]);
+        }
+        const int ln = 32 * g + r;                // fragment lane
+        // positions (hin ? 4 : 0) + {0, 2, 1, 3} hold elements c = 0, 1, 2, 3 -> store c order 0 2 1 3
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<h4*>(t_hi + ((ksl * 4 + s) * 64 + ln) * 16 + hin * 8) = h4{h[0], h[2], h[1], h[3]};
+        typedef short s2 __attribute__((ext_vector_type(2)));
+        s2 w = {0, 0};
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(w, h2{rl[0], rl[2]}, 1.0f, false);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(w, h2{rl[1], rl[3]}, 1.0f, true);
+        *reinterpret_cast<uint32_t*>(t_lo + ((ksl * 2 + (s >> 1)) * 64 + ln) * 16 + 8 * (s & 1) + 4 * hin) =
+            __builtin_bit_cast(uint32_t, w);
+        if ((lane & 7) == 0) {
+            const int bk = lane >> 3;
+            float xs = q.sum * inv;
+            asm volatile("" : "+v"(xs));
+            const _Float16 sh = (_Float16)xs;
+            reinterpret_cast<_Float16*>(t_sx)[r * 8 + bk] = sh;
+            reinterpret_cast<_Float16*>(t_sx)[(32 + r) * 8 + bk] = (_Float16)(xs - (float)sh);
+        }
+    }
+    __syncthreads();
+    const size_t tk = (size_t)T * ks_all + 4 * sb;
+    u32x4* dh = reinterpret_cast<u32x4*>(hi + tk * 4096);
+    u32x4* dl = reinterpret_cast<u32x4*>(lo + tk * 2048);
+    const int i = threadIdx.x;
+    dh[i] = reinterpret_cast<const u32x4*>(t_hi)[i];
+    dh[i + 512] = reinterpret_cast<const u32x4*>(t_hi)[i + 512];
+    dl[i] = reinterpret_cast<const u32x4*>(t_lo)[i];
+    if (i < 64) reinterpret_cast<u32x4*>(sx + ((size_t)T * nsb + sb) * 1024)[i] = reinterpret_cast<const u32x4*>(t_sx)[i];
+}
+
+struct FrPlanes {
+    uint8_t* hi;
+    uint8_t* lo;
+    uint8_t* sx;
+    float* escale;
+};
+
+size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
+
+FrPlanes carve_fr(void* base, int M, int K) {
+    const size_t Mp = (size_t)((M + 31) & ~31);
+    uint8_t* p = static_cast<uint8_t*>(base);
+    FrPlanes P;
+    P.hi = p;
+    p += up256(Mp * K * 2);
+    P.lo = p;
+    p += up256(Mp * K);
+    P.sx = p;
+    p += up256(Mp * (K / 256) * 32);
+    P.escale = reinterpret_cast<float*>(p);
+    return P;
+}
+
+}  // namespace
+
+size_t gemm_fr_planes_bytes(int M, int K) {
+    const size_t Mp = (size_t)((M + 31) & ~31);
+    return up256(Mp * K * 2) + up256(Mp * K) + up256(Mp * (K / 256) * 32) + up256(Mp * 4);
+}
+
+bool gemm_fr_supported(uint32_t type, int M, int K) {
+    return type == T_Q4_K && M >= kBm && K % 256 == 0 && K <= 32768;
+}
+
+// Planes from fp32 x (x != nullptr) or from quantized blocks A.
+hipError_t launch_fr_planes(const float* x, const ActView& A, void* planes, int M, int K, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    const FrPlanes P = carve_fr(planes, M, K);
+    const int Mp = (M + 31) & ~31;
+    const dim3 eg((Mp + 3) / 4), pg(K / 256, Mp / 32);
+    if (x) {
+        hipLaunchKernelGGL(fr_rowexp_kernel<false>, eg, dim3(256), 0, st, x, A, M, Mp, K, P.escale);
+        hipLaunchKernelGGL(fr_planes_kernel<false>, pg, dim3(512), 0, st, x, A, M, K, P.escale, P.hi, P.lo, P.sx);
+    } else {
+        hipLaunchKernelGGL(fr_rowexp_kernel<true>, eg, dim3(256), 0, st, x, A, M, Mp, K, P.escale);
+        hipLaunchKernelGGL(fr_planes_kernel<true>, pg, dim3(512), 0, st, x, A, M, K, P.escale, P.hi, P.lo, P.sx);
+    }
+    return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) fr_zero_kernel(float* __restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = 0.0f;
+}
+
+// Tiles of the grid that run whole: when the tiles beyond the last full
+// round of one workgroup per CU are at most half a round, they are split in
+// K instead (their two halves fill that round).
+static int fr_nfull(int ntiles, int K) {
+    const int cus = device_cu_count();
+    const int rem = cus > 0 ? ntiles % cus : 0;
+    return (rem > 0 && 2 * rem <= cus && (K >> 8) >= 2) ? ntiles - rem : ntiles;
+}
+
+hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st,
+                          unsigned long long* stamp) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    const FrPlanes P = carve_fr(planes, M, K);
+    const int ntm = (M + kBm - 1) / kBm, ntn = (N + kBn - 1) / kBn, ntiles = ntm * ntn;
+    FrArgs g{P.hi, P.lo, P.sx, P.escale, w, row_bytes(T_Q4_K, K), y, M, N, K, ntm, ntn, (M + 31) / 32,
+             fr_nfull(ntiles, K), stamp};
+    if (g.nfull < ntiles) {
+        // rows of the split tiles (and of whole tiles sharing those rows: they overwrite)
+        const size_t first = (size_t)(g.nfull / ntn) * kBm * N, n = (size_t)M * N - first;
+        hipLaunchKernelGGL(fr_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y + first, n);
+    }
+    constexpr int NS = 4;
+    const size_t lds = (size_t)NS * kStage + 2 * kSbuf + kNw * kBm * 4;
+    const long nblk = (long)g.nfull + 2L * (ntiles - g.nfull);
+    if (stamp) hipLaunchKernelGGL((gemm_q4k_fr<NS, true>), dim3((unsigned)nblk), dim3(256), lds, st, g);
+    else hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(256), lds, st, g);
+    return hipGetLastError();
+}
+
+}  // namespace lp

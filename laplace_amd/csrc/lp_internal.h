@@ -100,8 +100,17 @@ bool q6rq_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
 bool q6rq_preferred(uint32_t type, int M, int K, int N, const uint8_t* w);
 hipError_t launch_gemv_q6rq(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
 size_t gemm_planes_bytes(int M, int K);
+// Fragment-order planes and the prefill GEMM on them (lp_gemm_fr.hip);
+// launch_planes_from_x / launch_gemm_planes / launch_gemm take this route
+// where gemm_fr_preferred says so.
+size_t gemm_fr_planes_bytes(int M, int K);
+bool gemm_fr_supported(uint32_t type, int M, int K);
+hipError_t launch_fr_planes(const float* x, const ActView& A, void* planes, int M, int K, hipStream_t st);
+// stamp: phase-cycle sums of an instrumented build (null: the product kernel)
+hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st,
+                          unsigned long long* stamp = nullptr);
 // planes from fp32 x (quantize + planes in one pass)
-hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st);
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N);
 hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,
                               hipStream_t st);
 // planes from quantized activations A, then the product
