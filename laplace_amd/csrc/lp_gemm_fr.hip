@@ -60,17 +60,19 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef int i8x32 __attribute__((ext_vector_type(8)));   // 32 fp8 bytes
 
-constexpr int kTm = 4;            // 32-token tiles per workgroup (all waves share them)
-constexpr int kRt = 2;            // 32-row tiles per wave
-constexpr int kNw = 4;            // waves
-constexpr int kBm = 32 * kTm, kBn = 32 * kRt * kNw;
-constexpr int kHi = kTm * 4096, kLo = kTm * 2048, kCodes = kRt * kNw * 1024;
+constexpr int kTm = 4;            // 32-token tiles per workgroup
+constexpr int kTmW = 2;           // 32-token tiles per wave (token half th = wave & 1)
+constexpr int kRt = 2;            // 32-row tiles per wave (row quarter rq = wave >> 1)
+constexpr int kNw = 8;            // waves (two per SIMD)
+constexpr int kBm = 32 * kTm, kBn = 32 * kRt * (kNw * kTmW / kTm);
+constexpr int kHi = kTm * 4096, kLo = kTm * 2048, kCodes = (kBn / 32) * 1024;
 constexpr int kStage = kHi + kLo + kCodes;                   // 32 KiB
 constexpr int kHdr = kBn * 16, kSx = kTm * 1024;
 constexpr int kSbuf = kHdr + kSx;                            // 8 KiB
-constexpr int kDmaStep = 4 + 2 + kRt;                        // per wave and K step
-constexpr int kDmaSb = 2;                                    // per wave and super-block
-static_assert(kTm == kNw, "wave w copies token tile w");
+constexpr int kDmaStep = 4;                                  // per wave and K step
+constexpr int kDmaSb = 1;                                    // per wave and super-block
+static_assert(kHi / 1024 + kLo / 1024 + kCodes / 1024 == kNw * kDmaStep, "copies split evenly");
+static_assert(kHdr / 1024 + kSx / 1024 == kNw * kDmaSb, "super-block copies split evenly");
 
 struct FrArgs {
     const uint8_t* hi;
@@ -147,41 +149,46 @@ __device__ __forceinline__ uint32_t q4k_m(uint32_t hz, uint32_t hw, int j) {
 }
 
 // Per wave: copy sources fixed for the tile; a step changes scalar offsets.
+// Waves 0-3 copy the hi plane of token tile `wave` (four 1 KiB pieces per
+// step) and the headers of rows 64*wave..+64 (per super-block); waves 4-7
+// copy the lo plane of token tile wave-4 and the codes of row tiles
+// 2(wave-4), +1, and that token tile's min-term planes.
 struct FrPlan {
-    Rsrc rs_hi, rs_lo, rs_w, rs_sx;
-    uint32_t code_off[kRt], hdr_off;
-    int ks_all, nsb_all;
+    Rsrc rs_a, rs_b;          // waves 0-3: hi, weights; waves 4-7: lo, weights
+    Rsrc rs_sx;
+    uint32_t off_b[2];        // per-lane weight offsets (codes or header)
 };
 
-// Copy i of K step kt into stage `st` / super-block buffer `sbb`: 0-3 the hi
-// sub-steps, 4-5 the lo halves, 6-7 the two row tiles' codes, 8-9 the
-// super-block's headers and min-term planes (steps that start one). The
-// copies move through the CU's vector-memory path at ~64 B per clock and a
-// wave's issue waits for it, so the compute loop issues one copy after each
-// fp8 MFMA (64 cycles of MFMA work) instead of a burst.
+// Copy i (0..3) of K step kt into stage `st`; i = 4: the super-block's
+// copy into `sbb` (steps that start one). The copies move through the CU's
+// vector-memory path at ~64 B per clock and a wave's issue waits for it, so
+// the compute loop issues one copy after each fp8 MFMA instead of a burst.
 __device__ __forceinline__ void fr_issue(const FrPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
 #ifdef FR_NO_DMA
     if (kt >= 3) return;
 #endif
     const uint32_t lane16 = (threadIdx.x & 63) * 16;
     const int sb = kt >> 2, jb = kt & 3;
-    if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
-    else if (i < 6) dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (i - 4) * 1024), st + kHi + wave * 2048 + (i - 4) * 1024);
-    else if (i < 8)
-        dma16(d.rs_w, d.code_off[i - 6], (uint32_t)(sb * 144 + 32 * jb), st + kHi + kLo + (wave * kRt + i - 6) * 1024);
-    else if (jb == 0) {
-        if (i == 8) dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
-        else dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + kHdr + wave * 1024);
+    if (wave < 4) {
+        if (i < 4) dma16(d.rs_a, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
+        else if (jb == 0) dma16(d.rs_b, d.off_b[0], (uint32_t)(sb * 144), sbb + wave * 1024);
+    } else {
+        const int j = wave - 4;
+        if (i < 2) dma16(d.rs_a, lane16, (uint32_t)(kt * 2048 + i * 1024), st + kHi + j * 2048 + i * 1024);
+        else if (i < 4)
+            dma16(d.rs_b, d.off_b[i - 2], (uint32_t)(sb * 144 + 32 * jb), st + kHi + kLo + (2 * j + i - 2) * 1024);
+        else if (jb == 0) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + kHdr + j * 1024);
     }
 }
 
 __device__ __forceinline__ int fr_count(int k, int nk) { return k < nk ? kDmaStep + ((k & 3) == 0 ? kDmaSb : 0) : 0; }
 
 // STAMP: an instrumented build that sums s_memtime cycles per phase of a K
-// step (copy wait + barrier, copy issue, fp16/fp8 products, super-block
-// epilogue) into g.stamp; each stamp sits where no LDS read is in flight.
+// step (copy wait + barrier, -, products, super-block epilogue) into g.stamp
+// (plus whole-loop s_memtime and s_memrealtime, for the clock); each stamp
+// sits where no LDS read is in flight.
 template <int NS, bool STAMP = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(64 * kNw) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_q4k_fr(FrArgs g) {
     unsigned long long ph[4] = {0, 0, 0, 0}, tprev = 0;
     const unsigned long long c_beg = STAMP ? __builtin_amdgcn_s_memtime() : 0;
@@ -196,12 +203,11 @@ gemm_q4k_fr(FrArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // blocks are dealt to the 8 XCDs round-robin: each XCD gets a contiguous
-    // run of tiles, row tiles fastest (the workgroups in flight on one XCD
-    // share their activation tile in its L2)
+    const int th = wave & 1, rq = wave >> 1;
     // the whole tiles first; blocks are dealt to the 8 XCDs round-robin, so
-    // each XCD gets a contiguous run of them. The split tiles fill the last
-    // round of the grid with half-length work.
+    // each XCD gets a contiguous run of them, row tiles fastest (the
+    // workgroups in flight on one XCD share their activation tile in its L2).
+    // The split tiles fill the last round of the grid with half-length work.
     const int bid = blockIdx.x;
     int tile, part = 0, ksplit = 1;
     if (bid < g.nfull) {
@@ -219,33 +225,39 @@ gemm_q4k_fr(FrArgs g) {
 
     FrPlan d;
     {
-        int T = tm * kTm + wave;                               // this wave's token tile for the copies
+        int T = tm * kTm + (wave & 3);                         // token tile this wave copies
         T = T < g.tiles_pad ? T : g.tiles_pad - 1;
-        d.rs_hi = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
-        d.rs_lo = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
-        d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
         const int nt = g.N - n0 < kBn ? g.N - n0 : kBn;
-        d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+        d.rs_b = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+        d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
+        if (wave < 4) {
+            d.rs_a = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
+            int hrow = wave * 64 + lane;
+            hrow = hrow < nt ? hrow : nt - 1;
+            d.off_b[0] = d.off_b[1] = (uint32_t)((size_t)hrow * g.rb);
+        } else {
+            d.rs_a = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
 #pragma unroll
-        for (int r = 0; r < kRt; r++) {
-            int row = (wave * kRt + r) * 32 + (lane & 31);
-            row = row < nt ? row : nt - 1;
-            d.code_off[r] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
+            for (int r = 0; r < 2; r++) {
+                int row = (2 * (wave - 4) + r) * 32 + (lane & 31);
+                row = row < nt ? row : nt - 1;
+                d.off_b[r] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
+            }
         }
-        int hrow = wave * 64 + lane;
-        hrow = hrow < nt ? hrow : nt - 1;
-        d.hdr_off = (uint32_t)((size_t)hrow * g.rb);
     }
     auto stage = [&](int i) { return smem + i * kStage; };
     auto sbuf = [&](int i) { return smem + NS * kStage + i * kSbuf; };
 
     const uint32_t lds0 = lds_addr(smem);
-    const uint32_t l16 = lds0 + lane * 16;
-    const uint32_t hdr_a = lds0 + NS * kStage + (wave * 64 + (lane & 31)) * 16;   // + rt * 512
+    const uint32_t l16 = lds0 + lane * 16 + th * (kTmW * 4096);     // + this wave's token tiles
+    const uint32_t l16lo = lds0 + lane * 16 + kHi + th * (kTmW * 2048);
+    const uint32_t l16c = lds0 + lane * 16 + kHi + kLo + rq * (kRt * 1024);
+    const uint32_t hdr_a = lds0 + NS * kStage + (rq * 64 + (lane & 31)) * 16;   // + r * 512
+    const uint32_t sx_a = lds0 + NS * kStage + kHdr + th * (kTmW * 1024) + lane * 16;
 
-    f16v acc[kTm][kRt], mn[kTm][kRt];
+    f16v acc[kTmW][kRt], mn[kTmW][kRt];
 #pragma unroll
-    for (int a = 0; a < kTm; a++)
+    for (int a = 0; a < kTmW; a++)
 #pragma unroll
         for (int b = 0; b < kRt; b++)
 #pragma unroll
@@ -259,7 +271,7 @@ gemm_q4k_fr(FrArgs g) {
     for (int i = 0; i < NS - 1; i++)
         if (kt0 + i < nk)
 #pragma unroll
-            for (int p = 0; p < 10; p++) fr_issue(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
+            for (int p = 0; p < 5; p++) fr_issue(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
 
     for (int sb = sb_beg; sb < sb_end; sb++) {
         const uint32_t sbo = (uint32_t)((sb & 1) * kSbuf);
@@ -270,7 +282,9 @@ gemm_q4k_fr(FrArgs g) {
 #pragma unroll
             for (int i = 1; i < NS - 1; i++) later += fr_count(kt + i, nk);
             stamp(-1);
+#ifndef FR_NO_WAIT
             wait_dma(later);
+#endif
             // after this barrier every wave has finished step kt-1, whose
             // stage is the one step kt+NS-1 is copied into
 #ifndef FR_NO_BAR
@@ -313,20 +327,27 @@ gemm_q4k_fr(FrArgs g) {
 
             const uint32_t b = l16 + so;
             u32x4 cw[kRt];
-            h8 A[2][kTm];
-            rd128<kHi + kLo>(cw[0], b + (wave * kRt) * 1024);
-            rd128<kHi + kLo + 1024>(cw[1], b + (wave * kRt) * 1024);
+            // the whole step's fragments are requested up front (14 LDS reads
+            // in flight: codes, four hi sub-steps, the lo pair) and waited for
+            // in order
+            h8 A[4][kTmW];
+            u32x4 L[kTmW][2];
+            rd128<0>(cw[0], l16c + so);
+            rd128<1024>(cw[1], l16c + so);
             rd128h<0>(A[0][0], b);
             rd128h<4096>(A[0][1], b);
-            rd128h<8192>(A[0][2], b);
-            rd128h<12288>(A[0][3], b);
             rd128h<1024>(A[1][0], b);
             rd128h<1024 + 4096>(A[1][1], b);
-            rd128h<1024 + 8192>(A[1][2], b);
-            rd128h<1024 + 12288>(A[1][3], b);
-            lgkm<8>(cw);
+            rd128h<2048>(A[2][0], b);
+            rd128h<2048 + 4096>(A[2][1], b);
+            rd128h<3072>(A[3][0], b);
+            rd128h<3072 + 4096>(A[3][1], b);
+            rd128<0>(L[0][0], l16lo + so);
+            rd128<1024>(L[0][1], l16lo + so);
+            rd128<2048>(L[1][0], l16lo + so);
+            rd128<3072>(L[1][1], l16lo + so);
+            lgkm<12>(cw);
             uint32_t v8[kRt][8];
-            u32x4 L[kTm][2];
             // software-pipelined: sub-step s+1's weights are decoded (and s's
             // converted to e4m3) between sub-step s's MFMAs
             h8 Vc[kRt];
@@ -334,16 +355,16 @@ gemm_q4k_fr(FrArgs g) {
             for (int r = 0; r < kRt; r++) Vc[r] = decode4(cw[r][0], ml[r], al[r], mh[r], ah[r]);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                if (s == 0) lgkm<4>(A[0]);
-                else if (s == 1) lgkm<4>(A[1]);
-                else if (s == 2) lgkm<4>(A[0]);
-                else lgkm<8>(A[1]);
+                if (s == 0) lgkm<10>(A[0]);
+                else if (s == 1) lgkm<8>(A[1]);
+                else if (s == 2) lgkm<6>(A[2]);
+                else lgkm<4>(A[3]);
                 h8 Vn[kRt];
 #pragma unroll
                 for (int r = 0; r < kRt; r++)
 #pragma unroll
-                    for (int t = 0; t < kTm; t++)
-                        mn[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s & 1][t], Vc[r],
+                    for (int t = 0; t < kTmW; t++)
+                        mn[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s][t], Vc[r],
                                                                           (jb == 0 && s == 0) ? f16v{} : mn[t][r],
                                                                           0, 0, 0);
                 if (s < 3) {
@@ -359,16 +380,11 @@ gemm_q4k_fr(FrArgs g) {
 #pragma unroll
                 for (int r = 0; r < kRt; r++) {
                     const u32x4 q = __builtin_bit_cast(u32x4, Vc[r]);
-#ifdef FR_NO_DECODE
-                    v8[r][2 * s] = q.x;
-                    v8[r][2 * s + 1] = q.y;
-#else
                     v8[r][2 * s] = e4m3x4(q.x, q.y);
                     v8[r][2 * s + 1] = e4m3x4(q.z, q.w);
-#endif
                 }
 #pragma unroll
-                for (int i = 0; i < 2 * kTm; i++) {
+                for (int i = 0; i < kRt * kTmW; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
                     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // then up to four VALU
                 }
@@ -377,58 +393,25 @@ gemm_q4k_fr(FrArgs g) {
 #pragma unroll
                     for (int r = 0; r < kRt; r++) Vc[r] = Vn[r];
                 }
-#ifdef FR_NO_LDS
-                if (kt > 0) {
-                    asm volatile("" : "+v"(A[0][0]), "+v"(A[0][1]), "+v"(A[0][2]), "+v"(A[0][3]));
-                    asm volatile("" : "+v"(A[1][0]), "+v"(A[1][1]), "+v"(A[1][2]), "+v"(A[1][3]));
-                    for (int t = 0; t < kTm; t++) asm volatile("" : "+v"(L[t][0]), "+v"(L[t][1]));
-                } else
-#endif
-                if (s == 0) {
-                    rd128h<2048>(A[0][0], b);
-                    rd128h<2048 + 4096>(A[0][1], b);
-                    rd128h<2048 + 8192>(A[0][2], b);
-                    rd128h<2048 + 12288>(A[0][3], b);
-                } else if (s == 1) {
-                    rd128h<3072>(A[1][0], b);
-                    rd128h<3072 + 4096>(A[1][1], b);
-                    rd128h<3072 + 8192>(A[1][2], b);
-                    rd128h<3072 + 12288>(A[1][3], b);
-                } else if (s == 2) {
-                    rd128<kHi>(L[0][0], b);
-                    rd128<kHi + 1024>(L[0][1], b);
-                    rd128<kHi + 2048>(L[1][0], b);
-                    rd128<kHi + 3072>(L[1][1], b);
-                    rd128<kHi + 4096>(L[2][0], b);
-                    rd128<kHi + 5120>(L[2][1], b);
-                    rd128<kHi + 6144>(L[3][0], b);
-                    rd128<kHi + 7168>(L[3][1], b);
-                }
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-            for (int t = 0; t < kTm; t++) {
-                asm volatile("" : "+v"(L[t][0]), "+v"(L[t][1]));
-            }
+            for (int t = 0; t < kTmW; t++) asm volatile("" : "+v"(L[t][0]), "+v"(L[t][1]));
 #pragma unroll
             for (int r = 0; r < kRt; r++) {
                 const i8x32 bv = {(int)v8[r][0], (int)v8[r][1], (int)v8[r][2], (int)v8[r][3],
                                   (int)v8[r][4], (int)v8[r][5], (int)v8[r][6], (int)v8[r][7]};
 #pragma unroll
-                for (int t = 0; t < kTm; t++) {
+                for (int t = 0; t < kTmW; t++) {
                     const i8x32 av = {(int)L[t][0].x, (int)L[t][0].y, (int)L[t][0].z, (int)L[t][0].w,
                                       (int)L[t][1].x, (int)L[t][1].y, (int)L[t][1].z, (int)L[t][1].w};
                     mn[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, mn[t][r], 0, 0, 0, 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
-                    if (pf) fr_issue(d, wave, kt + NS - 1, pst, psb, r * kTm + t);
+                    if (pf) fr_issue(d, wave, kt + NS - 1, pst, psb, r * kTmW + t);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (pf) {
-                fr_issue(d, wave, kt + NS - 1, pst, psb, 8);
-                fr_issue(d, wave, kt + NS - 1, pst, psb, 9);
-            }
-
+            if (pf) fr_issue(d, wave, kt + NS - 1, pst, psb, 4);
             stamp(2);
 #ifdef FR_NO_EPI
             if (jb == 3 && sb == sb_end - 1) {
@@ -438,11 +421,9 @@ gemm_q4k_fr(FrArgs g) {
                 // min term: sum_b m_b * (xs_hi + xs_lo)_b as one K = 16 product
                 // (lanes 0-31: k = blocks 0..7 on the hi plane, 32-63: the same
                 // blocks on the residual plane; B = the exact m in both halves)
-                h8 S[kTm];
-                rd128h<0>(S[0], lds0 + NS * kStage + sbo + kHdr + lane * 16);
-                rd128h<1024>(S[1], lds0 + NS * kStage + sbo + kHdr + lane * 16);
-                rd128h<2048>(S[2], lds0 + NS * kStage + sbo + kHdr + lane * 16);
-                rd128h<3072>(S[3], lds0 + NS * kStage + sbo + kHdr + lane * 16);
+                h8 S[kTmW];
+                rd128h<0>(S[0], sx_a + sbo);
+                rd128h<1024>(S[1], sx_a + sbo);
                 h8 mb[kRt];
 #pragma unroll
                 for (int r = 0; r < kRt; r++)
@@ -452,7 +433,7 @@ gemm_q4k_fr(FrArgs g) {
 #pragma unroll
                 for (int r = 0; r < kRt; r++)
 #pragma unroll
-                    for (int t = 0; t < kTm; t++) {
+                    for (int t = 0; t < kTmW; t++) {
                         const f16v mm = __builtin_amdgcn_mfma_f32_32x32x16_f16(S[t], mb[r], f16v{}, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 16; i++) {
@@ -470,25 +451,22 @@ gemm_q4k_fr(FrArgs g) {
         atomicAdd(&g.stamp[4], __builtin_amdgcn_s_memtime() - c_beg);
         atomicAdd(&g.stamp[5], __builtin_amdgcn_s_memrealtime() - r_beg);
     }
-    // D[token][row] -> y[token * N + row] * 2^E_token; the tile's 128 row
+    // D[token][row] -> y[token * N + row] * 2^E_token; the wave's 64 row
     // scales go through a wave-private LDS slot (one load wait, not one per output)
-    float* esl = reinterpret_cast<float*>(smem + NS * kStage + 2 * kSbuf) + wave * kBm;
-#pragma unroll
-    for (int h = 0; h < kBm / 64; h++) {
-        const int m = m0 + 64 * h + lane;
-        esl[64 * h + lane] = m < g.M ? g.escale[m] : 0.0f;
-    }
+    const int mw = m0 + th * 32 * kTmW;
+    float* esl = reinterpret_cast<float*>(smem + NS * kStage + 2 * kSbuf) + wave * 64;
+    esl[lane] = mw + lane < g.M ? g.escale[mw + lane] : 0.0f;
     __builtin_amdgcn_wave_barrier();
     const int gl = lane >> 5;
 #pragma unroll
     for (int r = 0; r < kRt; r++) {
-        const int n = n0 + (wave * kRt + r) * 32 + (lane & 31);
+        const int n = n0 + (rq * kRt + r) * 32 + (lane & 31);
 #pragma unroll
-        for (int t = 0; t < kTm; t++)
+        for (int t = 0; t < kTmW; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int ml = t * 32 + 8 * (i >> 2) + 4 * gl + (i & 3);
-                const int m = m0 + ml;
+                const int m = mw + ml;
                 if (m < g.M && n < g.N) {
                     const float val = acc[t][r][i] * esl[ml];
                     if (ksplit == 1) g.y[(size_t)m * g.N + n] = val;
@@ -696,10 +674,10 @@ hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K
         hipLaunchKernelGGL(fr_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y + first, n);
     }
     constexpr int NS = 4;
-    const size_t lds = (size_t)NS * kStage + 2 * kSbuf + kNw * kBm * 4;
+    const size_t lds = (size_t)NS * kStage + 2 * kSbuf + kNw * 64 * 4;
     const long nblk = (long)g.nfull + 2L * (ntiles - g.nfull);
-    if (stamp) hipLaunchKernelGGL((gemm_q4k_fr<NS, true>), dim3((unsigned)nblk), dim3(256), lds, st, g);
-    else hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(256), lds, st, g);
+    if (stamp) hipLaunchKernelGGL((gemm_q4k_fr<NS, true>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
+    else hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
     return hipGetLastError();
 }
 
