@@ -716,6 +716,24 @@ def load_traffic(name):
         return json.load(f).get("traffic_bytes_per_launch")
 
 
+GEMM_SWEEP = [(n, 4096, m) for n in (2048, 4096, 8192, 14336) for m in (128, 256, 512, 1024, 2048)] + \
+    [(4096, 14336, 512), (4096, 14336, 2048)]
+GEMM_KERNELS = {1: "split-precision, row-major planes", 2: "fragment-order planes", 3: "int8 MFMA"}
+
+
+def gemm_sweep(g: Gpu):
+    """Step time of the Q4_K prefill GEMM (quantize/planes + product) per
+    kernel family over GEMM_SWEEP shapes (N, K, M); the routing table of
+    lp_gemm comes from these lines."""
+    for (n, k, m) in GEMM_SWEEP:
+        for kern, name in GEMM_KERNELS.items():
+            g.check(g.L.lp_set_gemm_kernel(kern), "lp_set_gemm_kernel")
+            r = measure_gemm(g, n, k, m, reps=10)
+            print(json.dumps({"kernel": kern, "family": name, **r}), flush=True)
+        g.torch.cuda.empty_cache()
+    g.check(g.L.lp_set_gemm_kernel(0), "lp_set_gemm_kernel")
+
+
 READ_SWEEP_BYTES = [33_030_144, 49_545_216, 66_060_288, 99_090_432, 132_120_576, 198_180_864,
                     264_241_152, 330_301_440, 415_236_096]
 
@@ -749,6 +767,9 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run N torch device copies of 256 MiB (a copy kernel of known "
                          "size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the Q4_K prefill GEMM, every kernel family (lp_set_gemm_kernel 1-3) over "
+                         "a grid of shapes, one JSON line each")
     ap.add_argument("--read-sweep", action="store_true",
                     help="only the streaming-read ceiling (lp_read_probe_dev) over read sizes "
                          "from the headline weight (33 MB) to the LM head (415 MB), one JSON line each")
@@ -768,6 +789,9 @@ def main():
         del a, b
     if args.read_sweep:
         read_sweep(g)
+        return
+    if args.gemm_sweep:
+        gemm_sweep(g)
         return
     t, N, K, M = Q4_K, 14336, 4096, 1
     r = measure_gemv(g, t, N, K, M, args.steps, args.warmup, read_ceiling=True)

@@ -227,6 +227,14 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
 
 /* ---- diagnostics ----------------------------------------------------------- */
 
+/* Kernel-family switch for the Q4_K prefill GEMM (M > 64), no reference
+ * counterpart; for comparison runs and tests. 0: chosen by shape (default);
+ * 1: split-precision fp16/fp8 MFMA on row-major planes; 2: fp16/fp8 MFMA on
+ * MFMA-fragment-order planes; 3: int8 MFMA with a per-block fp32 epilogue.
+ * All four meet the same parity bar. Process-wide; not thread-safe against
+ * concurrent matmul calls. Returns LP_EINVAL for other values. */
+int lp_set_gemm_kernel(int kernel);
+
 /* Routing probe, no reference counterpart: the name of the kernel family
  * lp_gemm_q_dev runs for these operands (with a workspace of
  * lp_act_workspace_bytes(M, K) bytes; the first chunk's kernel when M rows

@@ -24,7 +24,7 @@ OBJ = os.path.join(ROOT, "_build", "obj")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_gemm_fr.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_rq.hip", "lp_q6rq.hip", "lp_api.cpp"]
+SOURCES = ["lp_gemv.hip", "lp_gemm.hip", "lp_gemm_fr.hip", "lp_gemm_i8.hip", "lp_dequant.hip", "lp_moe_ffn.hip", "lp_rq.hip", "lp_q6rq.hip", "lp_api.cpp"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
@@ -36,7 +36,7 @@ CFLAGS = [
 
 # Per-source additions. lp_rq.hip: MFMA results in VGPRs (its int8 block sums
 # feed VALU at once; the AGPR form costs a v_accvgpr_read per value).
-SRC_FLAGS = {"lp_rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_q6rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SRC_FLAGS = {"lp_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_q6rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> str:

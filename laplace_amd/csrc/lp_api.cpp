@@ -382,7 +382,7 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         const ActView A = ws_view_full(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
-    } else if (use_gemm(type, M, K, N, wd)) {
+    } else if (use_gemm(type, M, K, N, wd) && !gemm_i8_preferred(type, M, K, N)) {
         void* planes = ws_planes(c->ws, M, K);
         LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream, N));
         LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
@@ -709,7 +709,7 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
         LP_HIP(launch_gemv_fused(type, w, x, y, M, K, N, static_cast<hipStream_t>(stream)));
         return LP_OK;
     }
-    if (use_gemm(type, M, K, N, w)) {
+    if (use_gemm(type, M, K, N, w) && !gemm_i8_preferred(type, M, K, N)) {
         // fp16 planes straight from x (one pass), then the MFMA product
         if (wsb < ws_bytes(M, K) || (M > 0 && (!x || !y))) {
             set_err("workspace %zu < %zu bytes or null pointer", wsb, ws_bytes(M, K));
@@ -1158,6 +1158,15 @@ int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int un
         return LP_EINVAL;
     }
     LP_HIP(launch_read_probe(buf, bytes, grid, block, unroll, sink, static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
+int lp_set_gemm_kernel(int kernel) {
+    if (kernel < 0 || kernel > 3) {
+        set_err("kernel %d: 0 (by shape), 1, 2 or 3", kernel);
+        return LP_EINVAL;
+    }
+    set_gemm_kernel(kernel);
     return LP_OK;
 }
 

@@ -24,7 +24,6 @@
 // two-plane fp16 form (hi = fp16(xd*q), lo = fp16(xd*q - hi)) on
 // v_mfma_f32_16x16x32_f16 (gemv_q4k_mf).
 #include <hip/hip_runtime.h>
-#include <stdlib.h>
 
 #include "lp_chunks.h"
 #include "lp_internal.h"
@@ -1264,20 +1263,36 @@ size_t gemm_planes_bytes(int M, int K) {
     auto r = [&](size_t v) { return (v + up - 1) / up * up; };
     const size_t sp = 2 * r((size_t)M * K * 2) + 2 * r((size_t)M * (K / 32) * 2) + r((size_t)M * 4);
     const size_t fr = gemm_fr_supported(T_Q4_K, M, K) ? gemm_fr_planes_bytes(M, K) : 0;
-    return sp > fr ? sp : fr;
+    const size_t i8 = gemm_i8_supported(T_Q4_K, M, K) ? gemm_i8_planes_bytes(M, K) : 0;
+    const size_t a = sp > fr ? sp : fr;
+    return a > i8 ? a : i8;
 }
 
-// The fragment-order GEMM (lp_gemm_fr.hip) for these shapes. LP_GEMM_FR=0
-// keeps the split-precision kernel (comparison runs).
+// Prefill GEMM kernel family: 0 = by shape (fr_auto), 1 = the
+// split-precision kernel on row-major planes (gemm_q4k_sp), 2 = the
+// fragment-order kernel (gemm_q4k_fr), 3 = the int8-MFMA kernel
+// (gemm_q4k_i8; measured slower, kept for comparison runs).
+static int g_gemm_kernel = 0;
+void set_gemm_kernel(int k) { g_gemm_kernel = k; }
+
+bool gemm_i8_preferred(uint32_t type, int M, int K, int N) {
+    return g_gemm_kernel == 3 && gemm_i8_supported(type, M, K) && N > 0;
+}
+
+// By shape: the fragment-order kernel where it measured faster by 5-11 %
+// (bench.py --gemm-sweep: N 8192 / 14336 at M 256..512), the split-precision
+// kernel elsewhere (equal within a few percent at M >= 1024, faster below 256
+// tokens, where the fragment-order planes' two passes over x cost more).
+static bool fr_auto(int M, int K, int N) {
+    (void)K;
+    return M >= 256 && M <= 768 && N >= 8192;
+}
+
 static bool gemm_fr_preferred(int M, int K, int N) {
-    static const int env = [] {
-        const char* e = getenv("LP_GEMM_FR");
-        return e ? atoi(e) : -1;
-    }();
-    if (env == 0 || !gemm_fr_supported(T_Q4_K, M, K)) return false;
-    return N >= 256;
+    if (!gemm_fr_supported(T_Q4_K, M, K) || N < 128) return false;
+    if (g_gemm_kernel == 1 || g_gemm_kernel == 3) return false;
+    return g_gemm_kernel == 2 || fr_auto(M, K, N);
 }
-
 
 bool gemm_supported(uint32_t type, int M, int K) {
     return type == T_Q4_K && M >= kMfMinM && K % 256 == 0;
@@ -1365,6 +1380,7 @@ hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* 
                        int M, int K, int N, hipStream_t st) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
+    if (gemm_i8_preferred(type, M, K, N)) return launch_gemm_i8(w, A, planes, y, M, K, N, st);
     hipError_t e = gemm_fr_preferred(M, K, N) ? launch_fr_planes(nullptr, A, planes, M, K, st)
                                               : launch_planes_from_act(A, planes, M, K, st);
     if (e != hipSuccess) return e;

@@ -62,17 +62,17 @@ typedef int i8x32 __attribute__((ext_vector_type(8)));   // 32 fp8 bytes
 
 constexpr int kTm = 4;            // 32-token tiles per workgroup
 constexpr int kTmW = 2;           // 32-token tiles per wave (token half th = wave & 1)
-constexpr int kRt = 2;            // 32-row tiles per wave (row quarter rq = wave >> 1)
-constexpr int kNw = 8;            // waves (two per SIMD)
+constexpr int kRt = 2;            // 32-row tiles per wave (row half rq = wave >> 1)
+constexpr int kNw = 4;            // waves; two workgroups per CU
 constexpr int kBm = 32 * kTm, kBn = 32 * kRt * (kNw * kTmW / kTm);
 constexpr int kHi = kTm * 4096, kLo = kTm * 2048, kCodes = (kBn / 32) * 1024;
-constexpr int kStage = kHi + kLo + kCodes;                   // 32 KiB
+constexpr int kStage = kHi + kLo + kCodes;                   // 28 KiB
 constexpr int kHdr = kBn * 16, kSx = kTm * 1024;
-constexpr int kSbuf = kHdr + kSx;                            // 8 KiB
-constexpr int kDmaStep = 4;                                  // per wave and K step
-constexpr int kDmaSb = 1;                                    // per wave and super-block
+constexpr int kSbuf = kHdr + kSx;                            // 6 KiB
+constexpr int kDmaStep = 7;                                  // per wave and K step
 static_assert(kHi / 1024 + kLo / 1024 + kCodes / 1024 == kNw * kDmaStep, "copies split evenly");
-static_assert(kHdr / 1024 + kSx / 1024 == kNw * kDmaSb, "super-block copies split evenly");
+static_assert(kSx / 1024 == kNw && kHdr / 1024 == 2, "super-block copies: one min-term piece per wave, "
+                                                      "headers on waves 0-1");
 
 struct FrArgs {
     const uint8_t* hi;
@@ -149,46 +149,43 @@ __device__ __forceinline__ uint32_t q4k_m(uint32_t hz, uint32_t hw, int j) {
 }
 
 // Per wave: copy sources fixed for the tile; a step changes scalar offsets.
-// Waves 0-3 copy the hi plane of token tile `wave` (four 1 KiB pieces per
-// step) and the headers of rows 64*wave..+64 (per super-block); waves 4-7
-// copy the lo plane of token tile wave-4 and the codes of row tiles
-// 2(wave-4), +1, and that token tile's min-term planes.
+// Wave w copies token tile w's hi (four 1 KiB pieces per step) and lo (two)
+// planes and row tile w's codes (one), and per super-block token tile w's
+// min-term planes; waves 0-1 also the headers of rows 64w..+64.
 struct FrPlan {
-    Rsrc rs_a, rs_b;          // waves 0-3: hi, weights; waves 4-7: lo, weights
-    Rsrc rs_sx;
-    uint32_t off_b[2];        // per-lane weight offsets (codes or header)
+    Rsrc rs_hi, rs_lo, rs_w, rs_sx;
+    uint32_t code_off, hdr_off;
 };
 
-// Copy i (0..3) of K step kt into stage `st`; i = 4: the super-block's
-// copy into `sbb` (steps that start one). The copies move through the CU's
-// vector-memory path at ~64 B per clock and a wave's issue waits for it, so
-// the compute loop issues one copy after each fp8 MFMA instead of a burst.
+// Copy i of K step kt into stage `st` (i = 0..6), or of the super-block that
+// kt starts into `sbb` (i = 7: min-term planes, 8: headers). The copies move
+// through the CU's vector-memory path at ~64 B per clock and a wave's issue
+// waits for it, so the compute loop spreads them over its fp8 MFMAs.
 __device__ __forceinline__ void fr_issue(const FrPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
 #ifdef FR_NO_DMA
     if (kt >= 3) return;
 #endif
     const uint32_t lane16 = (threadIdx.x & 63) * 16;
     const int sb = kt >> 2, jb = kt & 3;
-    if (wave < 4) {
-        if (i < 4) dma16(d.rs_a, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
-        else if (jb == 0) dma16(d.rs_b, d.off_b[0], (uint32_t)(sb * 144), sbb + wave * 1024);
-    } else {
-        const int j = wave - 4;
-        if (i < 2) dma16(d.rs_a, lane16, (uint32_t)(kt * 2048 + i * 1024), st + kHi + j * 2048 + i * 1024);
-        else if (i < 4)
-            dma16(d.rs_b, d.off_b[i - 2], (uint32_t)(sb * 144 + 32 * jb), st + kHi + kLo + (2 * j + i - 2) * 1024);
-        else if (jb == 0) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + kHdr + j * 1024);
+    if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
+    else if (i < 6) dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (i - 4) * 1024), st + kHi + wave * 2048 + (i - 4) * 1024);
+    else if (i == 6) dma16(d.rs_w, d.code_off, (uint32_t)(sb * 144 + 32 * jb), st + kHi + kLo + wave * 1024);
+    else if (jb == 0) {
+        if (i == 7) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + kHdr + wave * 1024);
+        else if (wave < 2) dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
     }
 }
 
-__device__ __forceinline__ int fr_count(int k, int nk) { return k < nk ? kDmaStep + ((k & 3) == 0 ? kDmaSb : 0) : 0; }
+__device__ __forceinline__ int fr_count(int k, int nk, int wave) {
+    return k < nk ? kDmaStep + ((k & 3) == 0 ? (wave < 2 ? 2 : 1) : 0) : 0;
+}
 
 // STAMP: an instrumented build that sums s_memtime cycles per phase of a K
 // step (copy wait + barrier, -, products, super-block epilogue) into g.stamp
 // (plus whole-loop s_memtime and s_memrealtime, for the clock); each stamp
 // sits where no LDS read is in flight.
 template <int NS, bool STAMP = false>
-__global__ void __launch_bounds__(64 * kNw) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(64 * kNw, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_q4k_fr(FrArgs g) {
     unsigned long long ph[4] = {0, 0, 0, 0}, tprev = 0;
     const unsigned long long c_beg = STAMP ? __builtin_amdgcn_s_memtime() : 0;
@@ -217,7 +214,18 @@ gemm_q4k_fr(FrArgs g) {
         part = (bid - g.nfull) & 1;
         ksplit = 2;
     }
-    const int tm = tile / g.ntn, tn = tile % g.ntn;
+    // groups of FR_GM token tiles walk the weight tiles together (the
+    // workgroups in flight share both operands in L2)
+#ifndef FR_GM
+#define FR_GM 2
+#endif
+    int tm, tn;
+    {
+        const int per = FR_GM * g.ntn, grp = tile / per, in = tile % per;
+        const int gm = g.ntm - grp * FR_GM < FR_GM ? g.ntm - grp * FR_GM : FR_GM;
+        tm = grp * FR_GM + in % gm;
+        tn = in / gm;
+    }
     const int m0 = tm * kBm, n0 = tn * kBn;
     const int nsb_all = g.K >> 8, ks_all = g.K >> 6;
     const int sb_beg = part * nsb_all / ksplit, sb_end = (part + 1) * nsb_all / ksplit;
@@ -225,25 +233,19 @@ gemm_q4k_fr(FrArgs g) {
 
     FrPlan d;
     {
-        int T = tm * kTm + (wave & 3);                         // token tile this wave copies
+        int T = tm * kTm + wave;                               // token tile this wave copies
         T = T < g.tiles_pad ? T : g.tiles_pad - 1;
         const int nt = g.N - n0 < kBn ? g.N - n0 : kBn;
-        d.rs_b = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+        d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+        d.rs_hi = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
+        d.rs_lo = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
         d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
-        if (wave < 4) {
-            d.rs_a = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
-            int hrow = wave * 64 + lane;
-            hrow = hrow < nt ? hrow : nt - 1;
-            d.off_b[0] = d.off_b[1] = (uint32_t)((size_t)hrow * g.rb);
-        } else {
-            d.rs_a = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
-#pragma unroll
-            for (int r = 0; r < 2; r++) {
-                int row = (2 * (wave - 4) + r) * 32 + (lane & 31);
-                row = row < nt ? row : nt - 1;
-                d.off_b[r] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
-            }
-        }
+        int row = wave * 32 + (lane & 31);
+        row = row < nt ? row : nt - 1;
+        d.code_off = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
+        int hrow = (wave & 1) * 64 + lane;
+        hrow = hrow < nt ? hrow : nt - 1;
+        d.hdr_off = (uint32_t)((size_t)hrow * g.rb);
     }
     auto stage = [&](int i) { return smem + i * kStage; };
     auto sbuf = [&](int i) { return smem + NS * kStage + i * kSbuf; };
@@ -271,7 +273,7 @@ gemm_q4k_fr(FrArgs g) {
     for (int i = 0; i < NS - 1; i++)
         if (kt0 + i < nk)
 #pragma unroll
-            for (int p = 0; p < 5; p++) fr_issue(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
+            for (int p = 0; p < 9; p++) fr_issue(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
 
     for (int sb = sb_beg; sb < sb_end; sb++) {
         const uint32_t sbo = (uint32_t)((sb & 1) * kSbuf);
@@ -280,7 +282,7 @@ gemm_q4k_fr(FrArgs g) {
             const int kt = 4 * sb + jb;
             int later = 0;                       // copies of steps kt+1 .. kt+NS-2 (may stay in flight)
 #pragma unroll
-            for (int i = 1; i < NS - 1; i++) later += fr_count(kt + i, nk);
+            for (int i = 1; i < NS - 1; i++) later += fr_count(kt + i, nk, wave);
             stamp(-1);
 #ifndef FR_NO_WAIT
             wait_dma(later);
@@ -411,7 +413,10 @@ gemm_q4k_fr(FrArgs g) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (pf) fr_issue(d, wave, kt + NS - 1, pst, psb, 4);
+            if (pf) {
+#pragma unroll
+                for (int i = kRt * kTmW; i < 9; i++) fr_issue(d, wave, kt + NS - 1, pst, psb, i);
+            }
             stamp(2);
 #ifdef FR_NO_EPI
             if (jb == 3 && sb == sb_end - 1) {
@@ -653,12 +658,15 @@ __global__ void __launch_bounds__(256) fr_zero_kernel(float* __restrict__ y, siz
 }
 
 // Tiles of the grid that run whole: when the tiles beyond the last full
-// round of one workgroup per CU are at most half a round, they are split in
+// round of two workgroups per CU are at most half a round, they are split in
 // K instead (their two halves fill that round).
 static int fr_nfull(int ntiles, int K) {
-    const int cus = device_cu_count();
-    const int rem = cus > 0 ? ntiles % cus : 0;
-    return (rem > 0 && 2 * rem <= cus && (K >> 8) >= 2) ? ntiles - rem : ntiles;
+#ifdef FR_NOSPLIT
+    return ntiles;
+#endif
+    const int slots = 2 * device_cu_count();                     // two workgroups per CU
+    const int rem = slots > 0 ? ntiles % slots : 0;
+    return (rem > 0 && 2 * rem <= slots && (K >> 8) >= 2) ? ntiles - rem : ntiles;
 }
 
 hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st,
@@ -673,7 +681,7 @@ hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K
         const size_t first = (size_t)(g.nfull / ntn) * kBm * N, n = (size_t)M * N - first;
         hipLaunchKernelGGL(fr_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y + first, n);
     }
-    constexpr int NS = 4;
+    constexpr int NS = 2;
     const size_t lds = (size_t)NS * kStage + 2 * kSbuf + kNw * 64 * 4;
     const long nblk = (long)g.nfull + 2L * (ntiles - g.nfull);
     if (stamp) hipLaunchKernelGGL((gemm_q4k_fr<NS, true>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);

@@ -104,6 +104,16 @@ size_t gemm_planes_bytes(int M, int K);
 // launch_planes_from_x / launch_gemm_planes / launch_gemm take this route
 // where gemm_fr_preferred says so.
 size_t gemm_fr_planes_bytes(int M, int K);
+// Int8-MFMA prefill GEMM from the quantized blocks (lp_gemm_i8.hip): its
+// scale planes take gemm_i8_planes_bytes of the planes area; launch_gemm
+// takes this route where gemm_i8_preferred says so.
+size_t gemm_i8_planes_bytes(int M, int K);
+bool gemm_i8_supported(uint32_t type, int M, int K);
+bool gemm_i8_preferred(uint32_t type, int M, int K, int N);
+// Prefill GEMM kernel family (0 by shape, 1 split-precision, 2 fragment-order, 3 int8).
+void set_gemm_kernel(int k);
+hipError_t launch_gemm_i8(const uint8_t* w, const ActView& A, void* planes, float* y, int M, int K, int N,
+                          hipStream_t st);
 bool gemm_fr_supported(uint32_t type, int M, int K);
 hipError_t launch_fr_planes(const float* x, const ActView& A, void* planes, int M, int K, hipStream_t st);
 // stamp: phase-cycle sums of an instrumented build (null: the product kernel)

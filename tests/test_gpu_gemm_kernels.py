@@ -1,0 +1,57 @@
+"""The three Q4_K prefill GEMM kernel families (lp_set_gemm_kernel 1-3:
+split-precision fp16/fp8 MFMA on row-major planes, the same arithmetic on
+MFMA-fragment-order planes, int8 MFMA with a per-block fp32 epilogue), each
+against the oracle's gemm_int (src/matmul_simd.cpp:226-283, 432-455) within
+1e-4 normwise, and each bit-identical between the one-call path
+(lp_gemm_dev: quantize and planes from fp32 x) and the two-step path
+(lp_quantize_act_dev + lp_gemm_q_dev: planes from the stored blocks).
+Shapes cover partial token and row tiles and the K-split tail round (tiles
+of two workgroups adding into a zeroed y)."""
+import numpy as np
+import pytest
+
+from hip_util import L, Q4_K, gemm_dev, normwise, stream, synth_weights, synth_x, to_dev, workspace
+from laplace_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(512, 300, 130), (4096, 512, 257), (2816, 200, 129), (1024, 4096, 384), (4096, 14336, 128)]
+
+
+@pytest.fixture
+def kernel_family():
+    def use(k):
+        _lib.check(L().lp_set_gemm_kernel(k), "lp_set_gemm_kernel")
+    yield use
+    _lib.check(L().lp_set_gemm_kernel(0), "lp_set_gemm_kernel")
+
+
+@pytest.mark.parametrize("kern", [1, 2, 3])
+@pytest.mark.parametrize("K,N,M", SHAPES, ids=lambda v: str(v))
+def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
+    import torch
+    print(f"gemm kernel {kern} K={K} N={N} M={M}", flush=True)
+    kernel_family(kern)
+    w = synth_weights(Q4_K, K, N, seed=K + N + kern)
+    x = synth_x(M, K, seed=M + 3, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    assert np.isfinite(y).all()
+    rng = np.random.default_rng(M + N)
+    toks = np.sort(rng.choice(M, min(M, 40), replace=False))
+    rows = np.sort(rng.choice(N, min(N, 64), replace=False))
+    rb = len(w) // N
+    wsub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    ref = orc.gemm_int(Q4_K, x[toks], wsub, len(rows))
+    assert normwise(y[np.ix_(toks, rows)], ref) <= 1e-4
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(M, K)
+    y2 = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    assert L().lp_quantize_act_dev(xd.data_ptr(), M, K, ws.data_ptr(), nb, stream()) == 0
+    assert L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), Q4_K, y2.data_ptr(), M, K, N, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(M, N).view(np.uint32), y.view(np.uint32))
+
+
+def test_gemm_kernel_rejects_unknown():
+    assert L().lp_set_gemm_kernel(4) == _lib.LP_EINVAL
+    assert L().lp_set_gemm_kernel(-1) == _lib.LP_EINVAL
