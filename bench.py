@@ -734,6 +734,35 @@ def gemm_sweep(g: Gpu):
     g.check(g.L.lp_set_gemm_kernel(0), "lp_set_gemm_kernel")
 
 
+def mfma_probe(g: Gpu, iters=20000):
+    """Sustained MFMA rate of the prefill GEMM's instruction mix on register
+    operands (no memory traffic), 256 workgroups x 8 waves: near-constant
+    operands against random ones of the GEMM's value ranges, as a fraction of
+    the nominal rate at the spec clock (fp16 2.5 PFLOP/s with the fp8 part at
+    twice that; int8 5.0 POPS)."""
+    torch = g.torch
+    grid = 256
+    out = torch.empty(grid * 512, dtype=torch.float32, device=g.dev)
+    for kind, name in ((0, "fp16 32x32x16 x16 + fp8 32x32x64 x4 per step"), (1, "int8 32x32x32 x8 per step")):
+        for rnd in (0, 1):
+            g.check(g.L.lp_mfma_probe_dev(kind, rnd, 100, grid, out.data_ptr(), g.stream()), "probe")
+            torch.cuda.synchronize()
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            g.check(g.L.lp_mfma_probe_dev(kind, rnd, iters, grid, out.data_ptr(), g.stream()), "probe")
+            ev1.record()
+            torch.cuda.synchronize()
+            us = ev0.elapsed_time(ev1) * 1e3
+            waves = grid * 8
+            # nominal cycles per iteration per SIMD (2 waves per SIMD)
+            clk = (16 * 32 + 4 * 64) if kind == 0 else 8 * 32
+            ideal_us = clk * iters * (waves / 1024) / 2.4e9 * 1e6
+            print(json.dumps({"mfma_probe": name, "random_operands": bool(rnd), "us": round(us, 1),
+                              "nominal_us_at_2.4GHz": round(ideal_us, 1),
+                              "frac_of_nominal": round(ideal_us / us, 4)}), flush=True)
+
+
 READ_SWEEP_BYTES = [33_030_144, 49_545_216, 66_060_288, 99_090_432, 132_120_576, 198_180_864,
                     264_241_152, 330_301_440, 415_236_096]
 
@@ -770,6 +799,8 @@ def main():
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the Q4_K prefill GEMM, every kernel family (lp_set_gemm_kernel 1-3) over "
                          "a grid of shapes, one JSON line each")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only the MFMA throughput probe (lp_mfma_probe_dev), near-constant vs random operands")
     ap.add_argument("--read-sweep", action="store_true",
                     help="only the streaming-read ceiling (lp_read_probe_dev) over read sizes "
                          "from the headline weight (33 MB) to the LM head (415 MB), one JSON line each")
@@ -792,6 +823,9 @@ def main():
         return
     if args.gemm_sweep:
         gemm_sweep(g)
+        return
+    if args.mfma_probe:
+        mfma_probe(g)
         return
     t, N, K, M = Q4_K, 14336, 4096, 1
     r = measure_gemv(g, t, N, K, M, args.steps, args.warmup, read_ceiling=True)

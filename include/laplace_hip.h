@@ -253,6 +253,15 @@ const char* lp_gemm_route(uint32_t type, int M, int K, int N, const void* w);
 int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int unroll, uint32_t* sink,
                       void* stream);
 
+/* Measurement hook, no reference counterpart: `grid` workgroups of 8 waves
+ * issue `iters` times the MFMA sequence of one 64-element K step of the
+ * prefill GEMM (kind 0: 16 fp16 32x32x16 + 4 fp8 32x32x64 products on a 2 x 2
+ * tile set; kind 1: 8 int8 32x32x32 products) on register operands, either
+ * near-constant (random_operands = 0) or random values of the GEMM's ranges;
+ * `out` takes grid * 512 floats. Its time against the nominal rate is how
+ * much of the MFMA peak the part sustains on such data. */
+int lp_mfma_probe_dev(int kind, int random_operands, int iters, int grid, float* out, void* stream);
+
 /* Text of the last error on this thread ("" if none). */
 const char* lp_last_error(void);
 /* 1 if the current device is usable (gfx950), 0 otherwise. */

@@ -41,6 +41,7 @@ SIGNATURES = {
     "lp_gemm_q_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
     "lp_gemm_route": (C.c_char_p, [_u32, _i, _i, _i, _vp]),
     "lp_set_gemm_kernel": (_i, [_i]),
+    "lp_mfma_probe_dev": (_i, [_i, _i, _i, _i, _vp, _vp]),
     "lp_gemm_dev_noalloc": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
     "lp_block_sums_dev": (_i, [_vp, _vp, _u32, _vp, _i, _i, _i, _vp]),
     "lp_moe_grouped_dev": (_i, [_vp, _i, _vp, _vp, _u32, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),

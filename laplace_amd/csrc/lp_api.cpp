@@ -1161,6 +1161,15 @@ int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int un
     return LP_OK;
 }
 
+int lp_mfma_probe_dev(int kind, int random_operands, int iters, int grid, float* out, void* stream) {
+    if (!out || iters < 1 || grid < 1 || (kind != 0 && kind != 1)) {
+        set_err("bad probe arguments");
+        return LP_EINVAL;
+    }
+    LP_HIP(launch_mfma_probe(kind, random_operands, iters, grid, out, static_cast<hipStream_t>(stream)));
+    return LP_OK;
+}
+
 int lp_set_gemm_kernel(int kernel) {
     if (kernel < 0 || kernel > 3) {
         set_err("kernel %d: 0 (by shape), 1, 2 or 3", kernel);

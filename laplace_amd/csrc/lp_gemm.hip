@@ -1279,13 +1279,14 @@ bool gemm_i8_preferred(uint32_t type, int M, int K, int N) {
     return g_gemm_kernel == 3 && gemm_i8_supported(type, M, K) && N > 0;
 }
 
-// By shape: the fragment-order kernel where it measured faster by 5-11 %
-// (bench.py --gemm-sweep: N 8192 / 14336 at M 256..512), the split-precision
-// kernel elsewhere (equal within a few percent at M >= 1024, faster below 256
-// tokens, where the fragment-order planes' two passes over x cost more).
+// By shape: the fragment-order kernel at N >= 8192 rows from 256 tokens,
+// where it measured faster per step (bench.py --gemm-sweep: N 14336 M 2048
+// 491 vs 512 us, M 512 137 vs 154, N 8192 M 512 103 vs 119), the
+// split-precision kernel elsewhere (N 4096 M 2048 154 vs 161, M 512 68 vs 80;
+// below 256 tokens the fragment-order planes' two passes over x cost more).
 static bool fr_auto(int M, int K, int N) {
     (void)K;
-    return M >= 256 && M <= 768 && N >= 8192;
+    return M >= 256 && N >= 8192;
 }
 
 static bool gemm_fr_preferred(int M, int K, int N) {

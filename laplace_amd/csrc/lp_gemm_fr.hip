@@ -500,8 +500,15 @@ __global__ void __launch_bounds__(256) fr_rowexp_kernel(const float* __restrict_
         for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     } else if (m < M) {
         const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * K);
-        for (int i = lane; i < K / 4; i += 64) {
-            const float4 u = xr[i];
+        for (int i0 = lane; i0 < K / 4; i0 += 256) {
+            // four loads in flight per lane (K / 4 is a multiple of 8; lanes past
+            // the row's end take a zero)
+            float4 uu[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) uu[c] = i0 + 64 * c < K / 4 ? xr[i0 + 64 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+            const float4 u = uu[c];
             float amax = fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w)));
             uint32_t nan = (u.x != u.x) | (u.y != u.y) | (u.z != u.z) | (u.w != u.w);
 #pragma unroll
@@ -510,6 +517,7 @@ __global__ void __launch_bounds__(256) fr_rowexp_kernel(const float* __restrict_
                 nan |= __shfl_xor(nan, o, 8);
             }
             if (!nan) mx = fmaxf(mx, amax);
+            }
         }
 #pragma unroll
         for (int o = 8; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -541,6 +549,14 @@ __global__ void __launch_bounds__(512) fr_planes_kernel(const float* __restrict_
     const int ksl = lane >> 4;                    // K step within the super-block
     const int hin = (lane >> 3) & 1;              // elements 32..63 of the step (high nibbles)
     const int g = (lane >> 2) & 1, s = lane & 3;
+    // the wave's four token rows requested together
+    float4 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int m = T * 32 + wave * 4 + j;
+        xv[j] = (!ACT && m < M) ? *reinterpret_cast<const float4*>(x + (size_t)m * K + 256 * sb + 4 * lane)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int r = wave * 4 + j;               // token within the tile
@@ -557,9 +573,7 @@ __global__ void __launch_bounds__(512) fr_planes_kernel(const float* __restrict_
                 q.sum = Aq.sum[bi];
             }
         } else {
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (m < M) v = *reinterpret_cast<const float4*>(x + (size_t)m * K + 256 * sb + 4 * lane);
-            q = quant_group8(v);
+            q = quant_group8(xv[j]);
         }
         const float inv = 1.0f / escale[T * 32 + r];     // a power of two: exact
         const float ds = q.d * inv;
@@ -608,6 +622,92 @@ struct FrPlanes {
     uint8_t* sx;
     float* escale;
 };
+
+// MFMA throughput probe (measurement hook): per iteration a wave issues the
+// fragment-order GEMM's products of one 64-element step on a 2 x 2 tile
+// set (16 v_mfma_f32_32x32x16_f16 + 4 v_mfma_f32_32x32x64_f8f6f4, kind 0)
+// or 8 v_mfma_i32_32x32x32_i8 (kind 1), operands in registers: either
+// near-constant (mostly zero) or random bit patterns of the GEMM's value
+// ranges, which shows how much of the nominal MFMA rate the part sustains
+// on real data (clock and power).
+template <int KIND>
+__global__ void __launch_bounds__(512) mfma_probe_kernel(int rnd_ops, int iters, float* __restrict__ out) {
+    uint32_t x = (threadIdx.x + 1) * 2654435761u + blockIdx.x * 97u;
+    auto rnd = [&]() {
+        x ^= x << 13;
+        x ^= x >> 17;
+        x ^= x << 5;
+        return x;
+    };
+    const int lane = threadIdx.x & 63;
+    h8 A[4][2], B[4][2];
+    i8x32 L[2], V8[2];
+    for (int s = 0; s < 4; s++)
+        for (int t = 0; t < 2; t++)
+            for (int j = 0; j < 8; j++) {
+                A[s][t][j] = rnd_ops ? (_Float16)((int)(rnd() % 20001) - 10000) : (_Float16)(j == 0 ? lane * 0.001f : 0.0f);
+                B[s][t][j] = rnd_ops ? (_Float16)((rnd() % 64) * (rnd() % 16) * 0.25f) : (_Float16)(j == 1 ? 0.5f : 0.0f);
+            }
+    for (int t = 0; t < 2; t++)
+        for (int j = 0; j < 8; j++) {
+            L[t][j] = rnd_ops ? (int)(rnd() & 0x3f3f3f3fu) : 0;
+            V8[t][j] = rnd_ops ? (int)(rnd() & 0x5f5f5f5fu) : 0;
+        }
+    f16v acc[2][2];
+    typedef int i16v __attribute__((ext_vector_type(16)));
+    typedef int i4v __attribute__((ext_vector_type(4)));
+    i16v iacc[2][2];
+    for (int t = 0; t < 2; t++)
+        for (int r = 0; r < 2; r++)
+            for (int i = 0; i < 16; i++) {
+                acc[t][r][i] = 0.0f;
+                iacc[t][r][i] = 0;
+            }
+    for (int it = 0; it < iters; it++) {
+        if (KIND == 0) {
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int t = 0; t < 2; t++)
+                        acc[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s][t], B[s][r], acc[t][r], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+                    acc[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(L[t], V8[r], acc[t][r], 0, 0, 0, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const i4v a = {L[t][4 * h], L[t][4 * h + 1], L[t][4 * h + 2], L[t][4 * h + 3]};
+                        const i4v b = {V8[r][4 * h], V8[r][4 * h + 1], V8[r][4 * h + 2], V8[r][4 * h + 3]};
+                        iacc[t][r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, iacc[t][r], 0, 0, 0);
+                    }
+        }
+        asm volatile("" : "+v"(A[0][0]), "+v"(B[0][0]), "+v"(L[0]), "+v"(V8[0]));
+    }
+    float sm = 0.0f;
+    for (int t = 0; t < 2; t++)
+        for (int r = 0; r < 2; r++)
+            for (int i = 0; i < 16; i++) sm += acc[t][r][i] + (float)iacc[t][r][i];
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = sm;
+}
+
+}  // namespace
+
+hipError_t launch_mfma_probe(int kind, int rnd_ops, int iters, int grid, float* out, hipStream_t st) {
+    if (kind == 0) hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(grid), dim3(512), 0, st, rnd_ops, iters, out);
+    else if (kind == 1) hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(grid), dim3(512), 0, st, rnd_ops, iters, out);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+namespace {
 
 size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
 
