@@ -88,7 +88,6 @@ struct FrArgs {
     int nfull;          // tiles [0, nfull) run whole; each later tile is two workgroups,
                         // one per half of K, adding into a zeroed y (two fp32 additions
                         // onto 0 give the same sum in either order)
-    unsigned long long* stamp;   // phase cycle sums (instrumented build only)
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
@@ -162,9 +161,6 @@ struct FrPlan {
 // through the CU's vector-memory path at ~64 B per clock and a wave's issue
 // waits for it, so the compute loop spreads them over its fp8 MFMAs.
 __device__ __forceinline__ void fr_issue(const FrPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
-#ifdef FR_NO_DMA
-    if (kt >= 3) return;
-#endif
     const uint32_t lane16 = (threadIdx.x & 63) * 16;
     const int sb = kt >> 2, jb = kt & 3;
     if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
@@ -180,23 +176,9 @@ __device__ __forceinline__ int fr_count(int k, int nk, int wave) {
     return k < nk ? kDmaStep + ((k & 3) == 0 ? (wave < 2 ? 2 : 1) : 0) : 0;
 }
 
-// STAMP: an instrumented build that sums s_memtime cycles per phase of a K
-// step (copy wait + barrier, -, products, super-block epilogue) into g.stamp
-// (plus whole-loop s_memtime and s_memrealtime, for the clock); each stamp
-// sits where no LDS read is in flight.
-template <int NS, bool STAMP = false>
+template <int NS>
 __global__ void __launch_bounds__(64 * kNw, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_q4k_fr(FrArgs g) {
-    unsigned long long ph[4] = {0, 0, 0, 0}, tprev = 0;
-    const unsigned long long c_beg = STAMP ? __builtin_amdgcn_s_memtime() : 0;
-    const unsigned long long r_beg = STAMP ? __builtin_amdgcn_s_memrealtime() : 0;
-    auto stamp = [&](int i) {
-        if (STAMP) {
-            const unsigned long long t = __builtin_amdgcn_s_memtime();
-            if (i >= 0) ph[i] += t - tprev;
-            tprev = t;
-        }
-    };
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -214,16 +196,14 @@ gemm_q4k_fr(FrArgs g) {
         part = (bid - g.nfull) & 1;
         ksplit = 2;
     }
-    // groups of FR_GM token tiles walk the weight tiles together (the
-    // workgroups in flight share both operands in L2)
-#ifndef FR_GM
-#define FR_GM 2
-#endif
+    // pairs of token tiles walk the weight tiles together (the workgroups in
+    // flight share both operands in L2)
+    constexpr int GM = 2;
     int tm, tn;
     {
-        const int per = FR_GM * g.ntn, grp = tile / per, in = tile % per;
-        const int gm = g.ntm - grp * FR_GM < FR_GM ? g.ntm - grp * FR_GM : FR_GM;
-        tm = grp * FR_GM + in % gm;
+        const int per = GM * g.ntn, grp = tile / per, in = tile % per;
+        const int gm = g.ntm - grp * GM < GM ? g.ntm - grp * GM : GM;
+        tm = grp * GM + in % gm;
         tn = in / gm;
     }
     const int m0 = tm * kBm, n0 = tn * kBn;
@@ -283,20 +263,13 @@ gemm_q4k_fr(FrArgs g) {
             int later = 0;                       // copies of steps kt+1 .. kt+NS-2 (may stay in flight)
 #pragma unroll
             for (int i = 1; i < NS - 1; i++) later += fr_count(kt + i, nk, wave);
-            stamp(-1);
-#ifndef FR_NO_WAIT
             wait_dma(later);
-#endif
             // after this barrier every wave has finished step kt-1, whose
             // stage is the one step kt+NS-1 is copied into
-#ifndef FR_NO_BAR
             __builtin_amdgcn_s_barrier();
-#endif
-            stamp(0);
             const bool pf = kt + NS - 1 < nk;
             uint8_t* const pst = stage((kt + NS - 1 - kt0) % NS);
             uint8_t* const psb = sbuf(((kt + NS - 1) >> 2) & 1);
-            stamp(1);
             const uint32_t so = (uint32_t)(((kt - kt0) % NS) * kStage);
 
             if (jb == 0) {
@@ -372,11 +345,7 @@ gemm_q4k_fr(FrArgs g) {
                 if (s < 3) {
 #pragma unroll
                     for (int r = 0; r < kRt; r++) {
-#ifdef FR_NO_DECODE
-                        Vn[r] = Vc[r];
-#else
                         Vn[r] = decode4(cw[r][s + 1], ml[r], al[r], mh[r], ah[r]);
-#endif
                     }
                 }
 #pragma unroll
@@ -417,12 +386,7 @@ gemm_q4k_fr(FrArgs g) {
 #pragma unroll
                 for (int i = kRt * kTmW; i < 9; i++) fr_issue(d, wave, kt + NS - 1, pst, psb, i);
             }
-            stamp(2);
-#ifdef FR_NO_EPI
-            if (jb == 3 && sb == sb_end - 1) {
-#else
             if (jb == 3) {
-#endif
                 // min term: sum_b m_b * (xs_hi + xs_lo)_b as one K = 16 product
                 // (lanes 0-31: k = blocks 0..7 on the hi plane, 32-63: the same
                 // blocks on the residual plane; B = the exact m in both halves)
@@ -447,15 +411,9 @@ gemm_q4k_fr(FrArgs g) {
                         }
                     }
             }
-            stamp(3);
         }
     }
 
-    if (STAMP && lane == 0) {
-        for (int i = 0; i < 4; i++) atomicAdd(&g.stamp[i], ph[i]);
-        atomicAdd(&g.stamp[4], __builtin_amdgcn_s_memtime() - c_beg);
-        atomicAdd(&g.stamp[5], __builtin_amdgcn_s_memrealtime() - r_beg);
-    }
     // D[token][row] -> y[token * N + row] * 2^E_token; the wave's 64 row
     // scales go through a wave-private LDS slot (one load wait, not one per output)
     const int mw = m0 + th * 32 * kTmW;
@@ -761,21 +719,17 @@ __global__ void __launch_bounds__(256) fr_zero_kernel(float* __restrict__ y, siz
 // round of two workgroups per CU are at most half a round, they are split in
 // K instead (their two halves fill that round).
 static int fr_nfull(int ntiles, int K) {
-#ifdef FR_NOSPLIT
-    return ntiles;
-#endif
     const int slots = 2 * device_cu_count();                     // two workgroups per CU
     const int rem = slots > 0 ? ntiles % slots : 0;
     return (rem > 0 && 2 * rem <= slots && (K >> 8) >= 2) ? ntiles - rem : ntiles;
 }
 
-hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st,
-                          unsigned long long* stamp) {
+hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
     const FrPlanes P = carve_fr(planes, M, K);
     const int ntm = (M + kBm - 1) / kBm, ntn = (N + kBn - 1) / kBn, ntiles = ntm * ntn;
     FrArgs g{P.hi, P.lo, P.sx, P.escale, w, row_bytes(T_Q4_K, K), y, M, N, K, ntm, ntn, (M + 31) / 32,
-             fr_nfull(ntiles, K), stamp};
+             fr_nfull(ntiles, K)};
     if (g.nfull < ntiles) {
         // rows of the split tiles (and of whole tiles sharing those rows: they overwrite)
         const size_t first = (size_t)(g.nfull / ntn) * kBm * N, n = (size_t)M * N - first;
@@ -784,8 +738,7 @@ hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K
     constexpr int NS = 2;
     const size_t lds = (size_t)NS * kStage + 2 * kSbuf + kNw * 64 * 4;
     const long nblk = (long)g.nfull + 2L * (ntiles - g.nfull);
-    if (stamp) hipLaunchKernelGGL((gemm_q4k_fr<NS, true>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
-    else hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
+    hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
     return hipGetLastError();
 }
 
