@@ -32,6 +32,14 @@ int moe_topk_max_experts();
 // norms of x [T, H]; when Aq.qs is set, ein is also quantized into Aq (H % 32 == 0)
 hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
                             float eps, float* rin, float* ein, const ActView& Aq, hipStream_t st);
+// Both norms, the expert input's quantization and the F32 router products in
+// one launch for 1..4 tokens (moe_norm_router_supported); logits equal to
+// launch_moe_norms + the F32 router GEMV bit for bit.
+bool moe_norm_router_supported(int T, int H, uint32_t router_type, const void* router, const void* gate_scale,
+                               const void* pre_norm);
+hipError_t launch_moe_norm_router(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
+                                  float eps, const float* router, int n_exp, float* logits, float* ein,
+                                  const ActView& Aq, hipStream_t st);
 // Top-k and the route table in one launch (up to 16 tokens; preferred for
 // T <= 4: moe_topk_route_supported).
 bool moe_topk_route_supported(int T);

@@ -77,6 +77,95 @@ moe_norms_kernel(const float* __restrict__ x, int H, const float* __restrict__ g
     }
 }
 
+// A few tokens (MR <= 4) with an F32 router: the two norms and the router
+// products in one launch. Every workgroup recomputes each token's inv from x
+// (the same sum in the same order as moe_norms_kernel), quantizes its slice
+// of the expert input (32-element blocks, 8 threads each), and its waves take
+// router rows as gemv_dense_kernel<F32, MR> does (lane: 8 consecutive
+// elements of each 512-element slab, 8 slabs in flight, then the wave sum),
+// with the router input r[i] = (x[i] * inv) * (gate_scale[i] * inv_sqrt_h)
+// formed on the fly: logits bit-identical to the two-kernel path.
+template <int MR>
+__global__ void __launch_bounds__(256)
+moe_norm_router_kernel(const float* __restrict__ x, int H, const float* __restrict__ gate_scale,
+                       const float* __restrict__ pre_norm, float inv_sqrt_h, float eps,
+                       const float* __restrict__ router, int n_exp, float* __restrict__ logits,
+                       float* __restrict__ ein, ActView Aq) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    float inv[MR];
+#pragma unroll
+    for (int t = 0; t < MR; t++) {
+        const float* xr = x + (size_t)t * H;
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < H; i += 256) ss += xr[i] * xr[i];
+        const float ms = block_sum256(ss, red);
+        inv[t] = 1.0f / sqrtf(ms / (float)H + eps);
+    }
+    // this workgroup's share of the expert input (whole 32-element blocks)
+    const int h4 = H >> 2;
+    for (int i4 = blockIdx.x * 256 + threadIdx.x; i4 < MR * h4; i4 += gridDim.x * 256) {
+        const int t = i4 / h4, c4 = i4 - t * h4;
+        float it = inv[0];
+#pragma unroll
+        for (int u = 1; u < MR; u++) it = t == u ? inv[u] : it;
+        const float4 xv = reinterpret_cast<const float4*>(x + (size_t)t * H)[c4];
+        const float4 pn = reinterpret_cast<const float4*>(pre_norm)[c4];
+        const float4 e = make_float4((xv.x * it) * pn.x, (xv.y * it) * pn.y, (xv.z * it) * pn.z,
+                                     (xv.w * it) * pn.w);
+        reinterpret_cast<float4*>(ein + (size_t)t * H)[c4] = e;
+        store_q8_block(Aq, t, H, c4, e);
+    }
+    // router rows, one per wave
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * 256 + threadIdx.x) >> 6;
+    if (row >= n_exp) return;
+    const float* wr = router + (size_t)row * H;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+    constexpr int U = 8;
+    for (int e0 = 8 * lane; e0 < H; e0 += U * 512) {
+        float wv[U][8];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (e0 + 512 * u < H) {
+                const float4 a = reinterpret_cast<const float4*>(wr + e0 + 512 * u)[0];
+                const float4 b = reinterpret_cast<const float4*>(wr + e0 + 512 * u)[1];
+                wv[u][0] = a.x; wv[u][1] = a.y; wv[u][2] = a.z; wv[u][3] = a.w;
+                wv[u][4] = b.x; wv[u][5] = b.y; wv[u][6] = b.z; wv[u][7] = b.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int e = e0 + 512 * u;
+            if (e < H) {
+                const float4 g0 = reinterpret_cast<const float4*>(gate_scale + e)[0];
+                const float4 g1 = reinterpret_cast<const float4*>(gate_scale + e)[1];
+                const float gs[8] = {g0.x * inv_sqrt_h, g0.y * inv_sqrt_h, g0.z * inv_sqrt_h, g0.w * inv_sqrt_h,
+                                     g1.x * inv_sqrt_h, g1.y * inv_sqrt_h, g1.z * inv_sqrt_h, g1.w * inv_sqrt_h};
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const float4 a = reinterpret_cast<const float4*>(x + (size_t)m * H + e)[0];
+                    const float4 b = reinterpret_cast<const float4*>(x + (size_t)m * H + e)[1];
+                    const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                    float t = acc[m];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) t = fmaf((xv[j] * inv[m]) * gs[j], wv[u][j], t);
+                    acc[m] = t;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float s2 = acc[m];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off, 64);
+        if (lane == 0) logits[(size_t)m * n_exp + row] = s2;
+    }
+}
+
 // Wave-wide reductions with DPP lane moves (the pattern of group_sum: the
 // result lands in lane 63, read back as a wave-uniform value). A lane with no
 // source in a step keeps its own value, the identity of max / arg-max.
@@ -296,6 +385,31 @@ hipError_t launch_moe_norms(const float* x, int T, int H, const float* gate_scal
     const float inv_sqrt_h = 1.0f / sqrtf((float)H);
     hipLaunchKernelGGL(moe_norms_kernel, dim3(T), dim3(256), 0, st, x, H, gate_scale, pre_norm, inv_sqrt_h, eps,
                        rin, ein, Aq);
+    return hipGetLastError();
+}
+
+bool moe_norm_router_supported(int T, int H, uint32_t router_type, const void* router, const void* gate_scale,
+                               const void* pre_norm) {
+    return T >= 1 && T <= 4 && router_type == T_F32 && H % 32 == 0 &&
+           reinterpret_cast<uintptr_t>(router) % 16 == 0 && reinterpret_cast<uintptr_t>(gate_scale) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(pre_norm) % 16 == 0;
+}
+
+hipError_t launch_moe_norm_router(const float* x, int T, int H, const float* gate_scale, const float* pre_norm,
+                                  float eps, const float* router, int n_exp, float* logits, float* ein,
+                                  const ActView& Aq, hipStream_t st) {
+    if (T < 1 || T > 4 || H % 32 != 0 || !Aq.qs) return hipErrorInvalidValue;
+    const float inv_sqrt_h = 1.0f / sqrtf((float)H);
+    const dim3 grid((unsigned)((n_exp + 3) / 4));
+#define LP_NR(MRV) hipLaunchKernelGGL(moe_norm_router_kernel<MRV>, grid, dim3(256), 0, st, x, H, gate_scale, pre_norm, \
+                                      inv_sqrt_h, eps, router, n_exp, logits, ein, Aq)
+    switch (T) {
+        case 1: LP_NR(1); break;
+        case 2: LP_NR(2); break;
+        case 3: LP_NR(3); break;
+        default: LP_NR(4); break;
+    }
+#undef LP_NR
     return hipGetLastError();
 }
 
