@@ -718,15 +718,18 @@ def load_traffic(name):
 
 GEMM_SWEEP = [(n, 4096, m) for n in (2048, 4096, 8192, 14336) for m in (128, 256, 512, 1024, 2048)] + \
     [(4096, 14336, 512), (4096, 14336, 2048)]
-GEMM_KERNELS = {1: "split-precision, row-major planes", 2: "fragment-order planes", 3: "int8 MFMA"}
+GEMM_KERNELS = {1: "split-precision, row-major planes", 2: "fragment-order planes", 3: "int8 MFMA",
+                4: "fragment-order planes, 128-token wave tiles"}
 
 
-def gemm_sweep(g: Gpu):
+def gemm_sweep(g: Gpu, kernels=None, shapes=None):
     """Step time of the Q4_K prefill GEMM (quantize/planes + product) per
     kernel family over GEMM_SWEEP shapes (N, K, M); the routing table of
     lp_gemm comes from these lines."""
-    for (n, k, m) in GEMM_SWEEP:
+    for (n, k, m) in (shapes or GEMM_SWEEP):
         for kern, name in GEMM_KERNELS.items():
+            if kernels and kern not in kernels:
+                continue
             g.check(g.L.lp_set_gemm_kernel(kern), "lp_set_gemm_kernel")
             r = measure_gemm(g, n, k, m, reps=10)
             print(json.dumps({"kernel": kern, "family": name, **r}), flush=True)
@@ -799,6 +802,8 @@ def main():
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the Q4_K prefill GEMM, every kernel family (lp_set_gemm_kernel 1-3) over "
                          "a grid of shapes, one JSON line each")
+    ap.add_argument("--sweep-kernels", default="", help="with --gemm-sweep: comma-separated families")
+    ap.add_argument("--sweep-shapes", default="", help="with --gemm-sweep: NxKxM,... instead of the table")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only the MFMA throughput probe (lp_mfma_probe_dev), near-constant vs random operands")
     ap.add_argument("--read-sweep", action="store_true",
@@ -822,7 +827,9 @@ def main():
         read_sweep(g)
         return
     if args.gemm_sweep:
-        gemm_sweep(g)
+        kern = [int(v) for v in args.sweep_kernels.split(",") if v]
+        shp = [tuple(int(v) for v in t.split("x")) for t in args.sweep_shapes.split(",") if t]
+        gemm_sweep(g, kern or None, shp or None)
         return
     if args.mfma_probe:
         mfma_probe(g)

@@ -36,7 +36,7 @@ CFLAGS = [
 
 # Per-source additions. lp_rq.hip: MFMA results in VGPRs (its int8 block sums
 # feed VALU at once; the AGPR form costs a v_accvgpr_read per value).
-SRC_FLAGS = {"lp_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_q6rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SRC_FLAGS = {"lp_gemm_fr.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "lp_q6rq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> str:

@@ -1292,7 +1292,7 @@ static bool fr_auto(int M, int K, int N) {
 static bool gemm_fr_preferred(int M, int K, int N) {
     if (!gemm_fr_supported(T_Q4_K, M, K) || N < 128) return false;
     if (g_gemm_kernel == 1 || g_gemm_kernel == 3) return false;
-    return g_gemm_kernel == 2 || fr_auto(M, K, N);
+    return g_gemm_kernel == 2 || g_gemm_kernel == 4 || fr_auto(M, K, N);
 }
 
 bool gemm_supported(uint32_t type, int M, int K) {
@@ -1352,7 +1352,8 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
                               hipStream_t st) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (gemm_fr_preferred(M, K, N)) return launch_fr_gemm(w, planes, y, M, K, N, st);
+    if (gemm_fr_preferred(M, K, N))
+        return g_gemm_kernel == 4 ? launch_wt_gemm(w, planes, y, M, K, N, st) : launch_fr_gemm(w, planes, y, M, K, N, st);
     const Planes P = carve_planes(planes, M, K);
     if (M <= kMfMaxM) {
         MfArgs a{w, (long)row_bytes(type, K), N, K, M, P, y};

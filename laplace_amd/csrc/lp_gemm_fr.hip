@@ -47,6 +47,7 @@
 // super-block. NS stages in flight, one barrier per K step, one workgroup per
 // CU (LDS NS x 32 KiB + 16 KiB).
 #include <hip/hip_runtime.h>
+#include <cstdlib>
 
 #include "lp_chunks.h"
 #include "lp_internal.h"
@@ -739,6 +740,466 @@ hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K
     const long nblk = (long)g.nfull + 2L * (ntiles - g.nfull);
     hipLaunchKernelGGL((gemm_q4k_fr<NS>), dim3((unsigned)nblk), dim3(64 * kNw), lds, st, g);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Wide-token prefill GEMM (gemm_q4k_wt) on the same fragment-order planes.
+//
+// Same arithmetic as gemm_q4k_fr; what changes is the work split. Each wave
+// owns 128 tokens and 64 weight rows (4 x 2 MFMA tiles of 32 x 32), so every
+// weight element is decoded once per 128 tokens, half the decode VALU per
+// MFMA of a 64-token wave tile. A workgroup is 4 * TH waves (TH token halves
+// of 128 tokens, 4 row quarters of 64 rows): a tile of 128 * TH tokens x 256
+// rows. TH = 2 puts two waves on each SIMD, which is what lets one wave's
+// VALU work (decode, e4m3 conversion, super-block fold) issue under the other
+// wave's MFMAs; with one wave per SIMD a wave's own VALU work between its
+// MFMAs leaves the matrix pipe idle.
+//
+// The super-block scale is applied by keeping each row's accumulators in
+// units u = d_sb * 2^-7 of the current super-block: the MFMAs add the
+// unscaled main products straight into the accumulators, and at each
+// super-block boundary acc = acc * (u_old / u_new) - (dmin_old / u_new) *
+// min_old (one accumulator set instead of two). A super-block whose d is
+// zero keeps the old unit and decodes its V as zero (its main term is zero);
+// a non-finite d makes the row NaN.
+//
+// Per K step wave w copies token tile w's hi (4 x 1 KiB) and lo (2 x 1 KiB)
+// pieces and code piece w (32 rows x 32 B; with TH = 1 also piece w + 4), and
+// per super-block token tile w's min-term piece and (waves 0-3) the headers
+// of 64 rows.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int TH>
+struct WtCfg {
+    static constexpr int Tm = 4 * TH;                 // 32-token tiles per workgroup
+    static constexpr int Nw = 4 * TH;                 // waves
+    static constexpr int Bm = 32 * Tm, Bn = 256;
+    static constexpr int Hi = Tm * 4096, Lo = Tm * 2048, Codes = 8 * 1024;
+    static constexpr int Stage = Hi + Lo + Codes;
+    static constexpr int Hdr = Bn * 16, Sx = Tm * 1024;
+    static constexpr int Sbuf = Hdr + Sx;
+    static constexpr int NS = TH == 1 ? 3 : 2;
+    static constexpr int CodesPerWave = 8 / Nw;      // 2 or 1
+    static constexpr int DmaStep = 6 + CodesPerWave;
+    static constexpr size_t Lds = (size_t)NS * Stage + 2 * Sbuf + Nw * 128 * 4;
+    static_assert(Stage / 1024 == Nw * DmaStep, "copies split evenly");
+};
+
+struct WtArgs {
+    const uint8_t* hi;
+    const uint8_t* lo;
+    const uint8_t* sx;
+    const float* escale;
+    const uint8_t* w;
+    size_t rb;
+    float* y;
+    int M, N, K;
+    int ntm, ntn;
+    int tiles_pad;
+    int nfull;          // tiles [0, nfull) run whole; each later one is two
+                        // workgroups over the halves of K adding into a zeroed y
+};
+
+struct WtPlan {
+    Rsrc rs_hi, rs_lo, rs_w, rs_sx;
+    uint32_t code_off[2], hdr_off;
+};
+
+template <int TH>
+__device__ __forceinline__ void wt_issue(const WtPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
+    using C = WtCfg<TH>;
+    const uint32_t lane16 = (threadIdx.x & 63) * 16;
+    const int sb = kt >> 2, jb = kt & 3;
+    if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
+    else if (i < 6) dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (i - 4) * 1024), st + C::Hi + wave * 2048 + (i - 4) * 1024);
+    else if (i < 6 + C::CodesPerWave)
+        dma16(d.rs_w, d.code_off[i - 6], (uint32_t)(sb * 144 + 32 * jb),
+              st + C::Hi + C::Lo + (wave + (i - 6) * C::Nw) * 1024);
+    else if (jb == 0) {
+        if (i == C::DmaStep) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + C::Hdr + wave * 1024);
+        else if (wave < 4) dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
+    }
+}
+
+template <int TH>
+__device__ __forceinline__ int wt_count(int k, int nk, int wave) {
+    using C = WtCfg<TH>;
+    return k < nk ? C::DmaStep + ((k & 3) == 0 ? (wave < 4 ? 2 : 1) : 0) : 0;
+}
+
+template <int TH, int ABL>
+__global__ void __launch_bounds__(256 * TH, 1) __attribute__((amdgpu_waves_per_eu(TH, TH)))
+gemm_q4k_wt(WtArgs g) {
+    using C = WtCfg<TH>;
+    constexpr int NS = C::NS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int th = wave >> 2, rq = wave & 3;          // token half, row quarter
+    const int bid = blockIdx.x;
+    int tile, part = 0, ksplit = 1;
+    if (bid < g.nfull) {
+        tile = (g.nfull & 7) == 0 ? (bid & 7) * (g.nfull >> 3) + (bid >> 3) : bid;
+    } else {
+        tile = g.nfull + ((bid - g.nfull) >> 1);
+        part = (bid - g.nfull) & 1;
+        ksplit = 2;
+    }
+    constexpr int GM = 2;
+    int tm, tn;
+    {
+        const int per = GM * g.ntn, grp = tile / per, in = tile % per;
+        const int gm = g.ntm - grp * GM < GM ? g.ntm - grp * GM : GM;
+        tm = grp * GM + in % gm;
+        tn = in / gm;
+    }
+    const int m0 = tm * C::Bm, n0 = tn * C::Bn;
+    const int nsb_all = g.K >> 8, ks_all = g.K >> 6;
+    const int sb_beg = part * nsb_all / ksplit, sb_end = (part + 1) * nsb_all / ksplit;
+    const int kt0 = 4 * sb_beg, nk = 4 * sb_end;
+
+    WtPlan d;
+    {
+        int T = tm * C::Tm + wave;
+        T = T < g.tiles_pad ? T : g.tiles_pad - 1;
+        const int nt = g.N - n0 < C::Bn ? g.N - n0 : C::Bn;
+        d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
+        d.rs_hi = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
+        d.rs_lo = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
+        d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            int row = (wave + c * C::Nw) * 32 + (lane & 31);      // code piece wave + c * Nw
+            row = row < nt ? row : nt - 1;
+            d.code_off[c] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
+        }
+        int hrow = (wave & 3) * 64 + lane;
+        hrow = hrow < nt ? hrow : nt - 1;
+        d.hdr_off = (uint32_t)((size_t)hrow * g.rb);
+    }
+    auto stage = [&](int i) { return smem + i * C::Stage; };
+    auto sbuf = [&](int i) { return smem + NS * C::Stage + i * C::Sbuf; };
+
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t l16 = lds0 + lane * 16 + th * (4 * 4096);                 // this wave's 4 token tiles
+    const uint32_t l16lo = lds0 + lane * 16 + C::Hi + th * (4 * 2048);
+    const uint32_t l16c = lds0 + lane * 16 + C::Hi + C::Lo + rq * (2 * 1024);   // code pieces 2rq, 2rq+1
+    const uint32_t hdr_a = lds0 + NS * C::Stage + (rq * 64 + (lane & 31)) * 16;  // + r * 512
+    const uint32_t sx_a = lds0 + NS * C::Stage + C::Hdr + th * (4 * 1024) + lane * 16;
+
+    f16v acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.0f;
+
+    uint32_t hy[2], hz[2], hw[2];
+    float u[2], dmn[2], zs[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        u[r] = 1.0f;
+        dmn[r] = 0.0f;
+        zs[r] = 1.0f;
+        hy[r] = hz[r] = hw[r] = 0;
+    }
+
+    // min term of the previous super-block (its SX piece in buffer `sbo`, its
+    // m values in hz/hw) folded into the accumulators: acc = acc * rho - kap * min
+    auto fold = [&](uint32_t sbo, const float (&rho)[2], const float (&kap)[2]) {
+        h8 S[4];
+        rd128h<0>(S[0], sx_a + sbo);
+        rd128h<1024>(S[1], sx_a + sbo);
+        rd128h<2048>(S[2], sx_a + sbo);
+        rd128h<3072>(S[3], sx_a + sbo);
+        h8 mb[2];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) mb[r][j] = (_Float16)(float)q4k_m(hz[r], hw[r], j);
+        lgkm<0>(S);
+        // one tile's min product in registers at a time: each product's B
+        // operand is tied to the previous tile's folded accumulators, so the
+        // products cannot all be hoisted ahead of the folds
+        f16v prev = acc[0][0];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                h8 bm = mb[r];
+                asm volatile("" : "+v"(bm) : "v"(prev));
+                const f16v mm = __builtin_amdgcn_mfma_f32_32x32x16_f16(S[t], bm, f16v{}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[t][r][i] = fmaf(-kap[r], mm[i], acc[t][r][i] * rho[r]);
+                prev = acc[t][r];
+            }
+    };
+
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++)
+        if (kt0 + i < nk)
+#pragma unroll
+            for (int p = 0; p < C::DmaStep + 2; p++)
+                wt_issue<TH>(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
+
+    // residual (fp8) products of a step, run after the next step's barrier:
+    // their operands are in registers, so they fill the time the next
+    // step's first LDS reads take, and the next copies go out under them
+    // (zero before the first step: its residual call adds nothing)
+    u32x4 Lp[4][2];
+    i8x32 bvp[2];
+#pragma unroll
+    for (int t = 0; t < 4; t++) Lp[t][0] = Lp[t][1] = u32x4{0, 0, 0, 0};
+    bvp[0] = bvp[1] = i8x32{0, 0, 0, 0, 0, 0, 0, 0};
+    auto residual = [&](bool issue, int kt, uint8_t* pst, uint8_t* psb) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const i8x32 av = {(int)Lp[t][0].x, (int)Lp[t][0].y, (int)Lp[t][0].z, (int)Lp[t][0].w,
+                              (int)Lp[t][1].x, (int)Lp[t][1].y, (int)Lp[t][1].z, (int)Lp[t][1].w};
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                if (ABL != 2)
+                    acc[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bvp[r], acc[t][r], 0, 0, 0, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                const int ci = t * 2 + r;
+                if (issue && ci < C::DmaStep) wt_issue<TH>(d, wave, kt, pst, psb, ci);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (issue) {
+#pragma unroll
+            for (int i = C::DmaStep < 8 ? C::DmaStep : 8; i < C::DmaStep + 2; i++) wt_issue<TH>(d, wave, kt, pst, psb, i);
+        }
+    };
+
+    for (int sb = sb_beg; sb < sb_end; sb++) {
+        const uint32_t sbo = (uint32_t)((sb & 1) * C::Sbuf);
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+            const int kt = 4 * sb + jb;
+            int later = 0;
+#pragma unroll
+            for (int i = 1; i < NS - 1; i++) later += wt_count<TH>(kt + i, nk, wave);
+            if (ABL != 4 && ABL != 5) {
+                wait_dma(later);
+                __builtin_amdgcn_s_barrier();
+            }
+            const bool pf = ABL != 5 && kt + NS - 1 < nk;
+            uint8_t* const pst = stage((kt + NS - 1 - kt0) % NS);
+            uint8_t* const psb = sbuf(((kt + NS - 1) >> 2) & 1);
+            const uint32_t so = (uint32_t)(((kt - kt0) % NS) * C::Stage);
+            const uint32_t b = l16 + so;
+
+            // this step's first reads, then the previous step's residual
+            // products (and this step's copies) while they land
+            u32x4 h[2];
+            if (jb == 0) {
+                rd128<0>(h[0], hdr_a + sbo);
+                rd128<512>(h[1], hdr_a + sbo);
+            }
+            u32x4 cw[2];
+            h8 A[2][4];
+            rd128<0>(cw[0], l16c + so);
+            rd128<1024>(cw[1], l16c + so);
+            rd128h<0>(A[0][0], b);
+            rd128h<4096>(A[0][1], b);
+            rd128h<8192>(A[0][2], b);
+            rd128h<12288>(A[0][3], b);
+            residual(pf, kt + NS - 1, pst, psb);
+
+            if (jb == 0) {
+                if (jb == 0) lgkm<6>(h);
+                float rho[2], kap[2];
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const float dn = fp16_bits_to_f32(h[r].x);
+                    const float un = dn * 0.0078125f;
+                    const bool ok = un != 0.0f && __builtin_isfinite(un);
+                    const float unew = ok ? un : u[r];
+                    rho[r] = __builtin_isfinite(dn) ? u[r] / unew : __builtin_nanf("");
+                    kap[r] = dmn[r] / unew;
+                    u[r] = unew;
+                    zs[r] = ok ? 1.0f : 0.0f;
+                }
+                if (ABL != 3 && sb > sb_beg) fold(sbo ^ (uint32_t)C::Sbuf, rho, kap);
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    dmn[r] = fp16_bits_to_f32(h[r].x >> 16);
+                    hy[r] = h[r].y;
+                    hz[r] = h[r].z;
+                    hw[r] = h[r].w;
+                }
+            }
+            h2 ml[2], al[2], mh[2], ah[2];
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const float sl = (float)q4k_sc(hy[r], hw[r], 2 * jb) * (0.25f * zs[r]);
+                const float sh = (float)q4k_sc(hy[r], hw[r], 2 * jb + 1) * (0.25f * 0.0625f * zs[r]);
+                const _Float16 a = (_Float16)sl, b = (_Float16)(-1024.0f * sl);
+                const _Float16 c = (_Float16)sh, e = (_Float16)(-1024.0f * sh);
+                ml[r] = h2{a, a};
+                al[r] = h2{b, b};
+                mh[r] = h2{c, c};
+                ah[r] = h2{e, e};
+            }
+            uint32_t v8[2][8];
+            h8 Vc[2];
+            lgkm<4>(cw);
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+                Vc[r] = ABL == 1 ? __builtin_bit_cast(h8, cw[r]) : decode4(cw[r][0], ml[r], al[r], mh[r], ah[r]);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                h8 (&As)[4] = A[s & 1];
+                h8 (&An)[4] = A[(s + 1) & 1];
+                lgkm<0>(As);
+                if (s == 0) {
+                    rd128h<1024>(An[0], b);
+                    rd128h<1024 + 4096>(An[1], b);
+                    rd128h<1024 + 8192>(An[2], b);
+                    rd128h<1024 + 12288>(An[3], b);
+                } else if (s == 1) {
+                    rd128h<2048>(An[0], b);
+                    rd128h<2048 + 4096>(An[1], b);
+                    rd128h<2048 + 8192>(An[2], b);
+                    rd128h<2048 + 12288>(An[3], b);
+                } else if (s == 2) {
+                    rd128h<3072>(An[0], b);
+                    rd128h<3072 + 4096>(An[1], b);
+                    rd128h<3072 + 8192>(An[2], b);
+                    rd128h<3072 + 12288>(An[3], b);
+                } else {
+                    // this step's lo pieces, for its residual products after
+                    // the next barrier
+                    const uint32_t bl = l16lo + so;
+                    rd128<0>(Lp[0][0], bl);
+                    rd128<1024>(Lp[0][1], bl);
+                    rd128<2048>(Lp[1][0], bl);
+                    rd128<3072>(Lp[1][1], bl);
+                    rd128<4096>(Lp[2][0], bl);
+                    rd128<5120>(Lp[2][1], bl);
+                    rd128<6144>(Lp[3][0], bl);
+                    rd128<7168>(Lp[3][1], bl);
+                }
+                // the next fragments' reads go out before this sub-step's
+                // MFMAs (else the scheduler sinks them below the MFMAs that read
+                // the registers they would reuse, and their latency is exposed)
+                __builtin_amdgcn_sched_barrier(0);
+                h8 Vn[2];
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        acc[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(As[t], Vc[r], acc[t][r], 0, 0, 0);
+                if (s < 3) {
+#pragma unroll
+                    for (int r = 0; r < 2; r++)
+                        Vn[r] = ABL == 1 ? Vc[r] : decode4(cw[r][s + 1], ml[r], al[r], mh[r], ah[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const u32x4 q = __builtin_bit_cast(u32x4, Vc[r]);
+                    v8[r][2 * s] = ABL == 1 ? q.x : e4m3x4(q.x, q.y);
+                    v8[r][2 * s + 1] = ABL == 1 ? q.z : e4m3x4(q.z, q.w);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (s < 3) {
+#pragma unroll
+                    for (int r = 0; r < 2; r++) Vc[r] = Vn[r];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+                bvp[r] = i8x32{(int)v8[r][0], (int)v8[r][1], (int)v8[r][2], (int)v8[r][3],
+                               (int)v8[r][4], (int)v8[r][5], (int)v8[r][6], (int)v8[r][7]};
+            // the lo pieces must be in registers before the next barrier
+            // lets their stage be overwritten
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int t = 0; t < 4; t++) asm volatile("" : "+v"(Lp[t][0]), "+v"(Lp[t][1]));
+        }
+    }
+    residual(false, 0, nullptr, nullptr);
+    // the last super-block's min term; the accumulators leave in units of 1
+    {
+        float rho[2], kap[2];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            rho[r] = u[r];
+            kap[r] = dmn[r];
+        }
+        fold((uint32_t)(((sb_end - 1) & 1) * C::Sbuf), rho, kap);
+    }
+
+    const int mw = m0 + th * 128;
+    float* esl = reinterpret_cast<float*>(smem + NS * C::Stage + 2 * C::Sbuf) + wave * 128;
+    esl[lane] = mw + lane < g.M ? g.escale[mw + lane] : 0.0f;
+    esl[64 + lane] = mw + 64 + lane < g.M ? g.escale[mw + 64 + lane] : 0.0f;
+    __builtin_amdgcn_wave_barrier();
+    const int gl = lane >> 5;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int n = n0 + rq * 64 + r * 32 + (lane & 31);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int ml = t * 32 + 8 * (i >> 2) + 4 * gl + (i & 3);
+                const int m = mw + ml;
+                if (m < g.M && n < g.N) {
+                    const float val = acc[t][r][i] * esl[ml];
+                    if (ksplit == 1) g.y[(size_t)m * g.N + n] = val;
+                    else atomicAdd(&g.y[(size_t)m * g.N + n], val);
+                }
+            }
+    }
+}
+
+template <int TH>
+hipError_t launch_wt(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st) {
+    using C = WtCfg<TH>;
+    const FrPlanes P = carve_fr(planes, M, K);
+    const int ntm = (M + C::Bm - 1) / C::Bm, ntn = (N + C::Bn - 1) / C::Bn, ntiles = ntm * ntn;
+    const int cus = device_cu_count(), nsb = K >> 8;
+    // one workgroup per CU: a last round that would leave at least half the
+    // CUs idle runs its tiles as two workgroups over the halves of K instead
+    // (two fp32 additions onto a zeroed y give the same sum in either order;
+    // more parts would make the result depend on their order)
+    const int rem = ntiles % cus;
+    const bool split = rem > 0 && 2 * rem <= cus && nsb >= 2;
+    const int nfull = split ? ntiles - rem : ntiles;
+    WtArgs g{P.hi, P.lo, P.sx, P.escale, w, row_bytes(T_Q4_K, K), y, M, N, K, ntm, ntn, (M + 31) / 32, nfull};
+    if (nfull < ntiles) {
+        // rows of the token-tile pairs holding split tiles (whole tiles there overwrite)
+        const size_t first = (size_t)(nfull / (2 * ntn)) * 2 * C::Bm * N;
+        if (first < (size_t)M * N) {
+            const size_t n = (size_t)M * N - first;
+            hipLaunchKernelGGL(fr_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y + first, n);
+        }
+    }
+    const long nblk = (long)nfull + 2L * (ntiles - nfull);
+    static const int abl = getenv("LP_WT_ABL") ? atoi(getenv("LP_WT_ABL")) : 0;
+    switch (abl) {
+#define LP_A(a) case a: hipLaunchKernelGGL((gemm_q4k_wt<TH, a>), dim3((unsigned)nblk), dim3(64 * C::Nw), C::Lds, st, g); break;
+        LP_A(0) LP_A(1) LP_A(2) LP_A(3) LP_A(4) LP_A(5)
+#undef LP_A
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    static const int th = getenv("LP_WT_TH") ? atoi(getenv("LP_WT_TH")) : 2;
+    return th == 1 ? launch_wt<1>(w, planes, y, M, K, N, st) : launch_wt<2>(w, planes, y, M, K, N, st);
 }
 
 }  // namespace lp

@@ -127,6 +127,7 @@ hipError_t launch_fr_planes(const float* x, const ActView& A, void* planes, int 
 // MFMA throughput probe (lp_mfma_probe_dev): grid x 512 threads, `out` grid*512 floats.
 hipError_t launch_mfma_probe(int kind, int rnd_ops, int iters, int grid, float* out, hipStream_t st);
 hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st);
+hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st);
 // planes from fp32 x (quantize + planes in one pass)
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N);
 hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,

@@ -26,7 +26,7 @@ def kernel_family():
     _lib.check(L().lp_set_gemm_kernel(0), "lp_set_gemm_kernel")
 
 
-@pytest.mark.parametrize("kern", [1, 2, 3])
+@pytest.mark.parametrize("kern", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,N,M", SHAPES, ids=lambda v: str(v))
 def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
     import torch
@@ -53,5 +53,5 @@ def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
 
 
 def test_gemm_kernel_rejects_unknown():
-    assert L().lp_set_gemm_kernel(4) == _lib.LP_EINVAL
+    assert L().lp_set_gemm_kernel(5) == _lib.LP_EINVAL
     assert L().lp_set_gemm_kernel(-1) == _lib.LP_EINVAL
