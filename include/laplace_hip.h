@@ -230,8 +230,10 @@ int lp_moe_ffn_dev(const float* x, int T, int H, const uint8_t* router_w, uint32
 /* Kernel-family switch for the Q4_K prefill GEMM (M > 64), no reference
  * counterpart; for comparison runs and tests. 0: chosen by shape (default);
  * 1: split-precision fp16/fp8 MFMA on row-major planes; 2: fp16/fp8 MFMA on
- * MFMA-fragment-order planes; 3: int8 MFMA with a per-block fp32 epilogue.
- * All four meet the same parity bar. Process-wide; not thread-safe against
+ * MFMA-fragment-order planes; 3: int8 MFMA with a per-block fp32 epilogue;
+ * 4 and 5: the wide-token kernel (128-token wave tiles on fragment-order
+ * planes) with 128 x 256 and 256 x 256 workgroup tiles. All meet the same
+ * parity bar. Process-wide; not thread-safe against
  * concurrent matmul calls. Returns LP_EINVAL for other values. */
 int lp_set_gemm_kernel(int kernel);
 

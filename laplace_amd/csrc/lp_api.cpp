@@ -1179,8 +1179,8 @@ int lp_mfma_probe_dev(int kind, int random_operands, int iters, int grid, float*
 }
 
 int lp_set_gemm_kernel(int kernel) {
-    if (kernel < 0 || kernel > 4) {
-        set_err("kernel %d: 0 (by shape), 1, 2, 3 or 4", kernel);
+    if (kernel < 0 || kernel > 5) {
+        set_err("kernel %d: 0 (by shape) or 1-5", kernel);
         return LP_EINVAL;
     }
     set_gemm_kernel(kernel);

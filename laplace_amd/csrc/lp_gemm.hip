@@ -1268,10 +1268,11 @@ size_t gemm_planes_bytes(int M, int K) {
     return a > i8 ? a : i8;
 }
 
-// Prefill GEMM kernel family: 0 = by shape (fr_auto), 1 = the
-// split-precision kernel on row-major planes (gemm_q4k_sp), 2 = the
-// fragment-order kernel (gemm_q4k_fr), 3 = the int8-MFMA kernel
-// (gemm_q4k_i8; measured slower, kept for comparison runs).
+// Prefill GEMM kernel family: 0 = by shape, 1 = the split-precision kernel
+// on row-major planes (gemm_q4k_sp), 2 = the fragment-order kernel
+// (gemm_q4k_fr), 3 = the int8-MFMA kernel (gemm_q4k_i8; measured slower,
+// kept for comparison runs), 4 and 5 = the wide-token kernel on
+// fragment-order planes (gemm_q4k_wt) with 128 x 256 and 256 x 256 tiles.
 static int g_gemm_kernel = 0;
 void set_gemm_kernel(int k) { g_gemm_kernel = k; }
 
@@ -1279,20 +1280,16 @@ bool gemm_i8_preferred(uint32_t type, int M, int K, int N) {
     return g_gemm_kernel == 3 && gemm_i8_supported(type, M, K) && N > 0;
 }
 
-// By shape: the fragment-order kernel at N >= 8192 rows from 256 tokens,
-// where it measured faster per step (bench.py --gemm-sweep: N 14336 M 2048
-// 491 vs 512 us, M 512 137 vs 154, N 8192 M 512 103 vs 119), the
-// split-precision kernel elsewhere (N 4096 M 2048 154 vs 161, M 512 68 vs 80;
-// below 256 tokens the fragment-order planes' two passes over x cost more).
-static bool fr_auto(int M, int K, int N) {
-    (void)K;
-    return M >= 256 && N >= 8192;
-}
-
+// By shape (bench.py --gemm-sweep over N 2048-14336, M 128-2048, K 4096 and
+// 14336): the wide-token kernel wherever its workgroups fill the CUs
+// (wt_auto_cfg), the split-precision kernel elsewhere (few tiles: its
+// 64-token tiles and single planes pass win). The fragment-order kernel
+// measured slower than one of the two at every shape of the sweep.
 static bool gemm_fr_preferred(int M, int K, int N) {
     if (!gemm_fr_supported(T_Q4_K, M, K) || N < 128) return false;
     if (g_gemm_kernel == 1 || g_gemm_kernel == 3) return false;
-    return g_gemm_kernel == 2 || g_gemm_kernel == 4 || fr_auto(M, K, N);
+    if (g_gemm_kernel == 2 || g_gemm_kernel >= 4) return true;
+    return wt_auto_cfg(M, K, N) >= 0;
 }
 
 bool gemm_supported(uint32_t type, int M, int K) {
@@ -1353,7 +1350,9 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
     if (gemm_fr_preferred(M, K, N))
-        return g_gemm_kernel == 4 ? launch_wt_gemm(w, planes, y, M, K, N, st) : launch_fr_gemm(w, planes, y, M, K, N, st);
+        return g_gemm_kernel == 2 ? launch_fr_gemm(w, planes, y, M, K, N, st)
+                                  : launch_wt_gemm(w, planes, y, M, K, N, st,
+                                                   g_gemm_kernel >= 4 ? g_gemm_kernel - 4 : wt_auto_cfg(M, K, N));
     const Planes P = carve_planes(planes, M, K);
     if (M <= kMfMaxM) {
         MfArgs a{w, (long)row_bytes(type, K), N, K, M, P, y};

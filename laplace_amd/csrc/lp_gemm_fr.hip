@@ -47,7 +47,6 @@
 // super-block. NS stages in flight, one barrier per K step, one workgroup per
 // CU (LDS NS x 32 KiB + 16 KiB).
 #include <hip/hip_runtime.h>
-#include <cstdlib>
 
 #include "lp_chunks.h"
 #include "lp_internal.h"
@@ -770,20 +769,24 @@ hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K
 // ---------------------------------------------------------------------------
 namespace {
 
-template <int TH>
+// TM token groups of 128 x RQ row groups of 64, one wave each.
+template <int TM, int RQ>
 struct WtCfg {
-    static constexpr int Tm = 4 * TH;                 // 32-token tiles per workgroup
-    static constexpr int Nw = 4 * TH;                 // waves
-    static constexpr int Bm = 32 * Tm, Bn = 256;
-    static constexpr int Hi = Tm * 4096, Lo = Tm * 2048, Codes = 8 * 1024;
+    static constexpr int Nw = TM * RQ;                // waves
+    static constexpr int TT = 4 * TM;                 // 32-token tiles per workgroup
+    static constexpr int Bm = 32 * TT, Bn = 64 * RQ;
+    static constexpr int Hi = TT * 4096, Lo = TT * 2048, Codes = 2 * RQ * 1024;
     static constexpr int Stage = Hi + Lo + Codes;
-    static constexpr int Hdr = Bn * 16, Sx = Tm * 1024;
+    static constexpr int Hdr = Bn * 16, Sx = TT * 1024;
     static constexpr int Sbuf = Hdr + Sx;
-    static constexpr int NS = TH == 1 ? 3 : 2;
-    static constexpr int CodesPerWave = 8 / Nw;      // 2 or 1
-    static constexpr int DmaStep = 6 + CodesPerWave;
+    static constexpr int NS = Nw == 4 || TM == 1 ? 3 : 2;
+    static constexpr int WPT = Nw / TT;               // waves copying one token tile's pieces
+    static constexpr int NA = 6 / WPT;                // hi/lo pieces per wave and step
+    static constexpr int NC = 2 * RQ / Nw;            // code pieces per wave and step
+    static constexpr int DmaStep = NA + NC;
     static constexpr size_t Lds = (size_t)NS * Stage + 2 * Sbuf + Nw * 128 * 4;
     static_assert(Stage / 1024 == Nw * DmaStep, "copies split evenly");
+    static_assert(Lds <= 160 * 1024, "LDS");
 };
 
 struct WtArgs {
@@ -806,37 +809,47 @@ struct WtPlan {
     uint32_t code_off[2], hdr_off;
 };
 
-template <int TH>
+// Copy i of step kt: i < NA the wave's hi/lo pieces (wave w takes pieces
+// (w % WPT) * NA .. + NA of token tile w / WPT: 4 hi then 2 lo), then its NC
+// code pieces w * NC + k (32 rows x 32 B each); i = DmaStep, DmaStep + 1 on a
+// super-block's first step: token tile w's min-term piece (w < TT) and the
+// headers of rows 64w .. 64w + 63 (w < RQ).
+template <int TM, int RQ>
 __device__ __forceinline__ void wt_issue(const WtPlan& d, int wave, int kt, uint8_t* st, uint8_t* sbb, int i) {
-    using C = WtCfg<TH>;
+    using C = WtCfg<TM, RQ>;
     const uint32_t lane16 = (threadIdx.x & 63) * 16;
     const int sb = kt >> 2, jb = kt & 3;
-    if (i < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + i * 1024), st + wave * 4096 + i * 1024);
-    else if (i < 6) dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (i - 4) * 1024), st + C::Hi + wave * 2048 + (i - 4) * 1024);
-    else if (i < 6 + C::CodesPerWave)
-        dma16(d.rs_w, d.code_off[i - 6], (uint32_t)(sb * 144 + 32 * jb),
-              st + C::Hi + C::Lo + (wave + (i - 6) * C::Nw) * 1024);
-    else if (jb == 0) {
-        if (i == C::DmaStep) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + C::Hdr + wave * 1024);
-        else if (wave < 4) dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
+    if (i < C::NA) {
+        const int tt = wave / C::WPT, j = (wave % C::WPT) * C::NA + i;
+        if (j < 4) dma16(d.rs_hi, lane16, (uint32_t)(kt * 4096 + j * 1024), st + tt * 4096 + j * 1024);
+        else dma16(d.rs_lo, lane16, (uint32_t)(kt * 2048 + (j - 4) * 1024), st + C::Hi + tt * 2048 + (j - 4) * 1024);
+    } else if (i < C::DmaStep) {
+        const int k = i - C::NA;
+        dma16(d.rs_w, d.code_off[k], (uint32_t)(sb * 144 + 32 * jb), st + C::Hi + C::Lo + (wave * C::NC + k) * 1024);
+    } else if (jb == 0) {
+        if (i == C::DmaStep) {
+            if (wave < C::TT) dma16(d.rs_sx, lane16, (uint32_t)(sb * 1024), sbb + C::Hdr + wave * 1024);
+        } else if (wave < RQ) {
+            dma16(d.rs_w, d.hdr_off, (uint32_t)(sb * 144), sbb + wave * 1024);
+        }
     }
 }
 
-template <int TH>
+template <int TM, int RQ>
 __device__ __forceinline__ int wt_count(int k, int nk, int wave) {
-    using C = WtCfg<TH>;
-    return k < nk ? C::DmaStep + ((k & 3) == 0 ? (wave < 4 ? 2 : 1) : 0) : 0;
+    using C = WtCfg<TM, RQ>;
+    return k < nk ? C::DmaStep + ((k & 3) == 0 ? (wave < C::TT ? 1 : 0) + (wave < RQ ? 1 : 0) : 0) : 0;
 }
 
-template <int TH, int ABL>
-__global__ void __launch_bounds__(256 * TH, 1) __attribute__((amdgpu_waves_per_eu(TH, TH)))
+template <int TM, int RQ>
+__global__ void __launch_bounds__(64 * TM * RQ, 1) __attribute__((amdgpu_waves_per_eu(TM * RQ / 4, TM * RQ / 4)))
 gemm_q4k_wt(WtArgs g) {
-    using C = WtCfg<TH>;
+    using C = WtCfg<TM, RQ>;
     constexpr int NS = C::NS;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int th = wave >> 2, rq = wave & 3;          // token half, row quarter
+    const int th = wave / RQ, rq = wave % RQ;         // token group, row group
     const int bid = blockIdx.x;
     int tile, part = 0, ksplit = 1;
     if (bid < g.nfull) {
@@ -861,20 +874,21 @@ gemm_q4k_wt(WtArgs g) {
 
     WtPlan d;
     {
-        int T = tm * C::Tm + wave;
-        T = T < g.tiles_pad ? T : g.tiles_pad - 1;
+        auto clampT = [&](int T) { return T < g.tiles_pad ? T : g.tiles_pad - 1; };
+        const int T = clampT(tm * C::TT + wave / C::WPT);
+        const int Ts = clampT(tm * C::TT + (wave < C::TT ? wave : 0));
         const int nt = g.N - n0 < C::Bn ? g.N - n0 : C::Bn;
         d.rs_w = make_rsrc(g.w + (size_t)n0 * g.rb, (uint32_t)((size_t)nt * g.rb));
         d.rs_hi = make_rsrc(g.hi + (size_t)T * ks_all * 4096, (uint32_t)(ks_all * 4096));
         d.rs_lo = make_rsrc(g.lo + (size_t)T * ks_all * 2048, (uint32_t)(ks_all * 2048));
-        d.rs_sx = make_rsrc(g.sx + (size_t)T * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
+        d.rs_sx = make_rsrc(g.sx + (size_t)Ts * nsb_all * 1024, (uint32_t)(nsb_all * 1024));
 #pragma unroll
         for (int c = 0; c < 2; c++) {
-            int row = (wave + c * C::Nw) * 32 + (lane & 31);      // code piece wave + c * Nw
+            int row = (wave * C::NC + (c < C::NC ? c : 0)) * 32 + (lane & 31);
             row = row < nt ? row : nt - 1;
             d.code_off[c] = (uint32_t)((size_t)row * g.rb) + 16 + 16 * (lane >> 5);
         }
-        int hrow = (wave & 3) * 64 + lane;
+        int hrow = (wave < RQ ? wave : 0) * 64 + lane;
         hrow = hrow < nt ? hrow : nt - 1;
         d.hdr_off = (uint32_t)((size_t)hrow * g.rb);
     }
@@ -942,7 +956,7 @@ gemm_q4k_wt(WtArgs g) {
         if (kt0 + i < nk)
 #pragma unroll
             for (int p = 0; p < C::DmaStep + 2; p++)
-                wt_issue<TH>(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
+                wt_issue<TM, RQ>(d, wave, kt0 + i, stage(i), sbuf(((kt0 + i) >> 2) & 1), p);
 
     // residual (fp8) products of a step, run after the next step's barrier:
     // their operands are in registers, so they fill the time the next
@@ -960,17 +974,16 @@ gemm_q4k_wt(WtArgs g) {
                               (int)Lp[t][1].x, (int)Lp[t][1].y, (int)Lp[t][1].z, (int)Lp[t][1].w};
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                if (ABL != 2)
-                    acc[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bvp[r], acc[t][r], 0, 0, 0, 0, 0, 0);
+                acc[t][r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bvp[r], acc[t][r], 0, 0, 0, 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 const int ci = t * 2 + r;
-                if (issue && ci < C::DmaStep) wt_issue<TH>(d, wave, kt, pst, psb, ci);
+                if (issue && ci < C::DmaStep) wt_issue<TM, RQ>(d, wave, kt, pst, psb, ci);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (issue) {
 #pragma unroll
-            for (int i = C::DmaStep < 8 ? C::DmaStep : 8; i < C::DmaStep + 2; i++) wt_issue<TH>(d, wave, kt, pst, psb, i);
+            for (int i = C::DmaStep < 8 ? C::DmaStep : 8; i < C::DmaStep + 2; i++) wt_issue<TM, RQ>(d, wave, kt, pst, psb, i);
         }
     };
 
@@ -981,12 +994,10 @@ gemm_q4k_wt(WtArgs g) {
             const int kt = 4 * sb + jb;
             int later = 0;
 #pragma unroll
-            for (int i = 1; i < NS - 1; i++) later += wt_count<TH>(kt + i, nk, wave);
-            if (ABL != 4 && ABL != 5) {
-                wait_dma(later);
-                __builtin_amdgcn_s_barrier();
-            }
-            const bool pf = ABL != 5 && kt + NS - 1 < nk;
+            for (int i = 1; i < NS - 1; i++) later += wt_count<TM, RQ>(kt + i, nk, wave);
+            wait_dma(later);
+            __builtin_amdgcn_s_barrier();
+            const bool pf = kt + NS - 1 < nk;
             uint8_t* const pst = stage((kt + NS - 1 - kt0) % NS);
             uint8_t* const psb = sbuf(((kt + NS - 1) >> 2) & 1);
             const uint32_t so = (uint32_t)(((kt - kt0) % NS) * C::Stage);
@@ -1023,7 +1034,7 @@ gemm_q4k_wt(WtArgs g) {
                     u[r] = unew;
                     zs[r] = ok ? 1.0f : 0.0f;
                 }
-                if (ABL != 3 && sb > sb_beg) fold(sbo ^ (uint32_t)C::Sbuf, rho, kap);
+                if (sb > sb_beg) fold(sbo ^ (uint32_t)C::Sbuf, rho, kap);
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     dmn[r] = fp16_bits_to_f32(h[r].x >> 16);
@@ -1049,7 +1060,7 @@ gemm_q4k_wt(WtArgs g) {
             lgkm<4>(cw);
 #pragma unroll
             for (int r = 0; r < 2; r++)
-                Vc[r] = ABL == 1 ? __builtin_bit_cast(h8, cw[r]) : decode4(cw[r][0], ml[r], al[r], mh[r], ah[r]);
+                Vc[r] = decode4(cw[r][0], ml[r], al[r], mh[r], ah[r]);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 h8 (&As)[4] = A[s & 1];
@@ -1096,13 +1107,13 @@ gemm_q4k_wt(WtArgs g) {
                 if (s < 3) {
 #pragma unroll
                     for (int r = 0; r < 2; r++)
-                        Vn[r] = ABL == 1 ? Vc[r] : decode4(cw[r][s + 1], ml[r], al[r], mh[r], ah[r]);
+                        Vn[r] = decode4(cw[r][s + 1], ml[r], al[r], mh[r], ah[r]);
                 }
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     const u32x4 q = __builtin_bit_cast(u32x4, Vc[r]);
-                    v8[r][2 * s] = ABL == 1 ? q.x : e4m3x4(q.x, q.y);
-                    v8[r][2 * s + 1] = ABL == 1 ? q.z : e4m3x4(q.z, q.w);
+                    v8[r][2 * s] = e4m3x4(q.x, q.y);
+                    v8[r][2 * s + 1] = e4m3x4(q.z, q.w);
                 }
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
@@ -1162,9 +1173,9 @@ gemm_q4k_wt(WtArgs g) {
     }
 }
 
-template <int TH>
+template <int TM, int RQ>
 hipError_t launch_wt(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st) {
-    using C = WtCfg<TH>;
+    using C = WtCfg<TM, RQ>;
     const FrPlanes P = carve_fr(planes, M, K);
     const int ntm = (M + C::Bm - 1) / C::Bm, ntn = (N + C::Bn - 1) / C::Bn, ntiles = ntm * ntn;
     const int cus = device_cu_count(), nsb = K >> 8;
@@ -1185,21 +1196,26 @@ hipError_t launch_wt(const uint8_t* w, void* planes, float* y, int M, int K, int
         }
     }
     const long nblk = (long)nfull + 2L * (ntiles - nfull);
-    static const int abl = getenv("LP_WT_ABL") ? atoi(getenv("LP_WT_ABL")) : 0;
-    switch (abl) {
-#define LP_A(a) case a: hipLaunchKernelGGL((gemm_q4k_wt<TH, a>), dim3((unsigned)nblk), dim3(64 * C::Nw), C::Lds, st, g); break;
-        LP_A(0) LP_A(1) LP_A(2) LP_A(3) LP_A(4) LP_A(5)
-#undef LP_A
-    }
+    hipLaunchKernelGGL((gemm_q4k_wt<TM, RQ>), dim3((unsigned)nblk), dim3(64 * C::Nw), C::Lds, st, g);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st) {
+int wt_auto_cfg(int M, int K, int N) {
+    const long cus = device_cu_count();
+    const long t1 = (long)((M + 255) / 256) * ((N + 255) / 256);
+    const long t0 = (long)((M + 127) / 128) * ((N + 255) / 256);
+    // K-weighted: a K-split tile round costs less than an idle one
+    if (t1 * (K / 256) >= 12L * cus) return 1;
+    if (t0 * 5 >= 2 * cus) return 0;
+    return -1;
+}
+
+hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st, int cfg) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    static const int th = getenv("LP_WT_TH") ? atoi(getenv("LP_WT_TH")) : 2;
-    return th == 1 ? launch_wt<1>(w, planes, y, M, K, N, st) : launch_wt<2>(w, planes, y, M, K, N, st);
+    if (cfg == 1) return launch_wt<2, 4>(w, planes, y, M, K, N, st);
+    return launch_wt<1, 4>(w, planes, y, M, K, N, st);
 }
 
 }  // namespace lp

@@ -118,7 +118,7 @@ size_t gemm_fr_planes_bytes(int M, int K);
 size_t gemm_i8_planes_bytes(int M, int K);
 bool gemm_i8_supported(uint32_t type, int M, int K);
 bool gemm_i8_preferred(uint32_t type, int M, int K, int N);
-// Prefill GEMM kernel family (0 by shape, 1 split-precision, 2 fragment-order, 3 int8).
+// Prefill GEMM kernel family (0 by shape, 1 split-precision, 2 fragment-order, 3 int8, 4/5 wide-token 128/256-token tiles).
 void set_gemm_kernel(int k);
 hipError_t launch_gemm_i8(const uint8_t* w, const ActView& A, void* planes, float* y, int M, int K, int N,
                           hipStream_t st);
@@ -127,7 +127,11 @@ hipError_t launch_fr_planes(const float* x, const ActView& A, void* planes, int 
 // MFMA throughput probe (lp_mfma_probe_dev): grid x 512 threads, `out` grid*512 floats.
 hipError_t launch_mfma_probe(int kind, int rnd_ops, int iters, int grid, float* out, hipStream_t st);
 hipError_t launch_fr_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st);
-hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st);
+hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K, int N, hipStream_t st, int cfg);
+// Wide-token GEMM configuration by shape: 1 (256 x 256 tiles, two waves per
+// SIMD), 0 (128 x 256 tiles, one wave per SIMD), or -1 (too few tiles for
+// either to fill the CUs).
+int wt_auto_cfg(int M, int K, int N);
 // planes from fp32 x (quantize + planes in one pass)
 hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N);
 hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,

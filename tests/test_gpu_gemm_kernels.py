@@ -1,6 +1,7 @@
-"""The three Q4_K prefill GEMM kernel families (lp_set_gemm_kernel 1-3:
+"""The Q4_K prefill GEMM kernel families (lp_set_gemm_kernel 1-5:
 split-precision fp16/fp8 MFMA on row-major planes, the same arithmetic on
-MFMA-fragment-order planes, int8 MFMA with a per-block fp32 epilogue), each
+MFMA-fragment-order planes, int8 MFMA with a per-block fp32 epilogue, and
+the wide-token kernel with 128 x 256 and 256 x 256 tiles), each
 against the oracle's gemm_int (src/matmul_simd.cpp:226-283, 432-455) within
 1e-4 normwise, and each bit-identical between the one-call path
 (lp_gemm_dev: quantize and planes from fp32 x) and the two-step path
@@ -26,7 +27,7 @@ def kernel_family():
     _lib.check(L().lp_set_gemm_kernel(0), "lp_set_gemm_kernel")
 
 
-@pytest.mark.parametrize("kern", [1, 2, 3, 4])
+@pytest.mark.parametrize("kern", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("K,N,M", SHAPES, ids=lambda v: str(v))
 def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
     import torch
@@ -53,5 +54,5 @@ def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
 
 
 def test_gemm_kernel_rejects_unknown():
-    assert L().lp_set_gemm_kernel(5) == _lib.LP_EINVAL
+    assert L().lp_set_gemm_kernel(6) == _lib.LP_EINVAL
     assert L().lp_set_gemm_kernel(-1) == _lib.LP_EINVAL
