@@ -9,7 +9,9 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblaplace_hip.so")
+# LAPLACE_HIP_LIB: load another build of the library (side-by-side timing runs)
+LIB_PATH = os.environ.get("LAPLACE_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                             "liblaplace_hip.so")
 
 LP_OK, LP_UNSUPPORTED, LP_EINVAL, LP_EHIP, LP_ENODEV = 0, 1, 2, 3, 4
 STATUS_NAMES = {0: "LP_OK", 1: "LP_UNSUPPORTED", 2: "LP_EINVAL", 3: "LP_EHIP", 4: "LP_ENODEV"}
