@@ -718,7 +718,7 @@ def load_traffic(name):
 
 GEMM_SWEEP = [(n, 4096, m) for n in (2048, 4096, 8192, 14336) for m in (128, 256, 512, 1024, 2048)] + \
     [(4096, 14336, 512), (4096, 14336, 2048)]
-GEMM_KERNELS = {1: "split-precision, row-major planes", 2: "fragment-order planes", 3: "int8 MFMA",
+GEMM_KERNELS = {0: "by shape", 1: "split-precision, row-major planes", 2: "fragment-order planes", 3: "int8 MFMA",
                 4: "wide-token, 128 x 256 tiles", 5: "wide-token, 256 x 256 tiles"}
 
 
