@@ -764,6 +764,26 @@ def mfma_probe(g: Gpu, iters=20000):
             print(json.dumps({"mfma_probe": name, "random_operands": bool(rnd), "us": round(us, 1),
                               "nominal_us_at_2.4GHz": round(ideal_us, 1),
                               "frac_of_nominal": round(ideal_us / us, 4)}), flush=True)
+    # co-issue: 32 fp16 products per iteration and wave with NV VALU
+    # operations after each; 256 workgroups of 8 waves (two per SIMD) or of 4
+    # waves (one per SIMD)
+    for kind in range(2, 10):
+        nv = (0, 1, 3, 6)[(kind - 2) % 4]
+        nw = 8 if kind < 6 else 4
+        it = iters // 4
+        g.check(g.L.lp_mfma_probe_dev(kind, 0, 100, grid, out.data_ptr(), g.stream()), "probe")
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        g.check(g.L.lp_mfma_probe_dev(kind, 0, it, grid, out.data_ptr(), g.stream()), "probe")
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3
+        ideal_us = 32 * 32 * it * (grid * nw / 1024) / 2.4e9 * 1e6
+        print(json.dumps({"coissue_probe": f"{nv} VALU per fp16 product, {nw // 4} wave(s) per SIMD",
+                          "us": round(us, 1), "nominal_us_at_2.4GHz": round(ideal_us, 1),
+                          "frac_of_nominal": round(ideal_us / us, 4)}), flush=True)
 
 
 READ_SWEEP_BYTES = [33_030_144, 49_545_216, 66_060_288, 99_090_432, 132_120_576, 198_180_864,

@@ -261,7 +261,11 @@ int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int un
  * tile set; kind 1: 8 int8 32x32x32 products) on register operands, either
  * near-constant (random_operands = 0) or random values of the GEMM's ranges;
  * `out` takes grid * 512 floats. Its time against the nominal rate is how
- * much of the MFMA peak the part sustains on such data. */
+ * much of the MFMA peak the part sustains on such data. Kinds 2-9: 32 fp16
+ * 32x32x16 products per iteration with 0, 1, 3 or 6 independent VALU
+ * operations after each, in 8-wave (2-5) or 4-wave (6-9) workgroups: how
+ * much of the matrix pipe's rate survives VALU work issued by the same wave
+ * (random_operands ignored). */
 int lp_mfma_probe_dev(int kind, int random_operands, int iters, int grid, float* out, void* stream);
 
 /* Text of the last error on this thread ("" if none). */

@@ -1170,7 +1170,7 @@ int lp_read_probe_dev(const void* buf, size_t bytes, int grid, int block, int un
 }
 
 int lp_mfma_probe_dev(int kind, int random_operands, int iters, int grid, float* out, void* stream) {
-    if (!out || iters < 1 || grid < 1 || (kind != 0 && kind != 1)) {
+    if (!out || iters < 1 || grid < 1 || kind < 0 || kind > 9) {
         set_err("bad probe arguments");
         return LP_EINVAL;
     }

@@ -655,12 +655,78 @@ __global__ void __launch_bounds__(512) mfma_probe_kernel(int rnd_ops, int iters,
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = sm;
 }
 
+// MFMA / VALU co-issue probe (measurement hook): per iteration a wave issues
+// 32 v_mfma_f32_32x32x16_f16 on a 4 x 2 tile set (the wide-token GEMM's
+// K step) with NV independent packed-fp16 VALU operations after each
+// product, in workgroups of NW waves: how much of the matrix pipe's rate
+// survives VALU work between the products of one wave (NW = 4: one wave per
+// SIMD at one workgroup per CU) or of two (NW = 8).
+template <int NV, int NW>
+__global__ void __launch_bounds__(64 * NW) coissue_probe_kernel(int iters, float* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    h8 A[4], B[2];
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 8; j++) A[i][j] = (_Float16)((lane * 7 + i * 13 + j) % 17 - 8);
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 8; j++) B[i][j] = (_Float16)((lane * 3 + i * 5 + j) % 11);
+    h2 v[8];
+    for (int i = 0; i < 8; i++) v[i] = h2{(_Float16)(lane * 0.01f + i), (_Float16)0.5f};
+    const h2 m = {(_Float16)0.999f, (_Float16)0.999f}, a = {(_Float16)0.001f, (_Float16)0.001f};
+    f16v acc[4][2];
+    for (int t = 0; t < 4; t++)
+        for (int r = 0; r < 2; r++)
+            for (int i = 0; i < 16; i++) acc[t][r][i] = 0.0f;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[t], B[r], acc[t][r], 0, 0, 0);
+#pragma unroll
+            for (int k = 0; k < NV; k++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = __builtin_elementwise_fma(v[i], m, a);
+            if (NV > 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        asm volatile("" : "+v"(A[0]), "+v"(B[0]));
+    }
+    float sm = 0.0f;
+    for (int t = 0; t < 4; t++)
+        for (int r = 0; r < 2; r++)
+            for (int i = 0; i < 16; i++) sm += acc[t][r][i];
+    for (int i = 0; i < 8; i++) sm += (float)v[i][0];
+    out[(size_t)blockIdx.x * 512 + threadIdx.x] = sm;
+}
+
 }  // namespace
 
 hipError_t launch_mfma_probe(int kind, int rnd_ops, int iters, int grid, float* out, hipStream_t st) {
     if (kind == 0) hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(grid), dim3(512), 0, st, rnd_ops, iters, out);
     else if (kind == 1) hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(grid), dim3(512), 0, st, rnd_ops, iters, out);
-    else return hipErrorInvalidValue;
+    else if (kind >= 2 && kind <= 9) {
+        // kinds 2-5: 8-wave workgroups, 0 / 1 / 3 / 6 VALU operations per
+        // product; 6-9: the same with 4-wave workgroups
+#define LP_P(NV, NW) hipLaunchKernelGGL((coissue_probe_kernel<NV, NW>), dim3(grid), dim3(64 * NW), 0, st, iters, out)
+        switch (kind) {
+            case 2: LP_P(0, 8); break;
+            case 3: LP_P(1, 8); break;
+            case 4: LP_P(3, 8); break;
+            case 5: LP_P(6, 8); break;
+            case 6: LP_P(0, 4); break;
+            case 7: LP_P(1, 4); break;
+            case 8: LP_P(3, 4); break;
+            default: LP_P(6, 4); break;
+        }
+#undef LP_P
+    } else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
