@@ -56,3 +56,37 @@ def test_gemm_kernel_family(orc, kernel_family, kern, K, N, M):
 def test_gemm_kernel_rejects_unknown():
     assert L().lp_set_gemm_kernel(6) == _lib.LP_EINVAL
     assert L().lp_set_gemm_kernel(-1) == _lib.LP_EINVAL
+
+
+@pytest.mark.parametrize("kern", [2, 4, 5])
+def test_gemm_kernel_scale_edge_cases(orc, kernel_family, kern):
+    """Super-block scales the wide-token kernel's per-super-block units treat
+    specially: d = 0 (the unit stays, V decodes as zero, only the min term
+    counts), subnormal fp16 d and dmin, and dmin far larger than d (the unit
+    ratio d_old / d_new spans many binades). Against the oracle's gemm_int
+    (src/matmul_simd.cpp:226-283) within 1e-4 normwise, row by row."""
+    print(f"gemm scale edge cases kernel {kern}", flush=True)
+    kernel_family(kern)
+    K, N, M = 2048, 512, 300
+    w = synth_weights(Q4_K, K, N, seed=77).reshape(N, K // 256, 144)
+    rng = np.random.default_rng(78)
+    f16 = lambda v: np.array([v], np.float16).view(np.uint8)
+    w[0:8, 1, 0:2] = f16(0.0)                                 # d = 0 in one super-block
+    w[8:16, :, 0:2] = f16(0.0)                                # d = 0 everywhere (min terms only)
+    w[16:24, 3, 0:2] = np.frombuffer(np.uint16(3).tobytes(), np.uint8)     # subnormal d
+    w[24:32, 5, 2:4] = np.frombuffer(np.uint16(7).tobytes(), np.uint8)     # subnormal dmin
+    w[32:40, 2, 0:2] = f16(1e-5)                              # dmin / d ~ 1e3 ...
+    w[32:40, 2, 2:4] = f16(0.02)
+    w[40:48, ::2, 0:2] = f16(30.0)                            # ... and d jumping between binades
+    w = w.reshape(-1)
+    x = synth_x(M, K, seed=79, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    toks = np.sort(rng.choice(M, 48, replace=False))
+    rows = np.arange(0, 56)
+    rb = len(w) // N
+    wsub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
+    ref = orc.gemm_int(Q4_K, x[toks], wsub, len(rows))
+    got = y[np.ix_(toks, rows)]
+    assert np.isfinite(got).all()
+    for j in range(0, 56, 8):
+        assert normwise(got[:, j:j + 8], ref[:, j:j + 8]) <= 1e-4, f"rows {j}..{j + 7}"
