@@ -384,8 +384,8 @@ static int host_gemm(const float* x, const uint8_t* w, uint32_t type, float* y, 
         LP_HIP(launch_gemv_i8mf(type, wd, A, c->yd, M, K, N, c->stream));
     } else if (use_gemm(type, M, K, N, wd) && !gemm_i8_preferred(type, M, K, N)) {
         void* planes = ws_planes(c->ws, M, K);
-        LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream, N));
-        LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream));
+        LP_HIP(launch_planes_from_x(c->xd, planes, M, K, c->stream, N, c->yd));
+        LP_HIP(launch_gemm_planes(type, wd, planes, c->yd, M, K, N, c->stream, true));
     } else {
         const ActView A = ws_view_full(c->ws, M, K);
         LP_HIP(launch_quantize(c->xd, M, K, A, c->stream));
@@ -721,8 +721,8 @@ int lp_gemm_dev(const float* x, const uint8_t* w, uint32_t type, float* y, int M
         }
         void* planes = ws_planes(ws, M, K);
         hipStream_t hs = static_cast<hipStream_t>(stream);
-        LP_HIP(launch_planes_from_x(x, planes, M, K, hs, N));
-        LP_HIP(launch_gemm_planes(type, w, planes, y, M, K, N, hs));
+        LP_HIP(launch_planes_from_x(x, planes, M, K, hs, N, y));
+        LP_HIP(launch_gemm_planes(type, w, planes, y, M, K, N, hs, true));
         return LP_OK;
     }
     if ((rc = lp_quantize_act_dev(x, M, K, ws, wsb, stream)) != LP_OK) return rc;

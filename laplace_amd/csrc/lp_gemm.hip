@@ -89,9 +89,11 @@ template <bool SP>
 __global__ void __launch_bounds__(256)
 gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restrict__ lo,
                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
-                 float* __restrict__ escale) {
+                 float* __restrict__ escale, float* __restrict__ yz, int N) {
 #pragma clang fp contract(off)
     const int m = blockIdx.y;
+    if (yz && blockIdx.x == 0)
+        for (int i = threadIdx.x; i < N; i += blockDim.x) yz[(size_t)m * N + i] = 0.0f;
     const int nb = K >> 5;
     const float* d = A.d + (size_t)m * nb;
     const float* s = A.sum + (size_t)m * nb;
@@ -661,9 +663,11 @@ static Planes carve_planes(void* base, int M, int K) {
 // 2: codes, hi/lo and shi/slo from the registers.
 template <int NF, bool SP>
 __global__ void __launch_bounds__(1024)
-quant_planes_kernel(const float* __restrict__ x, int K, Planes P) {
+quant_planes_kernel(const float* __restrict__ x, int K, Planes P, float* __restrict__ yz, int N) {
 #pragma clang fp contract(off)
     const int m = blockIdx.x;
+    if (yz)
+        for (int i = threadIdx.x; i < N; i += blockDim.x) yz[(size_t)m * N + i] = 0.0f;
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * K);
     const int n4 = K >> 2, nb = K >> 5;
     const int nt = blockDim.x;
@@ -1300,8 +1304,20 @@ bool gemm_supported(uint32_t type, int M, int K) {
 // (M <= kMfMaxM), the split-precision pair for the GEMM otherwise.
 static bool planes_sp(int M) { return M > kMfMaxM; }
 
-hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N) {
+// The split-precision GEMM splits K over two workgroups that add into a
+// zeroed y when 64-token tiles leave CUs idle; the planes kernels zero y's
+// rows then (one fewer launch).
+static bool sp_ksplit(int M, int K, int N) {
+    if (M <= kMfMaxM || gemm_fr_preferred(M, K, N)) return false;
+    const long cus = device_cu_count();
+    const long t128 = (long)((N + 255) / 256) * ((M + 127) / 128);
+    const long t64 = (long)((N + 255) / 256) * ((M + 63) / 64);
+    return t128 < cus && t64 <= cus && (K >> 8) >= 2;
+}
+
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N, float* y) {
     if (M <= 0) return hipSuccess;
+    float* yz = (y && sp_ksplit(M, K, N)) ? y : nullptr;
     if (gemm_fr_preferred(M, K, N)) return launch_fr_planes(x, ActView{}, planes, M, K, st);
     // NF float4 per thread, at most 1024 threads (K <= 32768); 8 | K/4/NF since 32 | K
     const int n4 = K / 4;
@@ -1311,8 +1327,8 @@ hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipS
     const Planes P = carve_planes(planes, M, K);
     const bool sp = planes_sp(M);
 #define LP_QP(NF)                                                                                   \
-    if (sp) hipLaunchKernelGGL((quant_planes_kernel<NF, true>), dim3(M), dim3(threads), 0, st, x, K, P); \
-    else hipLaunchKernelGGL((quant_planes_kernel<NF, false>), dim3(M), dim3(threads), 0, st, x, K, P);
+    if (sp) hipLaunchKernelGGL((quant_planes_kernel<NF, true>), dim3(M), dim3(threads), 0, st, x, K, P, yz, N); \
+    else hipLaunchKernelGGL((quant_planes_kernel<NF, false>), dim3(M), dim3(threads), 0, st, x, K, P, yz, N);
     switch (nf) {
         case 1: LP_QP(1) break;
         case 2: LP_QP(2) break;
@@ -1323,15 +1339,17 @@ hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipS
     return hipGetLastError();
 }
 
-static hipError_t launch_planes_from_act(const ActView& A, void* planes, int M, int K, hipStream_t st) {
+static hipError_t launch_planes_from_act(const ActView& A, void* planes, int M, int K, hipStream_t st, int N,
+                                         float* y) {
+    float* yz = (y && sp_ksplit(M, K, N)) ? y : nullptr;
     const Planes P = carve_planes(planes, M, K);
     const dim3 grid((K + kPlaneChunk - 1) / kPlaneChunk, M);
     if (planes_sp(M))
         hipLaunchKernelGGL(gemm_prep_kernel<true>, grid, dim3(kPlaneChunk / 4), 0, st, A, K, P.hi, P.lo, P.shi,
-                           P.slo, P.escale);
+                           P.slo, P.escale, yz, N);
     else
         hipLaunchKernelGGL(gemm_prep_kernel<false>, grid, dim3(kPlaneChunk / 4), 0, st, A, K, P.hi, P.lo, P.shi,
-                           P.slo, P.escale);
+                           P.slo, P.escale, yz, N);
     return hipGetLastError();
 }
 
@@ -1346,7 +1364,7 @@ static hipError_t launch_sp(SpArgs g, hipStream_t st) {
 }
 
 hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,
-                              hipStream_t st) {
+                              hipStream_t st, bool y_zeroed) {
     if (!gemm_supported(type, M, K)) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0) return hipSuccess;
     if (gemm_fr_preferred(M, K, N))
@@ -1370,7 +1388,7 @@ hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, flo
     if (t128 >= cus) return launch_sp<4, 4, 2>(g, st);
     const long t64 = (long)((N + 255) / 256) * ((M + 63) / 64);
     g.ksplit = (t64 <= cus && (K >> 8) >= 2) ? 2 : 1;
-    if (g.ksplit == 2) {
+    if (g.ksplit == 2 && !y_zeroed) {
         const size_t n4 = (size_t)M * N;
         hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, st, y, n4);
     }
@@ -1383,9 +1401,9 @@ hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* 
     if (M <= 0 || N <= 0) return hipSuccess;
     if (gemm_i8_preferred(type, M, K, N)) return launch_gemm_i8(w, A, planes, y, M, K, N, st);
     hipError_t e = gemm_fr_preferred(M, K, N) ? launch_fr_planes(nullptr, A, planes, M, K, st)
-                                              : launch_planes_from_act(A, planes, M, K, st);
+                                              : launch_planes_from_act(A, planes, M, K, st, N, y);
     if (e != hipSuccess) return e;
-    return launch_gemm_planes(type, w, planes, y, M, K, N, st);
+    return launch_gemm_planes(type, w, planes, y, M, K, N, st, true);
 }
 
 bool moe_mf_supported(uint32_t type, int K) {

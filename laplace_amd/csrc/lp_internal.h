@@ -132,10 +132,13 @@ hipError_t launch_wt_gemm(const uint8_t* w, void* planes, float* y, int M, int K
 // SIMD), 0 (128 x 256 tiles, one wave per SIMD), or -1 (too few tiles for
 // either to fill the CUs).
 int wt_auto_cfg(int M, int K, int N);
-// planes from fp32 x (quantize + planes in one pass)
-hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N);
+// planes from fp32 x (quantize + planes in one pass); with y given, also the
+// zeroing of y that the product below needs at some shapes, which then runs
+// with y_zeroed = true
+hipError_t launch_planes_from_x(const float* x, void* planes, int M, int K, hipStream_t st, int N,
+                                float* y = nullptr);
 hipError_t launch_gemm_planes(uint32_t type, const uint8_t* w, void* planes, float* y, int M, int K, int N,
-                              hipStream_t st);
+                              hipStream_t st, bool y_zeroed = false);
 // planes from quantized activations A, then the product
 hipError_t launch_gemm(uint32_t type, const uint8_t* w, const ActView& A, void* planes, float* y,
                        int M, int K, int N, hipStream_t st);
