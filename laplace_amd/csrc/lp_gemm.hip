@@ -746,6 +746,7 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P, float* __restr
 
 constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
+constexpr int kMfMoeRows = 128;    // grouped MoE: weight rows per workgroup (at least two sets)
 constexpr int kMfMaxM = 16;
 // Measured on MI355X (Q4_K 18944 x 3584): the GEMV tile kernel is faster
 // up to M = 4, the small-M MFMA kernels from M = 5 to 16.
@@ -874,14 +875,25 @@ gemv_q4k_mf(MfArgs a) {
 // 4*(lane/16)+r, column = lane%16.
 typedef int i4v __attribute__((ext_vector_type(4)));
 
+// K-slices for a row of nsb super-blocks over nwv waves: the largest power
+// of two <= min(nsb, nwv) (nwv a power of two)
+__host__ __device__ inline int mf_kslices(int nsb, int nwv) {
+    int k = 1;
+    while (2 * k <= nsb && 2 * k <= nwv) k *= 2;
+    return k;
+}
+
 // MOE: blockIdx.y is a routed group (expert, first pair, n <= 16 pairs): the
 // group's activation rows (token, or pair in the multi form) and outputs
 // (pair rows) replace rows 0..M-1.
-// TL 16-row tiles per workgroup, NWV waves (K-slices).
-template <bool MOE, int TL = kMfTiles, int NWV = kMfWaves>
+// TL 16-row tiles per row set, NWV waves (K-slices); ri row sets per
+// workgroup, one after another, all served by one activation staging. RWS:
+// as many K-slices as the row has super-blocks (a power of two, at most
+// NWV), the remaining waves on further row tiles of the set.
+template <bool MOE, int TL = kMfTiles, int NWV = kMfWaves, bool RWS = false>
 __global__ void __launch_bounds__(64 * NWV)
 gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N,
-              const uint8_t* __restrict__ route, int max_groups, int multi, int topk, long ebytes) {
+              const uint8_t* __restrict__ route, int max_groups, int multi, int topk, long ebytes, int ri = 1) {
     __shared__ f4v red[NWV][TL][64];
     extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd, then [nb][16] xs
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -915,8 +927,17 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
     __syncthreads();
     const bool tv = tok < M;
     const int8_t* aq = A.qs + (size_t)act_row(tv ? tok : 0) * K + 8 * g;
-    const int row0 = blockIdx.x * (16 * TL) + (lane & 15);
-    const int sb0 = wv * nsb / NWV, sb1 = (wv + 1) * nsb / NWV;
+    // RWS: K-slices of whole super-blocks, as many as the row has (a power of
+    // two, at most NWV), the other waves on further row tiles
+    const int ks_n = RWS ? mf_kslices(nsb, NWV) : NWV, rw_n = NWV / ks_n;
+    const int ks = wv % ks_n, rw = wv / ks_n;
+    const int sb0 = ks * nsb / ks_n, sb1 = (ks + 1) * nsb / ks_n;
+    // ri consecutive row sets per workgroup: the activation staging above
+    // serves all of them
+    for (int it = 0; it < ri; it++) {
+    const int rbase = (blockIdx.x * ri + it) * rw_n * (16 * TL);
+    if (rbase >= N) break;
+    const int row0 = rbase + rw * (16 * TL) + (lane & 15);
     const uint8_t* wr[TL];
 #pragma unroll
     for (int t = 0; t < TL; t++) {
@@ -977,13 +998,12 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
 #pragma unroll
     for (int t = 0; t < TL; t++) red[wv][t][lane] = acc[t];
     __syncthreads();
-    // wave t sums tile t over the K-slices in a fixed order
-    if (wv < TL) {
-        const int t = wv;
-        f4v sum = red[0][t][lane];
-#pragma unroll
-        for (int i = 1; i < NWV; i++) sum += red[i][t][lane];
-        const int row = row0 + 16 * t;
+    // each output tile summed over its K-slices in a fixed order
+    for (int o = wv; o < rw_n * TL; o += NWV) {
+        const int ro = o / TL, t = o % TL;
+        f4v sum = red[ro * ks_n][t][lane];
+        for (int i = 1; i < ks_n; i++) sum += red[ro * ks_n + i][t][lane];
+        const int row = rbase + ro * (16 * TL) + 16 * t + (lane & 15);
         if (row < N) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -996,6 +1016,8 @@ gemv_q4k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
                 }
             }
         }
+    }
+    if (ri > 1) __syncthreads();                  // red is reused by the next row set
     }
 }
 
@@ -1414,9 +1436,18 @@ hipError_t launch_moe_i8mf(const uint8_t* w, const ActView& A, const void* route
                            int topk, float* y, int K, int N, hipStream_t st) {
     if ((size_t)(K / 32) * 16 * 8 > 64 * 1024) return hipErrorInvalidValue;
     const long rb = (long)row_bytes(T_Q4_K, K);
-    hipLaunchKernelGGL(gemv_q4k_i8mf<true>, dim3((N + 16 * kMfTiles - 1) / (16 * kMfTiles), max_groups),
+    // row sets of rw rows, ri of them per workgroup: 128 rows (K 2048: 4 sets
+    // of 32), two sets when a set has 128 (K 768: two K-slices, 4 row groups).
+    // Measured at 128 experts, top-8, 256 / 512 tokens (us per layer): one
+    // 32-row set and 8 K-slices for every K 358 / 591, 4 sets 313 / 496,
+    // with the row split at short K 291 / 451, two sets at K 768 281 / 451;
+    // 512 rows per workgroup 382 / 455 (too few workgroups)
+    const int rw = 16 * kMfTiles * (kMfWaves / mf_kslices(K / 256, kMfWaves));
+    const int ri = rw < kMfMoeRows ? kMfMoeRows / rw : 2;
+    const int rows = rw * ri;
+    hipLaunchKernelGGL((gemv_q4k_i8mf<true, kMfTiles, kMfWaves, true>), dim3((N + rows - 1) / rows, max_groups),
                        dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w, rb, A, y, 0, K, N,
-                       static_cast<const uint8_t*>(route), max_groups, multi, topk, rb * N);
+                       static_cast<const uint8_t*>(route), max_groups, multi, topk, rb * N, ri);
     return hipGetLastError();
 }
 
