@@ -410,6 +410,18 @@ __device__ __forceinline__ float dpp_x8f(float v, int x) {
     return __uint_as_float(x == 1 ? dpp_x8<1>(b) : x == 2 ? dpp_x8<2>(b) : dpp_x8<4>(b));
 }
 
+// Row exponent of the prefill planes: E with mx = f * 2^E, f in [0.5, 1)
+// (0 for a zero, NaN or infinite mx), clamped at -100 so that 2^E and 2^-E
+// are both finite normal floats: a row whose largest block scale is
+// subnormal (every |x| below ~1.5e-36) then gets t = xd * q * 2^(9 + 100),
+// still below 2^16 in magnitude, instead of an overflowing 2^-E.
+constexpr int kRowExpMin = -100;
+__device__ __forceinline__ int row_exponent(float mx) {
+    int e = 0;
+    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);
+    return e < kRowExpMin ? kRowExpMin : e;
+}
+
 __device__ __forceinline__ Q8Group quant_group8(const float4 v) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     uint32_t nan = (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);

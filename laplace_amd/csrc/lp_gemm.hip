@@ -107,8 +107,7 @@ gemm_prep_kernel(ActView A, int K, _Float16* __restrict__ hi, _Float16* __restri
         __syncthreads();
     }
     mx = red[0];
-    int e = 0;
-    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+    const int e = row_exponent(mx);
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0 && blockIdx.x == 0) escale[m] = ldexpf(1.0f, e);
     // this workgroup's chunk: 4 codes per thread
@@ -701,8 +700,7 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P, float* __restr
     mx = 0.0f;
     for (int wv = 0; wv < (nt + 63) / 64; wv++) mx = fmaxf(mx, red[wv]);
     mx = mx / 127.0f;
-    int e = 0;
-    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+    const int e = row_exponent(mx);
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0) P.escale[m] = ldexpf(1.0f, e);
     // pass 2

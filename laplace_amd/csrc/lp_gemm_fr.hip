@@ -480,8 +480,7 @@ __global__ void __launch_bounds__(256) fr_rowexp_kernel(const float* __restrict_
         for (int o = 8; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     }
     if (!ACT) mx = mx / 127.0f;
-    int e = 0;
-    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+    const int e = row_exponent(mx);
     if (lane == 0) escale[m] = ldexpf(1.0f, e);
 }
 
@@ -641,8 +640,7 @@ __global__ void __launch_bounds__(64 * kFxTok * kFxKw) fr_planes_x_kernel(const 
 #pragma unroll
             for (int k = 0; k < kFxKw; k++) mx = fmaxf(mx, wmax[k][rr]);
         }
-        int e = 0;
-        if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);
+        const int e = row_exponent(mx);
         const float es = ldexpf(1.0f, e);
         if (lane == 0 && kh == 0) escale[m] = es;
         const float inv = 1.0f / es;

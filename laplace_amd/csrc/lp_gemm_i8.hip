@@ -356,8 +356,7 @@ __global__ void __launch_bounds__(256) i8_prep_kernel(ActView A, int M, int Mp, 
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     }
-    int e = 0;
-    if (mx > 0.0f && mx == mx && mx < 3.0e38f) (void)frexpf(mx, &e);
+    const int e = row_exponent(mx);
     const float inv = ldexpf(1.0f, -e);
     if (lane == 0) escale[m] = ldexpf(1.0f, e);
     for (int b = lane; b < nb; b += 64) {

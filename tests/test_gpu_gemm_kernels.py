@@ -90,3 +90,43 @@ def test_gemm_kernel_scale_edge_cases(orc, kernel_family, kern):
     assert np.isfinite(got).all()
     for j in range(0, 56, 8):
         assert normwise(got[:, j:j + 8], ref[:, j:j + 8]) <= 1e-4, f"rows {j}..{j + 7}"
+
+
+@pytest.mark.parametrize("kern", [0, 1, 2, 4, 5])
+def test_gemm_kernel_activation_edge_rows(orc, kernel_family, kern):
+    """Activation rows the row exponent treats specially, through the
+    one-call path (planes from fp32 x: one launch for K <= 4096) and the
+    two-step path (planes from the stored blocks), bit for bit: a row of
+    zeros (exponent 0), a row of subnormals, a row whose only large block
+    holds a NaN (the NaN block's scale is skipped), rows with +-inf, a row
+    with one huge block. Finite rows also against the oracle within 1e-4;
+    the subnormal row's exponent is clamped, so its outputs stay finite."""
+    import torch
+    print(f"gemm activation edge rows kernel {kern}", flush=True)
+    kernel_family(kern)
+    K, N, M = 1024, 256, 160
+    w = synth_weights(Q4_K, K, N, seed=91)
+    x = synth_x(M, K, seed=92, outliers=0.01)
+    x[5] = 0.0
+    x[6] = np.float32(1e-40) * np.sign(x[6])
+    x[7, 64:96] *= 1e6
+    x[7, 70] = np.nan
+    x[8, 300] = np.inf
+    x[9, 900] = -np.inf
+    x[10, 512:544] *= 1e30
+    y = gemm_dev(Q4_K, x, w, N)
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(M, K)
+    y2 = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    assert L().lp_quantize_act_dev(xd.data_ptr(), M, K, ws.data_ptr(), nb, stream()) == 0
+    assert L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), Q4_K, y2.data_ptr(), M, K, N, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(M, N).view(np.uint32), y.view(np.uint32))
+    assert np.isfinite(y[[0, 5, 6, 10, 11, 159]]).all()
+    # the subnormal row (6) is left out here: the reference's own products
+    # of subnormal block scales (d * xd, src/matmul_simd.cpp:226-283) keep a
+    # few significant bits, so the oracle is no yardstick for it
+    fin = [0, 5, 10, 11, 159]
+    ref = orc.gemm_int(Q4_K, x[fin], w, N)
+    for i, r in enumerate(fin):
+        assert normwise(y[r], ref[i]) <= 1e-4, f"row {r}"
