@@ -130,3 +130,28 @@ def test_gemm_kernel_activation_edge_rows(orc, kernel_family, kern):
     ref = orc.gemm_int(Q4_K, x[fin], w, N)
     for i, r in enumerate(fin):
         assert normwise(y[r], ref[i]) <= 1e-4, f"row {r}"
+
+
+@pytest.mark.parametrize("kern", [0, 5])
+def test_gemm_planes_grid_stride(orc, kernel_family, kern):
+    """More token pairs than the one-launch planes kernel has workgroups (4
+    per CU): its workgroups take a second pair, whose rows were requested
+    while the first was processed. One-call path against the two-step
+    path bit for bit, sampled rows against the oracle."""
+    import torch
+    print(f"gemm planes grid stride kernel {kern}", flush=True)
+    kernel_family(kern)
+    K, N, M = 512, 256, 2 * 4 * 256 + 100
+    w = synth_weights(Q4_K, K, N, seed=95)
+    x = synth_x(M, K, seed=96, outliers=0.01)
+    y = gemm_dev(Q4_K, x, w, N)
+    xd, wd = to_dev(x), to_dev(w)
+    ws, nb = workspace(M, K)
+    y2 = torch.empty(M * N, dtype=torch.float32, device="cuda")
+    assert L().lp_quantize_act_dev(xd.data_ptr(), M, K, ws.data_ptr(), nb, stream()) == 0
+    assert L().lp_gemm_q_dev(ws.data_ptr(), wd.data_ptr(), Q4_K, y2.data_ptr(), M, K, N, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y2.cpu().numpy().reshape(M, N).view(np.uint32), y.view(np.uint32))
+    toks = np.array([0, 1, 2047, 2048, 2049, 2100, M - 1])
+    ref = orc.gemm_int(Q4_K, x[toks], w, N)
+    assert normwise(y[toks], ref) <= 1e-4
