@@ -164,3 +164,20 @@ def test_moe_many_pairs_per_expert_mfma(orc, multi):
     y = moe_dev(t, x, w, idx, E, N, multi)
     assert np.isfinite(y).all()
     assert normwise(y, oracle_grouped(orc, t, x, w, idx, K, N, multi)) <= TOL
+
+
+@pytest.mark.parametrize("K,N", [(256, 300), (768, 200), (2048, 96), (3072, 40)], ids=lambda v: str(v))
+def test_moe_mfma_row_sets(orc, K, N):
+    """The MFMA groups' workgroups take several row sets in turn, and at
+    short K split their waves into fewer K-slices and more row groups (K 256:
+    1 slice x 8 row groups, 768: 2 x 4, 2048: 8 x 1, 3072: 8 x 1 over 12
+    super-blocks): ragged N (a partial last row set, workgroups with fewer
+    sets), 6 experts, 64 tokens, top-2 (about 21 pairs per expert, so some
+    experts take two groups), against the oracle."""
+    t, E, T, topk = Q4_K, 6, 64, 2
+    w = synth_weights(t, K, N * E, seed=K + N)
+    idx = routing(T, topk, E, seed=K)
+    x = synth_x(T, K, seed=N, outliers=0.01)
+    y = moe_dev(t, x, w, idx, E, N, False)
+    assert np.isfinite(y).all()
+    assert normwise(y, oracle_grouped(orc, t, x, w, idx, K, N, False)) <= TOL
