@@ -437,6 +437,8 @@ static int moe_group_size(uint32_t type, int K, int P, int E) {
     return rq_moe_supported(type, K) && P > 2 * E ? kRqMoeGroup : 4;
 }
 
+static constexpr bool kMoeFuseQuantRoute = true;
+
 static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, uint32_t type,
                  float* y, int T, int topk, int E, int K, int N, void* ws, hipStream_t st) {
     const int P = T * topk, rows = multi ? P : T;
@@ -447,9 +449,16 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
     // 10 per expert 259 vs 274 us on the GEMV kernels, 8 per expert 246 vs
     // 236 us); decode-sized batches stay on the GEMV kernels
     const bool mf = moe_mf_supported(type, K) && P > 8 * E;
-    LP_HIP(launch_quantize(x, rows, K, A, st));
-    LP_HIP(launch_moe_grouped(type, w, A, mf ? 16 : moe_group_size(type, K, P, E), rows, idx, P, E, multi, topk,
-                              route, y, K, N, st));
+    const int gs = mf ? 16 : moe_group_size(type, K, P, E);
+    if (kMoeFuseQuantRoute) {
+        // one launch for the quantization and the route table (the route
+        // kernel alone is one short workgroup)
+        LP_HIP(launch_moe_quant_route(x, rows, K, A, idx, P, E, route, gs, st));
+        LP_HIP(launch_moe_grouped_routed(type, w, A, gs, rows, P, E, multi, topk, route, y, K, N, st));
+    } else {
+        LP_HIP(launch_quantize(x, rows, K, A, st));
+        LP_HIP(launch_moe_grouped(type, w, A, gs, rows, idx, P, E, multi, topk, route, y, K, N, st));
+    }
     return LP_OK;
 }
 

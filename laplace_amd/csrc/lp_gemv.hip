@@ -28,13 +28,14 @@ namespace lp {
 // ---------------------------------------------------------------------------
 // Quantizer: 8 lanes per 32-element block, one float4 per lane.
 
-__global__ void __launch_bounds__(256)
-quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
+// Workgroup wg of nwg quantizing workgroups.
+__device__ __forceinline__ void quantize_rows(const float* __restrict__ x, int M, int K, const ActView& A, int wg,
+                                              int nwg) {
     const int nb = K >> 5;
     const long total = (long)M * nb;
     const int g = threadIdx.x & 7;                       // lane within the block's group
-    const long stride = (long)gridDim.x * (blockDim.x >> 3);
-    for (long blk = (long)blockIdx.x * (blockDim.x >> 3) + (threadIdx.x >> 3); blk < total;
+    const long stride = (long)nwg * (blockDim.x >> 3);
+    for (long blk = (long)wg * (blockDim.x >> 3) + (threadIdx.x >> 3); blk < total;
          blk += stride) {
         const long m = blk / nb, b = blk - m * nb;
         const float4 v = *reinterpret_cast<const float4*>(x + m * K + 32 * b + 4 * g);
@@ -46,6 +47,11 @@ quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
             A.s16[blk] = q.s16;
         }
     }
+}
+
+__global__ void __launch_bounds__(256)
+quantize_act_kernel(const float* __restrict__ x, int M, int K, ActView A) {
+    quantize_rows(x, M, K, A, blockIdx.x, gridDim.x);
 }
 
 hipError_t launch_quantize(const float* x, int M, int K, const ActView& A, hipStream_t st) {
@@ -1846,6 +1852,34 @@ moe_route_kernel(const int* __restrict__ idx, int P, int E, uint8_t* __restrict_
                  int max_groups, int gsize) {
     extern __shared__ int rs[];
     build_route(idx, P, E, route, max_groups, gsize, rs);
+}
+
+// The grouped dispatch's two preparation steps in one launch: the last
+// workgroup builds the route table (build_route), the others quantize the
+// activation rows exactly as quantize_act_kernel does.
+__global__ void __launch_bounds__(kRouteThreads)
+moe_quant_route_kernel(const float* __restrict__ x, int M, int K, ActView A, const int* __restrict__ idx, int P,
+                       int E, uint8_t* __restrict__ route, int max_groups, int gsize) {
+    extern __shared__ int rs[];
+    if ((int)blockIdx.x == (int)gridDim.x - 1) {
+        build_route(idx, P, E, route, max_groups, gsize, rs);
+        return;
+    }
+    quantize_rows(x, M, K, A, blockIdx.x, gridDim.x - 1);
+}
+
+hipError_t launch_moe_quant_route(const float* x, int rows, int K, const ActView& A, const int* idx, int P, int E,
+                                  void* route, int gsize, hipStream_t st) {
+    if (P <= 0) return launch_quantize(x, rows, K, A, st);
+    if (E <= 0 || E > kMoeMaxExperts || gsize < kMoeGroup) return hipErrorInvalidValue;
+    const long blocks = (long)rows * (K >> 5);
+    long qwg = (blocks + 127) / 128;                     // 128 blocks per 1024-thread workgroup
+    if (qwg > 2048) qwg = 2048;
+    if (qwg < 1) qwg = 1;
+    const size_t rshm = sizeof(int) * (3 * (size_t)E + 2 * kRouteThreads);
+    hipLaunchKernelGGL(moe_quant_route_kernel, dim3((unsigned)(qwg + 1)), dim3(kRouteThreads), rshm, st, x, rows, K,
+                       A, idx, P, E, static_cast<uint8_t*>(route), moe_max_groups(P, E), gsize);
+    return hipGetLastError();
 }
 
 template <uint32_t T, int M>

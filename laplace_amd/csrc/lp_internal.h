@@ -165,6 +165,10 @@ hipError_t launch_moe_grouped(uint32_t type, const uint8_t* w, const ActView& A,
 // of <= gsize pairs), and the grouped products on a route table built for the
 // same pairs and group size.
 hipError_t launch_moe_route(const int* idx, int P, int E, void* route, int gsize, hipStream_t st);
+// launch_quantize(x, rows, K, A) and launch_moe_route(idx, P, E, route, gsize)
+// in one launch
+hipError_t launch_moe_quant_route(const float* x, int rows, int K, const ActView& A, const int* idx, int P, int E,
+                                  void* route, int gsize, hipStream_t st);
 // gu (the MoE layer's down pass): the activations are GeGLU of the pairs'
 // gate|up rows (2 K floats each), quantized while the GEMV stages them, where
 // moe_geglu_fusable says the kernel for (type, K, gsize, w) does that.
