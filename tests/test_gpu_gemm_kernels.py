@@ -16,7 +16,9 @@ from laplace_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(512, 300, 130), (4096, 512, 257), (2816, 200, 129), (1024, 4096, 384), (4096, 14336, 128)]
+# (K, N, M); K > 4096 takes the two-launch planes from fp32 x
+SHAPES = [(512, 300, 130), (4096, 512, 257), (2816, 200, 129), (1024, 4096, 384), (4096, 14336, 128),
+          (5120, 264, 160)]
 
 
 @pytest.fixture
