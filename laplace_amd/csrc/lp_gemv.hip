@@ -565,7 +565,7 @@ __device__ __forceinline__ float q4k_sb_dot(const u32x4 (&v)[9], uint32_t act_l,
 template <bool FUSEQ>
 __global__ void __launch_bounds__(1024)
 gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
-              int K, int N, int rpw) {
+              int K, int N, int rpw, int tail_lds) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
@@ -593,6 +593,23 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
             v[k] = ld_nt16(w + a);
         }
     };
+    // tail_lds: the super-blocks past the first nw segments are copied
+    // straight into LDS (1 KiB per wave instruction) before anything else is
+    // requested, and computed after the first round from there, instead of
+    // being requested only once the first segment is done
+    const int tail_sb = F - 64 * nw;
+    uint8_t* tbuf = smem + xbuf_off + (size_t)nw * 9216;
+    if (tail_lds && tail_sb > 0) {
+        const uintptr_t g0 = reinterpret_cast<uintptr_t>(w) + (uintptr_t)(base + (long)nw * 9216);
+        const uintptr_t glast = reinterpret_cast<uintptr_t>(w) + (uintptr_t)(total - 16);
+        const int pieces = (tail_sb * 144 + 1023) / 1024;
+        for (int p = wv; p < pieces; p += nw) {
+            uintptr_t ga = g0 + (uintptr_t)p * 1024 + (uintptr_t)lane * 16;
+            ga = ga > glast ? glast : ga;
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ga),
+                                             (__attribute__((address_space(3))) void*)(tbuf + p * 1024), 16, 0, 0);
+        }
+    }
     int s = wv;
     u32x4 v[9];
     if constexpr (FUSEQ) {
@@ -620,7 +637,7 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
     const uint32_t act0 = lds_addr_of(smem);
     float part0 = 0.0f, part1 = 0.0f;
 #pragma unroll 1
-    for (int r = 0; r < 2 && s < nseg; r++) {
+    for (int r = 0; r < (tail_lds ? 1 : 2) && s < nseg; r++) {
         // a second segment (only where segments outnumber waves) is requested
         // after the first is computed: two in registers would spill
         if (r == 1) load_seg(s, v);
@@ -644,10 +661,26 @@ gemv_q4k_flat(const uint8_t* __restrict__ w, ActView A, const float* __restrict_
         else part1 = t;
         s += nw;
     }
-    // every wave is past its transpose buffer: partial sums over them
+    // every wave is past its transpose buffer: partial sums over them; the
+    // tail copies are complete before the barrier
+    if (tail_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     float* ps = reinterpret_cast<float*>(smem + xbuf_off);
     const int f0 = 64 * wv + lane, f1 = f0 + 64 * nw;
+    if (tail_lds && s < nseg) {
+        // the tail segment from LDS: super-block f1 at (f1 - 64 nw) * 144
+        const u32x4* mine = reinterpret_cast<const u32x4*>(tbuf + (size_t)(f1 < F ? f1 - 64 * nw : 0) * 144);
+#pragma unroll
+        for (int k = 0; k < 9; k++) v[k] = mine[k];
+        const int sb = f1 - (f1 / nsb) * nsb;
+        float xd[8], xs[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            xd[k] = dl[8 * sb + k];
+            xs[k] = sl_[8 * sb + k];
+        }
+        part1 = q4k_sb_dot(v, act0 + sb * 272, xd, xs);
+    }
     if (f0 < F) ps[f0] = part0;
     if (f1 < F) ps[f1] = part1;
     __syncthreads();
@@ -1538,15 +1571,24 @@ static bool q4k_flat_geom(int K, int N, int& rpw, int& nw) {
     return true;
 }
 
+constexpr bool kFlatTailLds = true;
+
 static hipError_t launch_q4k_flat(const uint8_t* w, const ActView& A, const float* x, float* y, int K, int N,
                                   hipStream_t st) {
     int rpw, nw;
     if (!q4k_flat_geom(K, N, rpw, nw)) return hipErrorInvalidValue;
     const size_t act_lds = ((size_t)(K / 256) * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
-    const size_t shm = act_lds + (size_t)nw * 9216;
+    // the super-blocks past the first round, if their copy fits the LDS
+    const long tail_sb = (long)rpw * (K / 256) - 64L * nw;
+    const size_t tail_bytes = tail_sb > 0 ? (size_t)((tail_sb * 144 + 1023) / 1024) * 1024 : 0;
+    const int tail_lds = kFlatTailLds && tail_sb > 0 && tail_sb <= 64L * nw &&
+                         act_lds + (size_t)nw * 9216 + tail_bytes <= 160 * 1024;
+    const size_t shm = act_lds + (size_t)nw * 9216 + (tail_lds ? tail_bytes : 0);
     const unsigned grid = (unsigned)((N + rpw - 1) / rpw);
-    if (x) hipLaunchKernelGGL((gemv_q4k_flat<true>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw);
-    else hipLaunchKernelGGL((gemv_q4k_flat<false>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw);
+    if (x) hipLaunchKernelGGL((gemv_q4k_flat<true>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw,
+                              tail_lds);
+    else hipLaunchKernelGGL((gemv_q4k_flat<false>), dim3(grid), dim3(64 * nw), shm, st, w, A, x, y, K, N, rpw,
+                            tail_lds);
     return hipGetLastError();
 }
 
