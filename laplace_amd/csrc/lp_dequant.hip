@@ -507,9 +507,8 @@ __device__ __forceinline__ void dense8(const uint8_t* __restrict__ p, float (&o)
     }
 }
 
-constexpr int kDenseU = 8;                  // slabs in flight per lane
-
-template <uint32_t T, int MR>
+// U slabs in flight per lane
+template <uint32_t T, int MR, int U>
 __global__ void __launch_bounds__(256)
 gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int K,
                   int N, int ldy) {
@@ -523,13 +522,13 @@ gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, fl
         float acc[MR];
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[m] = 0.0f;
-        for (int e0 = 8 * lane; e0 < K; e0 += kDenseU * 512) {
-            float wv[kDenseU][8];
+        for (int e0 = 8 * lane; e0 < K; e0 += U * 512) {
+            float wv[U][8];
 #pragma unroll
-            for (int u = 0; u < kDenseU; u++)
+            for (int u = 0; u < U; u++)
                 if (e0 + 512 * u < K) dense8<T>(wr + (size_t)(e0 + 512 * u) * EB, wv[u]);
 #pragma unroll
-            for (int u = 0; u < kDenseU; u++) {
+            for (int u = 0; u < U; u++) {
                 const int e = e0 + 512 * u;
                 if (e < K) {
 #pragma unroll
@@ -598,17 +597,25 @@ static hipError_t launch_fact_t(const uint8_t* w, const float* x, float* y, int 
             const long waves = N < cap ? N : cap;
             const unsigned gx = (unsigned)((waves + 3) / 4);
             const int full = M / 4, rest = M % 4;
-            if (full)
-                hipLaunchKernelGGL((gemv_dense_kernel<T, 4>), dim3(gx, full), dim3(256), 0, st, w, x, y, K, N, N);
+            // eight slabs per lane while the rows fit 16 waves per CU; four
+            // (fewer registers, all 32 waves per CU resident) beyond (BF16,
+            // K 4096: 4096 rows 10.5 / 10.75 us with 8 / 4, 14336 rows 34.3 /
+            // 28.0; 16 slabs 15.4 / 35.1)
+            const bool u8 = N <= (long)device_cu_count() * 16;
+#define LP_DN(MR, G, XM, YM)                                                                                  \
+    if (u8) hipLaunchKernelGGL((gemv_dense_kernel<T, MR, 8>), G, dim3(256), 0, st, w, XM, YM, K, N, N);       \
+    else hipLaunchKernelGGL((gemv_dense_kernel<T, MR, 4>), G, dim3(256), 0, st, w, XM, YM, K, N, N)
+            if (full) LP_DN(4, dim3(gx, full), x, y);
             if (rest) {
                 const float* xm = x + (size_t)full * 4 * K;
                 float* ym = y + (size_t)full * 4 * N;
                 switch (rest) {
-                    case 1: hipLaunchKernelGGL((gemv_dense_kernel<T, 1>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
-                    case 2: hipLaunchKernelGGL((gemv_dense_kernel<T, 2>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
-                    default: hipLaunchKernelGGL((gemv_dense_kernel<T, 3>), dim3(gx), dim3(256), 0, st, w, xm, ym, K, N, N); break;
+                    case 1: LP_DN(1, dim3(gx), xm, ym); break;
+                    case 2: LP_DN(2, dim3(gx), xm, ym); break;
+                    default: LP_DN(3, dim3(gx), xm, ym); break;
                 }
             }
+#undef LP_DN
             return hipGetLastError();
         }
     }
