@@ -114,6 +114,94 @@ __device__ __forceinline__ float dequant_one(uint32_t type, const uint8_t* __res
         default: return 0.0f;
     }
 }
+// Q4_K, eight consecutive outputs from i0 (8 | i0): one 32-element block,
+// so one scale pair and eight consecutive code bytes (an 8-byte load; w
+// 8-byte aligned), the arithmetic of dequant_one.
+__device__ __forceinline__ void dequant8_q4k(const uint8_t* __restrict__ w, long i0, float (&v)[8]) {
+    const uint8_t* b = w + (i0 >> 8) * 144;
+    const int e = (int)(i0 & 255), jb = e >> 6, hi = (e >> 5) & 1, l0 = e & 31;
+    int sc, m;
+    scale_min(2 * jb + hi, b + 4, sc, m);
+    const float d1 = h2f(rd16(b)) * (float)sc, m1 = h2f(rd16(b + 2)) * (float)m;
+    const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * jb + l0);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t q = ((k < 4 ? q8.x : q8.y) >> (8 * (k & 3))) & 0xffu;
+        v[k] = d1 * (float)(hi ? (q >> 4) : (q & 0xF)) - m1;
+    }
+}
+// Eight bytes at a 2-byte aligned address (four 16-bit loads).
+__device__ __forceinline__ uint2 ld8_h(const uint8_t* p) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+__device__ __forceinline__ uint32_t byte_of(uint2 u, int k) { return ((k < 4 ? u.x : u.y) >> (8 * (k & 3))) & 0xffu; }
+
+// Eight consecutive outputs from i0 (8 | i0) of the types whose eight
+// elements share their block header and sit in consecutive bytes, with
+// dequant_one's arithmetic; false: not one of them (the caller decodes
+// element by element). Alignment of w: 16 bytes for F32/F16/BF16, 8 for
+// Q4_K, 2 for Q4_0/Q8_0/Q6_K (dequant_wide_ok).
+template <uint32_t T>
+__device__ __forceinline__ bool dequant8_wide(const uint8_t* __restrict__ w, long i0, float (&v)[8]) {
+    if constexpr (T == T_F32) {
+        const float4 a = reinterpret_cast<const float4*>(w)[i0 / 4], c = reinterpret_cast<const float4*>(w)[i0 / 4 + 1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+        return true;
+    } else if constexpr (T == T_F16 || T == T_BF16) {
+        const u32x4 q = reinterpret_cast<const u32x4*>(w)[i0 / 8];
+        const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (T == T_F16) {
+                v[2 * k] = h2f(u[k] & 0xffffu);
+                v[2 * k + 1] = h2f(u[k] >> 16);
+            } else {
+                v[2 * k] = __uint_as_float((u[k] & 0xffffu) << 16);
+                v[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+            }
+        }
+        return true;
+    } else if constexpr (T == T_Q4_0) {
+        const uint8_t* b = w + (i0 >> 5) * 18;
+        const int l0 = (int)(i0 & 31);
+        const float d = h2f(rd16(b));
+        const uint2 q8 = ld8_h(b + 2 + (l0 & 15));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = byte_of(q8, k);
+            v[k] = d * (float)((int)(l0 < 16 ? (q & 0xF) : (q >> 4)) - 8);
+        }
+        return true;
+    } else if constexpr (T == T_Q8_0) {
+        const uint8_t* b = w + (i0 >> 5) * 34;
+        const float d = h2f(rd16(b));
+        const uint2 q8 = ld8_h(b + 2 + (i0 & 31));
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = d * (float)(int8_t)byte_of(q8, k);
+        return true;
+    } else if constexpr (T == T_Q4_K) {
+        dequant8_q4k(w, i0, v);
+        return true;
+    } else if constexpr (T == T_Q6_K) {
+        const uint8_t* b = w + (i0 >> 8) * 210;
+        const int e = (int)(i0 & 255), h = e >> 7, r = e & 127, g = r >> 5, l0 = r & 31;
+        const uint2 ql = ld8_h(b + 64 * h + l0 + ((g & 1) ? 32 : 0));
+        const uint2 qh = ld8_h(b + 128 + 32 * h + l0);
+        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + 8 * h);
+        const float a = h2f(rd16(b + 208)) * (float)sc[(l0 >> 4) + 2 * g];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t lb = byte_of(ql, k);
+            const int nib = (g & 2) ? (int)(lb >> 4) : (int)(lb & 0xF);
+            const int q = (nib | (int)(((byte_of(qh, k) >> (2 * g)) & 3u) << 4)) - 32;
+            v[k] = a * (float)q;
+        }
+        return true;
+    } else {
+        return false;
+    }
+}
 #pragma clang fp contract(on)
 
 __global__ void __launch_bounds__(256)
@@ -123,17 +211,30 @@ dequant_kernel(uint32_t type, const uint8_t* __restrict__ w, float* __restrict__
         dst[i] = dequant_one(type, w, i);
 }
 
+// w's alignment for dequant8_wide
+static bool dequant_wide_ok(uint32_t type, const uint8_t* w) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+    switch (type) {
+        case T_F32: case T_F16: case T_BF16: return a % 16 == 0;
+        case T_Q4_K: return a % 8 == 0;
+        case T_Q4_0: case T_Q8_0: case T_Q6_K: return a % 2 == 0;
+        default: return false;
+    }
+}
+
 // Eight consecutive outputs per thread (two 16-byte stores; the type is a
 // template constant, so the eight inlined decodes share their block-header
 // loads). n % 8 == 0 and dst 16-byte aligned.
-template <uint32_t T>
+template <uint32_t T, bool WIDE>
 __global__ void __launch_bounds__(256)
 dequant8_kernel(const uint8_t* __restrict__ w, float* __restrict__ dst, long n8) {
     const long stride = (long)gridDim.x * blockDim.x;
     for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j < n8; j += stride) {
         float v[8];
+        if (!(WIDE && dequant8_wide<T>(w, 8 * j, v))) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = dequant_one(T, w, 8 * j + k);
+            for (int k = 0; k < 8; k++) v[k] = dequant_one(T, w, 8 * j + k);
+        }
         float4* o = reinterpret_cast<float4*>(dst + 8 * j);
         o[0] = make_float4(v[0], v[1], v[2], v[3]);
         o[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -739,8 +840,13 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* w, float* dst, long n, h
         long g8 = (n8 + 255) / 256;
         if (g8 > 65536) g8 = 65536;
         const dim3 grid((unsigned)g8);
+        const bool wide = dequant_wide_ok(type, w);
         switch (type) {
-#define LP_D(TT) case TT: hipLaunchKernelGGL((dequant8_kernel<TT>), grid, dim3(256), 0, st, w, dst, n8); return hipGetLastError();
+#define LP_D(TT)                                                                                          \
+    case TT:                                                                                              \
+        if (wide) hipLaunchKernelGGL((dequant8_kernel<TT, true>), grid, dim3(256), 0, st, w, dst, n8);    \
+        else hipLaunchKernelGGL((dequant8_kernel<TT, false>), grid, dim3(256), 0, st, w, dst, n8);        \
+        return hipGetLastError();
             LP_D(T_F32) LP_D(T_F16) LP_D(T_BF16) LP_D(T_Q4_0) LP_D(T_Q5_0) LP_D(T_Q8_0) LP_D(T_Q2_K) LP_D(T_Q3_K)
             LP_D(T_Q4_K) LP_D(T_Q5_K) LP_D(T_Q6_K)
 #undef LP_D
