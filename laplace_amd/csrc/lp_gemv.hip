@@ -1000,20 +1000,24 @@ __device__ __forceinline__ float b32_span(const uint32_t* wd, uint32_t act_l, co
     }
 }
 
-template <uint32_t T, int L, bool FUSEQ>
+// RW: rows per wave (0: 64 / L, every lane busy; fewer leave lanes idle so
+// that a few rows spread over more waves and workgroups).
+template <uint32_t T, int L, bool FUSEQ, int RW = 0>
 __global__ void __launch_bounds__(1024)
 gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ x, float* __restrict__ y,
             int K, int N, int wbuf_bytes) {
     constexpr int SBB = 8 * B32Geom<T>::BPB;      // 144 (Q4_0) or 272 (Q8_0)
     constexpr int NV = SBB / 16;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr int RPW = 64 / L;
+    constexpr int RPW = RW > 0 ? RW : 64 / L;
+    static_assert(RPW * L <= 64, "rows per wave");
     const int lane = threadIdx.x & 63;
     const int nsb = K >> 8, nb = K >> 5;
     const long rb = (long)nsb * SBB;
     const long total = (long)N * rb;
     const int sl = lane & (L - 1);
-    const int rsub = lane / L;
+    const int rsub = lane / L < RPW ? lane / L : 0;   // idle lanes read row 0's bytes
+    const bool rowlane = lane / L < RPW;
     const bool active = sl < nsb;
     const int sb = active ? sl : nsb - 1;
     float* dl = reinterpret_cast<float*>(smem + nsb * 272);
@@ -1024,7 +1028,7 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
 
     // the wave's row group: RPW rows of nsb blocks-of-8 (contiguous bytes),
     // fully coalesced 16-byte loads (lane l: bytes 16 l of each KiB)
-    constexpr int NLD = (64 * SBB + 1023) / 1024;          // KiB per group when nsb == L
+    constexpr int NLD = (RPW * L * SBB + 1023) / 1024;     // KiB per group when nsb == L
     // KiB requested together: a Q4_0 group at once (9), a Q8_0 group (17)
     // in chunks of 6, which keep the 69-dword span of the compute unspilled
     constexpr int CH = NLD <= 9 ? NLD : 6;
@@ -1099,7 +1103,7 @@ gemv_b32_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         t = active ? t : 0.0f;
         const long row = g * RPW + rsub;
         const float sum = group_sum(t, L);
-        if (sl == L - 1 && row < N) y[row] = sum;
+        if (sl == L - 1 && row < N && rowlane) y[row] = sum;
     }
 }
 
@@ -1725,27 +1729,51 @@ static hipError_t launch_q4k_sbm(const SbmArgs& args, int ngroups, hipStream_t s
     return hipGetLastError();
 }
 
+constexpr bool kB32OneRow = true;
+
 template <uint32_t T>
 static hipError_t launch_b32_sb(const uint8_t* w, const ActView& A, const float* x, float* y, int K, int N,
                                 hipStream_t st) {
     constexpr int SBB = 8 * B32Geom<T>::BPB;
     const int L = sb_lanes(K);
     if (L == 0) return hipErrorInvalidValue;
-    const int rpw = 64 / L;
     const int nsb = K / 256;
-    const int wbuf = ((rpw * nsb * SBB + 1023) / 1024) * 1024;
     const size_t act_lds = ((size_t)nsb * 272 + 8 * (size_t)(K / 32) + 15) & ~size_t(15);
-    int wg = x ? 16 : 8;
-    while (wg > 1 && act_lds + (size_t)wg * wbuf > 160 * 1024) wg >>= 1;
-    const long groups = ((long)N + rpw - 1) / rpw;
-    long waves = groups;
     const long cap = (long)device_cu_count() * 16;
-    if (waves > cap) waves = cap;
-    const unsigned grid = (unsigned)((waves + wg - 1) / wg);
+    // rows per wave: 64 / L (every lane busy), or one row per wave where the
+    // full row groups need workgroups of fewer than 16 waves (no early
+    // weight requests) that leave CUs without one, and one row per wave
+    // covers every row in one round. Measured (us): Q8_0 4096x4096 7.3 ->
+    // 6.1, 2048x2048 5.95 -> 4.7, 1024x4096 6.5 -> 5.3; not where 16-wave
+    // workgroups fit (Q4_0 4096x4096 6.12 -> 6.3) or the rows need more
+    // than one per wave (Q4_0 14336x4096 8.0 -> 14.7)
+    auto geom = [&](int rpw, int& wbuf, int& wg, unsigned& grid) {
+        wbuf = ((rpw * nsb * SBB + 1023) / 1024) * 1024;
+        wg = x ? 16 : 8;
+        while (wg > 1 && act_lds + (size_t)wg * wbuf > 160 * 1024) wg >>= 1;
+        long waves = ((long)N + rpw - 1) / rpw;
+        if (waves > cap) waves = cap;
+        grid = (unsigned)((waves + wg - 1) / wg);
+    };
+    int rpw = 64 / L, wbuf, wg;
+    unsigned grid;
+    geom(rpw, wbuf, wg, grid);
+    if (kB32OneRow && x && rpw > 1 && wg < 16 && (long)grid < device_cu_count() && (long)N <= cap) {
+        int wbuf1, wg1;
+        unsigned grid1;
+        geom(1, wbuf1, wg1, grid1);
+        if (grid1 > grid && wg1 == 16) {
+            rpw = 1;
+            wbuf = wbuf1;
+            wg = wg1;
+            grid = grid1;
+        }
+    }
     const size_t shm = act_lds + (size_t)wg * wbuf;
 #define LP_S(LL)                                                                                             \
     case LL:                                                                                                 \
-        if (x) hipLaunchKernelGGL((gemv_b32_sb<T, LL, true>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
+        if (x && rpw == 1) hipLaunchKernelGGL((gemv_b32_sb<T, LL, true, 1>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
+        else if (x) hipLaunchKernelGGL((gemv_b32_sb<T, LL, true>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
         else hipLaunchKernelGGL((gemv_b32_sb<T, LL, false>), dim3(grid), dim3(64 * wg), shm, st, w, A, x, y, K, N, wbuf); \
         break;
     switch (L) {
