@@ -141,7 +141,7 @@ __device__ __forceinline__ uint32_t byte_of(uint2 u, int k) { return ((k < 4 ? u
 // elements share their block header and sit in consecutive bytes, with
 // dequant_one's arithmetic; false: not one of them (the caller decodes
 // element by element). Alignment of w: 16 bytes for F32/F16/BF16, 8 for
-// Q4_K, 2 for Q4_0/Q8_0/Q6_K (dequant_wide_ok).
+// Q4_K/Q5_K, 2 for Q4_0/Q5_0/Q8_0/Q6_K (dequant_wide_ok).
 template <uint32_t T>
 __device__ __forceinline__ bool dequant8_wide(const uint8_t* __restrict__ w, long i0, float (&v)[8]) {
     if constexpr (T == T_F32) {
@@ -183,6 +183,36 @@ __device__ __forceinline__ bool dequant8_wide(const uint8_t* __restrict__ w, lon
     } else if constexpr (T == T_Q4_K) {
         dequant8_q4k(w, i0, v);
         return true;
+    } else if constexpr (T == T_Q5_0) {
+        const uint8_t* b = w + (i0 >> 5) * 22;
+        const int l0 = (int)(i0 & 31);
+        const uint16_t* hp = reinterpret_cast<const uint16_t*>(b + 2);
+        const uint32_t qh = (uint32_t)hp[0] | ((uint32_t)hp[1] << 16);
+        const float d = h2f(rd16(b));
+        const uint2 q8 = ld8_h(b + 6 + (l0 & 15));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = byte_of(q8, k);
+            const int l = l0 + k;
+            const int v5 = (int)(l0 < 16 ? (q & 0xF) : (q >> 4)) | (int)(((qh >> l) & 1u) << 4);
+            v[k] = d * (float)(v5 - 16);
+        }
+        return true;
+    } else if constexpr (T == T_Q5_K) {
+        const uint8_t* b = w + (i0 >> 8) * 176;
+        const int e = (int)(i0 & 255), jb = e >> 6, hi = (e >> 5) & 1, l0 = e & 31;
+        int sc, m;
+        scale_min(2 * jb + hi, b + 4, sc, m);
+        const float d1 = h2f(rd16(b)) * (float)sc, m1 = h2f(rd16(b + 2)) * (float)m;
+        const uint2 q8 = *reinterpret_cast<const uint2*>(b + 48 + 32 * jb + l0);
+        const uint2 h8 = *reinterpret_cast<const uint2*>(b + 16 + l0);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = byte_of(q8, k);
+            const int v5 = (int)(hi ? (q >> 4) : (q & 0xF)) + 16 * (int)((byte_of(h8, k) >> (2 * jb + hi)) & 1u);
+            v[k] = d1 * (float)v5 - m1;
+        }
+        return true;
     } else if constexpr (T == T_Q6_K) {
         const uint8_t* b = w + (i0 >> 8) * 210;
         const int e = (int)(i0 & 255), h = e >> 7, r = e & 127, g = r >> 5, l0 = r & 31;
@@ -216,8 +246,8 @@ static bool dequant_wide_ok(uint32_t type, const uint8_t* w) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     switch (type) {
         case T_F32: case T_F16: case T_BF16: return a % 16 == 0;
-        case T_Q4_K: return a % 8 == 0;
-        case T_Q4_0: case T_Q8_0: case T_Q6_K: return a % 2 == 0;
+        case T_Q4_K: case T_Q5_K: return a % 8 == 0;
+        case T_Q4_0: case T_Q5_0: case T_Q8_0: case T_Q6_K: return a % 2 == 0;
         default: return false;
     }
 }
