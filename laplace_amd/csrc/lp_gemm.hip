@@ -744,7 +744,8 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P, float* __restr
 
 constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
-constexpr int kMfMoeRows = 128;    // grouped MoE: weight rows per workgroup (at least two sets)
+constexpr int kMfMoeWaves = 2;      // grouped MoE: waves per workgroup
+constexpr int kMfMoeRows = 64;    // grouped MoE: weight rows per workgroup (at least two sets)
 constexpr int kMfMaxM = 16;
 // Measured on MI355X (Q4_K 18944 x 3584): the GEMV tile kernel is faster
 // up to M = 4, the small-M MFMA kernels from M = 5 to 16.
@@ -1434,17 +1435,21 @@ hipError_t launch_moe_i8mf(const uint8_t* w, const ActView& A, const void* route
                            int topk, float* y, int K, int N, hipStream_t st) {
     if ((size_t)(K / 32) * 16 * 8 > 64 * 1024) return hipErrorInvalidValue;
     const long rb = (long)row_bytes(T_Q4_K, K);
-    // row sets of rw rows, ri of them per workgroup: 128 rows (K 2048: 4 sets
-    // of 32), two sets when a set has 128 (K 768: two K-slices, 4 row groups).
-    // Measured at 128 experts, top-8, 256 / 512 tokens (us per layer): one
-    // 32-row set and 8 K-slices for every K 358 / 591, 4 sets 313 / 496,
-    // with the row split at short K 291 / 451, two sets at K 768 281 / 451;
-    // 512 rows per workgroup 382 / 455 (too few workgroups)
-    const int rw = 16 * kMfTiles * (kMfWaves / mf_kslices(K / 256, kMfWaves));
+    // two waves (two K-slices) per workgroup, row sets of rw rows, ri of them
+    // per workgroup: kMfMoeRows rows, at least two sets. Measured at 128
+    // experts, top-8, 160 / 256 / 512 tokens (us per layer): 8 waves with one
+    // 32-row set and 8 K-slices for every K - / 358 / 591, 4 sets 313 / 496
+    // (256 / 512), with fewer K-slices at short K 291 / 451, two sets at K 768
+    // 219 / 281 / 444; 512 rows per workgroup 382 / 455 (too few
+    // workgroups); then 4 waves 194-198 / 254-258 / 408-410, 2 waves with 64
+    // rows 195-198 / 253 / 394-398 (32 rows: the same; 128: 271-273 at 256
+    // tokens), 1 wave 193-197 / 274-277 / 404-407, 16 waves 287 / 472
+    constexpr int NWM = kMfMoeWaves;
+    const int rw = 16 * kMfTiles * (NWM / mf_kslices(K / 256, NWM));
     const int ri = rw < kMfMoeRows ? kMfMoeRows / rw : 2;
     const int rows = rw * ri;
-    hipLaunchKernelGGL((gemv_q4k_i8mf<true, kMfTiles, kMfWaves, true>), dim3((N + rows - 1) / rows, max_groups),
-                       dim3(64 * kMfWaves), (size_t)(K / 32) * 16 * 8, st, w, rb, A, y, 0, K, N,
+    hipLaunchKernelGGL((gemv_q4k_i8mf<true, kMfTiles, NWM, true>), dim3((N + rows - 1) / rows, max_groups),
+                       dim3(64 * NWM), (size_t)(K / 32) * 16 * 8, st, w, rb, A, y, 0, K, N,
                        static_cast<const uint8_t*>(route), max_groups, multi, topk, rb * N, ri);
     return hipGetLastError();
 }
