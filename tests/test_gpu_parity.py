@@ -390,10 +390,12 @@ def test_q4k_small_m_mfma(orc, K, N, M):
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0, Q6_K], ids=["Q8_0", "Q4_0", "Q6_K"])
-@pytest.mark.parametrize("K,N", [(256, 7), (768, 100), (3584, 257), (14336, 33), (18944, 40), (32768, 9)])
+@pytest.mark.parametrize("K,N", [(256, 7), (768, 100), (3584, 257), (4096, 1001), (2048, 4095), (14336, 33),
+                                 (18944, 40), (32768, 9)])
 def test_m1_gemv_shapes(orc, t, K, N):
     """M=1 GEMV for Q8_0 / Q4_0 / Q6_K over a range of K (rows that are not
-    16-byte multiples for Q6_K, K up to the 32768 limit), ragged N: the
+    16-byte multiples for Q6_K, K up to the 32768 limit), ragged N (Q8_0 at
+    K 2048-4096 with few rows runs one row per wave, idle lanes past it): the
     single-call path (lp_gemm_dev) against the oracle and bit-identical to
     the quantizer-fed path (lp_gemm_q_dev)."""
     import torch
