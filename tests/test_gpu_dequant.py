@@ -75,3 +75,24 @@ def test_dequant_host_api_and_errors(orc):
     assert L().lp_dequantize(w.ctypes.data, t, out.ctypes.data, 100) == _lib.LP_EINVAL
     assert L().lp_dequantize(w.ctypes.data, t, out.ctypes.data, 0) == _lib.LP_OK
     L().lp_release_weights()
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("shift", [1, 2, 4, 8])
+def test_dequant_unaligned_weights(orc, name, shift):
+    """Weights at an offset from the allocation (1, 2, 4 or 8 bytes): the
+    types whose eight-output path needs an aligned pointer (16 bytes for
+    F32/F16/BF16, 8 for Q4_K/Q5_K, 2 for Q4_0/Q5_0/Q8_0/Q6_K) fall back to
+    the per-element decode; every output bit-exact."""
+    torch = torch_dev()
+    t, epb, bpb = TYPES[name]
+    nblk = 2048 // epb if epb > 1 else 2048
+    rng = np.random.default_rng(7 * t + shift)
+    w = rng.integers(0, 256, nblk * bpb, dtype=np.uint8)
+    n = nblk * epb
+    buf = torch.zeros(len(w) + 16, dtype=torch.uint8, device="cuda")
+    buf[shift:shift + len(w)] = torch.from_numpy(w).to("cuda")
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    _lib.check(L().lp_dequantize_dev(buf.data_ptr() + shift, t, out.data_ptr(), n, stream()), "dequantize_dev")
+    torch.cuda.synchronize()
+    assert same(out.cpu().numpy(), orc.dequantize(t, w, n))
