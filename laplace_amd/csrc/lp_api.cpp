@@ -196,8 +196,8 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
     // no GEMM kernel for the type: chunks of rows through the widest small-M
     // path (Q8_0: several 16-token tiles per workgroup; 16 rows on int8 MFMA
     // where the type has it, else 8 on the GEMV)
-    if (M > 16 && b32_chunk_supported(type, K, N, w)) {
-        const int ch = b32_chunk_rows();
+    if (M > 16 && i8_chunk_supported(type, K, N, w)) {
+        const int ch = i8_chunk_rows();
         for (int m0 = 0; m0 < M; m0 += ch) {
             const int mt = M - m0 < ch ? M - m0 : ch;
             ActView sub = A;
@@ -205,7 +205,7 @@ static int gemm_q(const ActView& A, void* planes, const uint8_t* w, uint32_t typ
             sub.d = A.d + (size_t)m0 * (K / 32);
             sub.sum = A.sum + (size_t)m0 * (K / 32);
             sub.s16 = A.s16 + (size_t)m0 * (K / 32);
-            LP_HIP(launch_b32_chunk(w, sub, y + (size_t)m0 * N, mt, K, N, st));
+            LP_HIP(launch_i8_chunk(type, w, sub, y + (size_t)m0 * N, mt, K, N, st));
         }
         return LP_OK;
     }
@@ -229,7 +229,7 @@ static const char* gemm_q_route(uint32_t type, int M, int K, int N, const uint8_
     if (i8mf_supported(type, M, K, N, w))
         return rq_preferred(type, M, K, N, w) ? "rq" : q6rq_preferred(type, M, K, N, w) ? "q6rq" : "i8mf";
     if (use_gemm(type, M, K, N, w)) return "gemm";
-    if (M > 16 && b32_chunk_supported(type, K, N, w)) return "i8mf";
+    if (M > 16 && i8_chunk_supported(type, K, N, w)) return "i8mf";
     const int chunk = i8mf_supported(type, 16, K, N, w) ? 16 : 8;
     const int mt = M < chunk ? M : chunk;
     if (i8mf_supported(type, mt, K, N, w))

@@ -744,7 +744,8 @@ quant_planes_kernel(const float* __restrict__ x, int K, Planes P, float* __restr
 
 constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
-constexpr int kB32ChunkTt = 2;      // Q8_0 prefill chunks: 16-token tiles per workgroup
+constexpr int kI8ChunkTt = 2;      // Q8_0 / Q6_K prefill chunks: 16-token tiles per workgroup
+constexpr bool kQ6Chunk = true;
 constexpr int kMfMoeWaves = 2;      // grouped MoE: waves per workgroup
 constexpr int kMfMoeRows = 64;    // grouped MoE: weight rows per workgroup (at least two sets)
 constexpr int kMfMaxM = 16;
@@ -1041,21 +1042,28 @@ __device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
     return make_uint2((d0 >> 16) | (d1 << 16), (d1 >> 16) | (t << 16));
 }
 
-template <int TL, int NWV>
+template <int TL, int NWV, int TT = 1>
 __global__ void __launch_bounds__(64 * NWV)
 gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N) {
-    __shared__ f4v red[NWV][TL][64];
-    extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][16] xd
+    static_assert(TL * TT <= NWV, "one wave per output tile in the final sum");
+    constexpr int TK = 16 * TT;                  // tokens per workgroup (TT 16-token tiles)
+    __shared__ f4v red[NWV][TL * TT][64];
+    extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][TK] xd
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int tok = lane & 15, g = lane >> 4;
     const int nsb = K >> 8, nb = K >> 5;
-    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
-        const int b = i >> 4, t = i & 15;
+    for (int i = threadIdx.x; i < nb * TK; i += blockDim.x) {
+        const int b = i / TK, t = i % TK;
         sdx[i] = t < M ? A.d[(size_t)t * nb + b] : 0.0f;
     }
     __syncthreads();
-    const bool tv = tok < M;
-    const int8_t* aq = A.qs + (size_t)(tv ? tok : 0) * K + 8 * g;
+    bool tv[TT];
+    const int8_t* aq[TT];
+#pragma unroll
+    for (int u = 0; u < TT; u++) {
+        tv[u] = tok + 16 * u < M;
+        aq[u] = A.qs + (size_t)(tv[u] ? tok + 16 * u : 0) * K + 8 * g;
+    }
     const int row0 = blockIdx.x * (16 * TL) + (lane & 15);
     const int sb0 = wv * nsb / NWV, sb1 = (wv + 1) * nsb / NWV;
     const uint8_t* wr[TL];
@@ -1068,9 +1076,11 @@ gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
     const bool first_half = g < 2;                 // k 0..15 of the block
     const i4v zi = {0, 0, 0, 0};
     const f4v z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    f4v acc[TL];
+    f4v acc[TL][TT];
 #pragma unroll
-    for (int t = 0; t < TL; t++) acc[t] = z4;
+    for (int t = 0; t < TL; t++)
+#pragma unroll
+        for (int u = 0; u < TT; u++) acc[t][u] = z4;
     for (int s = sb0; s < sb1; s++) {
         uint2 ql[TL][4], qh[TL][2];
         uint32_t scw[TL][4];
@@ -1086,13 +1096,15 @@ gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
             scw[t][0] = s0.x; scw[t][1] = s0.y; scw[t][2] = s1.x; scw[t][3] = s1.y;
             d[t] = fp16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
         }
-        long av[8];
+        long av[TT][8];
 #pragma unroll
-        for (int b = 0; b < 8; b++) av[b] = tv ? *reinterpret_cast<const long*>(aq + 32 * (8 * s + b)) : 0L;
+        for (int u = 0; u < TT; u++)
+#pragma unroll
+            for (int b = 0; b < 8; b++)
+                av[u][b] = tv[u] ? *reinterpret_cast<const long*>(aq[u] + 32 * (8 * s + b)) : 0L;
 #pragma unroll
         for (int b = 0; b < 8; b++) {
             const int h = b >> 2, g6 = b & 3;
-            const f4v xd = *reinterpret_cast<const f4v*>(sdx + (size_t)(8 * s + b) * 16 + 4 * g);
 #pragma unroll
             for (int t = 0; t < TL; t++) {
                 const uint2 l = ql[t][2 * h + (g6 & 1)], hh = qh[t][h];
@@ -1104,33 +1116,40 @@ gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
                 c1 = ((c1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
                 const long bw = (long)((unsigned long)c0 | ((unsigned long)c1 << 32));
                 const long b0 = first_half ? bw : 0L, b1 = first_half ? 0L : bw;
-                const i4v S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[b], b0, zi, 0, 0, 0);
-                const i4v S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[b], b1, zi, 0, 0, 0);
                 const int si = 8 * h + 2 * g6;          // scales of the block's two halves
                 const float sc0 = (float)(int8_t)(scw[t][si >> 2] >> (8 * (si & 3)));
                 const float sc1 = (float)(int8_t)(scw[t][(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float dx = d[t] * xd[r];
-                    acc[t][r] = fmaf(dx * sc0, (float)S0[r], acc[t][r]);
-                    acc[t][r] = fmaf(dx * sc1, (float)S1[r], acc[t][r]);
+                for (int u = 0; u < TT; u++) {
+                    const f4v xd = *reinterpret_cast<const f4v*>(sdx + (size_t)(8 * s + b) * TK + 16 * u + 4 * g);
+                    const i4v S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][b], b0, zi, 0, 0, 0);
+                    const i4v S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][b], b1, zi, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float dx = d[t] * xd[r];
+                        acc[t][u][r] = fmaf(dx * sc0, (float)S0[r], acc[t][u][r]);
+                        acc[t][u][r] = fmaf(dx * sc1, (float)S1[r], acc[t][u][r]);
+                    }
                 }
             }
         }
     }
 #pragma unroll
-    for (int t = 0; t < TL; t++) red[wv][t][lane] = acc[t];
-    __syncthreads();
-    if (wv < TL) {
-        const int t = wv;
-        f4v sum = red[0][t][lane];
+    for (int t = 0; t < TL; t++)
 #pragma unroll
-        for (int i = 1; i < NWV; i++) sum += red[i][t][lane];
+        for (int u = 0; u < TT; u++) red[wv][t * TT + u][lane] = acc[t][u];
+    __syncthreads();
+    // wave i sums output tile i (row tile i / TT, token tile i % TT)
+    if (wv < TL * TT) {
+        const int t = wv / TT, u = wv % TT;
+        f4v sum = red[0][wv][lane];
+#pragma unroll
+        for (int i = 1; i < NWV; i++) sum += red[i][wv][lane];
         const int row = row0 + 16 * t;
         if (row < N) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int tt = 4 * g + r;
+                const int tt = 16 * u + 4 * g + r;
                 if (tt < M) y[(size_t)tt * N + row] = sum[r];
             }
         }
@@ -1251,27 +1270,32 @@ bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
     return false;
 }
 
-// Q8_0 prefill rows in chunks of kB32ChunkTt * 16 tokens (one weight pass
-// per chunk), where the 32-row workgroups fill 1.5 rounds of CUs:
-// 1 <= M <= 16 * kB32ChunkTt. Measured against 16-row chunks (us per call):
+// Q8_0 and Q6_K prefill rows in chunks of kI8ChunkTt * 16 tokens (one
+// weight pass per chunk), where the 32-row workgroups fill 1.5 rounds of CUs:
+// 1 <= M <= 16 * kI8ChunkTt. Measured against 16-row chunks (us per call):
 // 14336x4096 M = 32 / 64 / 256 113 / 223 / 884 -> 67 / 132 / 522; with
 // 16-row workgroups of 16 waves (fewer rows) slower: 4096x4096 M=128 141 ->
 // 151, 4096x14336 M=64 223 -> 249; four token tiles slower everywhere
 // (14336x4096 M=256 948)
-bool b32_chunk_supported(uint32_t type, int K, int N, const uint8_t* w) {
-    return type == T_Q8_0 && K % 256 == 0 && (size_t)(K / 32) * 16 * kB32ChunkTt * 4 <= 64 * 1024 &&
-           reinterpret_cast<uintptr_t>(w) % 2 == 0 && 2 * ((N + 31) / 32) >= 3 * device_cu_count();
+bool i8_chunk_supported(uint32_t type, int K, int N, const uint8_t* w) {
+    return (type == T_Q8_0 || (type == T_Q6_K && kQ6Chunk)) && K % 256 == 0 &&
+           (size_t)(K / 32) * 16 * kI8ChunkTt * 4 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 2 == 0 &&
+           2 * ((N + 31) / 32) >= 3 * device_cu_count();
 }
-int b32_chunk_rows() { return 16 * kB32ChunkTt; }
+int i8_chunk_rows() { return 16 * kI8ChunkTt; }
 
-hipError_t launch_b32_chunk(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st) {
+hipError_t launch_i8_chunk(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
+                            hipStream_t st) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (M > 16 * kB32ChunkTt || !b32_chunk_supported(T_Q8_0, K, N, w)) return hipErrorInvalidValue;
-    constexpr int TT = kB32ChunkTt;
+    if (M > 16 * kI8ChunkTt || !i8_chunk_supported(type, K, N, w)) return hipErrorInvalidValue;
+    constexpr int TT = kI8ChunkTt;
     const size_t shm = (size_t)(K / 32) * 16 * TT * 4;
-    const long rbq = (long)row_bytes(T_Q8_0, K);
-    hipLaunchKernelGGL((gemv_b32_i8mf<T_Q8_0, 2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y, M,
-                       K, N);
+    const long rbq = (long)row_bytes(type, K);
+    if (type == T_Q6_K)
+        hipLaunchKernelGGL((gemv_q6k_i8mf<2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y, M, K, N);
+    else
+        hipLaunchKernelGGL((gemv_b32_i8mf<T_Q8_0, 2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y,
+                           M, K, N);
     return hipGetLastError();
 }
 

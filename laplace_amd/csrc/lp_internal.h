@@ -94,11 +94,12 @@ bool gemm_supported(uint32_t type, int M, int K);
 // Q4_K and Q6_K for 5 <= M <= 16 (Q4_K from M = 3 when N < 32 x CUs and K >= 14336),
 // Q8_0 for 9 <= M <= 16.
 bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w);
-// Q8_0 rows beyond 16 in chunks of b32_chunk_rows() on the int8 MFMA kernel
-// with several token tiles per workgroup (lp_gemm.hip).
-bool b32_chunk_supported(uint32_t type, int K, int N, const uint8_t* w);
-int b32_chunk_rows();
-hipError_t launch_b32_chunk(const uint8_t* w, const ActView& A, float* y, int M, int K, int N, hipStream_t st);
+// Q8_0 / Q6_K rows beyond 16 in chunks of i8_chunk_rows() on the int8 MFMA
+// kernels with several token tiles per workgroup (lp_gemm.hip).
+bool i8_chunk_supported(uint32_t type, int K, int N, const uint8_t* w);
+int i8_chunk_rows();
+hipError_t launch_i8_chunk(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
+                            hipStream_t st);
 hipError_t launch_gemv_i8mf(uint32_t type, const uint8_t* w, const ActView& A, float* y, int M, int K, int N,
                             hipStream_t st);
 // Q4_K for 1 <= M <= 8 on 4x4 int8 MFMA blocks, a row quad per wave

@@ -442,25 +442,25 @@ def test_prefill_rows_other_types(orc, t, M):
     assert normwise(y, orc.gemm_int(t, x, w, N)) <= TOL
 
 
+@pytest.mark.parametrize("t", [Q8_0, Q6_K], ids=["Q8_0", "Q6_K"])
 @pytest.mark.parametrize("M", [17, 40, 70])
-def test_q8_0_prefill_chunks(orc, M):
-    """Q8_0 rows beyond 16 run in chunks of 32 on the int8 MFMA kernel with
-    two token tiles per workgroup (one weight pass per chunk): sampled
-    outputs against the oracle, and the first 16 rows bit-identical to a
-    16-row call (same per-output arithmetic)."""
-    import torch
-    from hip_util import L, stream, to_dev, workspace  # noqa: F401
+def test_i8_prefill_chunks(orc, t, M):
+    """Q8_0 and Q6_K rows beyond 16 run in chunks of 32 on the int8 MFMA
+    kernels with two token tiles per workgroup (one weight pass per chunk):
+    sampled outputs against the oracle, and the first 16 rows bit-identical
+    to a 16-row call (same per-output arithmetic)."""
+    from hip_util import L, to_dev
     K, N = 1024, 12288
-    w = synth_weights(Q8_0, K, N, seed=500 + M)
-    assert L().lp_gemm_route(Q8_0, M, K, N, to_dev(w).data_ptr()).decode() == "i8mf"
+    w = synth_weights(t, K, N, seed=500 + M + t)
+    assert L().lp_gemm_route(t, M, K, N, to_dev(w).data_ptr()).decode() == "i8mf"
     x = synth_x(M, K, seed=501, outliers=0.01)
-    y = gemm_dev(Q8_0, x, w, N)
+    y = gemm_dev(t, x, w, N)
     assert np.isfinite(y).all()
     rng = np.random.default_rng(M)
     rows = np.sort(rng.choice(N, 48, replace=False))
     rb = len(w) // N
     wsub = np.concatenate([w[r * rb:(r + 1) * rb] for r in rows])
-    ref = orc.gemm_int(Q8_0, x, wsub, len(rows))
+    ref = orc.gemm_int(t, x, wsub, len(rows))
     assert normwise(y[:, rows], ref) <= 1e-4
-    y16 = gemm_dev(Q8_0, x[:16], w, N)
+    y16 = gemm_dev(t, x[:16], w, N)
     assert np.array_equal(y[:16].view(np.uint32), y16.view(np.uint32))
