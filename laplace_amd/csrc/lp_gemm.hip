@@ -746,6 +746,7 @@ constexpr int kMfWaves = 8;
 constexpr int kMfTiles = 2;         // 16-row tiles per workgroup (every wave takes all of them)
 constexpr int kI8ChunkTt = 2;      // Q8_0 / Q6_K prefill chunks: 16-token tiles per workgroup
 constexpr bool kQ6Chunk = true;
+constexpr bool kQ40Chunk = true;
 constexpr int kMfMoeWaves = 2;      // grouped MoE: waves per workgroup
 constexpr int kMfMoeRows = 64;    // grouped MoE: weight rows per workgroup (at least two sets)
 constexpr int kMfMaxM = 16;
@@ -1165,9 +1166,9 @@ gemv_q6k_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
 template <uint32_t T, int TL, int NWV, int TT = 1>
 __global__ void __launch_bounds__(64 * NWV)
 gemv_b32_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restrict__ y, int M, int K, int N) {
-    static_assert(T == T_Q8_0, "Q8_0 only");
+    static_assert(T == T_Q8_0 || T == T_Q4_0, "Q8_0 / Q4_0");
     static_assert(TL * TT <= NWV, "one wave per output tile in the final sum");
-    constexpr int BPB = 34;
+    constexpr int BPB = T == T_Q8_0 ? 34 : 18;
     constexpr int TK = 16 * TT;
     __shared__ f4v red[NWV][TL * TT][64];
     extern __shared__ __attribute__((aligned(16))) float sdx[];   // [nb][TK] xd
@@ -1216,7 +1217,17 @@ gemv_b32_i8mf(const uint8_t* __restrict__ w, long rb, ActView A, float* __restri
             for (int t = 0; t < TL; t++) {
                 const uint8_t* blk = wr[t] + (size_t)kb * BPB;
                 const float d = fp16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
-                const uint2 c = ld8_a2(blk + 2 + 8 * g);
+                uint2 c;
+                if constexpr (T == T_Q8_0) {
+                    c = ld8_a2(blk + 2 + 8 * g);
+                } else {
+                    // elements 8g..8g+7: low nibbles of bytes 8g.. (g < 2), high
+                    // nibbles of bytes 8(g - 2).. ; code - 8 per byte (no borrow)
+                    const uint2 r = ld8_a2(blk + 2 + 8 * (g & 1));
+                    const int sh = g < 2 ? 0 : 4;
+                    c.x = ((((r.x >> sh) & 0x0f0f0f0fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                    c.y = ((((r.y >> sh) & 0x0f0f0f0fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                }
                 const long bw = (long)((unsigned long)c.x | ((unsigned long)c.y << 32));
 #pragma unroll
                 for (int u = 0; u < TT; u++) {
@@ -1278,7 +1289,7 @@ bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
 // 151, 4096x14336 M=64 223 -> 249; four token tiles slower everywhere
 // (14336x4096 M=256 948)
 bool i8_chunk_supported(uint32_t type, int K, int N, const uint8_t* w) {
-    return (type == T_Q8_0 || (type == T_Q6_K && kQ6Chunk)) && K % 256 == 0 &&
+    return (type == T_Q8_0 || (type == T_Q6_K && kQ6Chunk) || (type == T_Q4_0 && kQ40Chunk)) && K % 256 == 0 &&
            (size_t)(K / 32) * 16 * kI8ChunkTt * 4 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 2 == 0 &&
            2 * ((N + 31) / 32) >= 3 * device_cu_count();
 }
@@ -1293,6 +1304,9 @@ hipError_t launch_i8_chunk(uint32_t type, const uint8_t* w, const ActView& A, fl
     const long rbq = (long)row_bytes(type, K);
     if (type == T_Q6_K)
         hipLaunchKernelGGL((gemv_q6k_i8mf<2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y, M, K, N);
+    else if (type == T_Q4_0)
+        hipLaunchKernelGGL((gemv_b32_i8mf<T_Q4_0, 2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y,
+                           M, K, N);
     else
         hipLaunchKernelGGL((gemv_b32_i8mf<T_Q8_0, 2, 8, TT>), dim3((N + 31) / 32), dim3(512), shm, st, w, rbq, A, y,
                            M, K, N);
