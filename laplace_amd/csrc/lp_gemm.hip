@@ -1281,17 +1281,19 @@ bool i8mf_supported(uint32_t type, int M, int K, int N, const uint8_t* w) {
     return false;
 }
 
-// Q8_0 and Q6_K prefill rows in chunks of kI8ChunkTt * 16 tokens (one
-// weight pass per chunk), where the 32-row workgroups fill 1.5 rounds of CUs:
-// 1 <= M <= 16 * kI8ChunkTt. Measured against 16-row chunks (us per call):
-// 14336x4096 M = 32 / 64 / 256 113 / 223 / 884 -> 67 / 132 / 522; with
-// 16-row workgroups of 16 waves (fewer rows) slower: 4096x4096 M=128 141 ->
-// 151, 4096x14336 M=64 223 -> 249; four token tiles slower everywhere
-// (14336x4096 M=256 948)
+// Q8_0, Q4_0 and Q6_K prefill rows in chunks of kI8ChunkTt * 16 tokens
+// (one weight pass per chunk), 32-row workgroups of 8 waves; Q6_K only where
+// those fill 1.5 rounds of CUs: 1 <= M <= 16 * kI8ChunkTt. Measured (us per
+// call), Q8_0 against 16-row chunks: 14336x4096 M = 32 / 64 / 256 113 / 223
+// / 884 -> 67 / 132 / 522, 4096x4096 M=128 142 -> 134 (16-row workgroups of
+// 16 waves there: 151); Q4_0 against 8-row GEMV chunks: 14336x4096 M=64 262
+// -> 130, 4096x4096 M=128 193 -> 131, 1024x4096 M=64 72.5 -> 65; Q6_K
+// 14336x4096 M=64 156 -> 100, but 4096x4096 M=128 97.5 -> 111 (so not
+// there); four token tiles slower everywhere (Q8_0 14336x4096 M=256 948)
 bool i8_chunk_supported(uint32_t type, int K, int N, const uint8_t* w) {
     return (type == T_Q8_0 || (type == T_Q6_K && kQ6Chunk) || (type == T_Q4_0 && kQ40Chunk)) && K % 256 == 0 &&
            (size_t)(K / 32) * 16 * kI8ChunkTt * 4 <= 64 * 1024 && reinterpret_cast<uintptr_t>(w) % 2 == 0 &&
-           2 * ((N + 31) / 32) >= 3 * device_cu_count();
+           (2 * ((N + 31) / 32) >= 3 * device_cu_count() || type != T_Q6_K);
 }
 int i8_chunk_rows() { return 16 * kI8ChunkTt; }
 
