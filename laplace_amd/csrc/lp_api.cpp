@@ -462,7 +462,8 @@ static int moe_q(const float* x, int multi, const int* idx, const uint8_t* w, ui
     // groups of <= 16 pairs on the int8 MFMA kernel pay off when experts are
     // chosen by more than 8 pairs on average (prefill; at 128 experts, top-8:
     // 10 per expert 259 vs 274 us on the GEMV kernels, 8 per expert 246 vs
-    // 236 us); decode-sized batches stay on the GEMV kernels
+    // 236 us; 6 per expert 177 vs 137 us); decode-sized batches stay on the
+    // GEMV kernels
     const bool mf = moe_mf_supported(type, K) && P > 8 * E;
     const int gs = mf ? 16 : moe_group_size(type, K, P, E);
     if (kMoeFuseQuantRoute) {
