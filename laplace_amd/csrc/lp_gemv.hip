@@ -406,7 +406,10 @@ gemv_q4k_sb(const uint8_t* __restrict__ w, ActView A, const float* __restrict__ 
         // 14336 x 4096; a quarter or three quarters of the waves early, or all
         // of them, were slower: x's loads then queue behind the weights).
         // The quantizing half's x requests go out first, one barrier ahead of
-        // the weight requests (quantize_x_lds<6>: 8.46 -> 8.05 us).
+        // the weight requests (quantize_x_lds<6>: 8.46 -> 8.05 us). Every
+        // wave requesting its weights right behind x's requests, the
+        // quantizing waves waiting for x alone, measured slower (7.9 -> 9.8;
+        // Q4_0 4096x14336 10.4 -> 11.8): x still arrives behind the flood.
         const int nq = (int)blockDim.x >= 1024 ? (int)blockDim.x / 2 : (int)blockDim.x;
         const bool early = (int)threadIdx.x >= nq;
         if (nq < (int)blockDim.x && (K >> 2) <= 6 * nq) {
